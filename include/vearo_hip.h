@@ -1,0 +1,216 @@
+/*
+ * vearo_hip.h -- C ABI of libvearo_hip.so, the MI355X (gfx950) backend for
+ * vearo's fused layer kernels.
+ *
+ * This is the drop-in boundary: the entry points a `vearo-backend-hip` crate
+ * binds with `extern "C"` to fill vearo's BackendOps table
+ * (reference: crates/vearo-core/src/tensor.rs:1108-1175) and its storage hooks
+ * (tensor.rs:1321-1363). All arguments are plain pointers, sizes and flags:
+ *   - tensors are f32 device pointers (vh_alloc or any HIP device allocation);
+ *     hot-path entries take contiguous row-major buffers; strided inputs go
+ *     through vh_strided_copy first (the device replacement for the host
+ *     round-trip in Tensor::contiguous, tensor.rs:345-486);
+ *   - ids and targets are f32, as in the reference API (cpu lib.rs:892-899);
+ *   - `stream` is a hipStream_t passed as void*; NULL selects the runtime's own
+ *     stream (vh_stream()). Launches are asynchronous on that stream.
+ * Every entry returns 0 on success or a VH_ERR_* code; vh_last_error() gives a
+ * thread-local message. Nothing throws across the ABI. Zero-sized work returns
+ * 0 without launching (the reference returns empty outputs, cpu lib.rs:669-672).
+ *
+ * Data the CPU backend would panic on (negative / out-of-range token ids and
+ * targets, cpu lib.rs:893-905, 1015-1027) is caught on the device: the kernel
+ * records the first offending element and vh_sync() / vh_check_device_error()
+ * return VH_ERR_DEVICE_PANIC with the CPU backend's panic text.
+ *
+ * "cpu" below is crates/vearo-backend-cpu/src/lib.rs, "cuda" is
+ * crates/vearo-backend-cuda/src/lib.rs, "autograd" is crates/vearo-autograd/src/lib.rs.
+ */
+#ifndef VEARO_HIP_H
+#define VEARO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VH_OK 0
+#define VH_ERR_INVALID 1       /* bad argument: shape, size, null pointer      */
+#define VH_ERR_HIP 2           /* HIP runtime error                           */
+#define VH_ERR_NOT_INIT 3      /* vh_init has not run                         */
+#define VH_ERR_DEVICE_PANIC 4  /* a kernel met data the CPU backend panics on */
+#define VH_ERR_UNSUPPORTED 5   /* size outside the implemented range          */
+#define VH_ERR_OOM 6           /* device allocation failed                    */
+
+#define VH_MAX_RANK 8
+
+/* dims + element strides, as vearo-core's Shape pair (shape.rs:8-12, rank <= 8). */
+typedef struct {
+  int32_t rank;
+  int32_t pad_;
+  int64_t dims[VH_MAX_RANK];
+  int64_t strides[VH_MAX_RANK];
+} vh_layout;
+
+typedef struct {
+  size_t live_bytes;    /* handed out and not yet freed                  */
+  size_t cached_bytes;  /* held in the arena's free lists                */
+  size_t peak_bytes;    /* high-water mark of live_bytes                 */
+  size_t hip_bytes;     /* total obtained from hipMalloc                 */
+} vh_mem_stats;
+
+/* ------------------------------------------------------------- runtime -- */
+
+/* Device init: select the GPU, create the stream, load the embedded gfx950
+ * code object with hipModuleLoadData, zero the device error record.
+ * Replaces cuda init (load_ptx + CudaDevice::new, cuda:165-242). Idempotent. */
+int vh_init(int device);
+/* Release the stream, module and every cached allocation. */
+int vh_shutdown(void);
+/* Thread-local text of the last failure (empty string if none). */
+const char* vh_last_error(void);
+/* The runtime's stream as a hipStream_t. */
+void* vh_stream(void);
+/* Number of compute units of the current device. */
+int vh_device_cu_count(void);
+/* Wait for the stream, then check the device error record. Replaces the
+ * implicit sync of cuda's read hook (cuda:124-132). */
+int vh_sync(void);
+/* Check (and clear) the device error record; syncs the stream first. */
+int vh_check_device_error(void);
+
+/* -------------------------------------------------------------- memory -- */
+
+/* Arena allocation over hipMalloc (size classes, cached free lists, 256-byte
+ * alignment). zero != 0 fills with 0.0f on the stream, as the CUDA slot arena
+ * zero-fills on reuse (cuda:41-112) and Tensor::zeros_on relies on
+ * (tensor.rs:88-117). Replaces the alloc hook of register_cuda_hooks. */
+int vh_alloc(size_t bytes, int zero, void** out);
+/* Return a block to the arena (stream-ordered reuse). Replaces refcount_dec's
+ * slot release (cuda:134-163). */
+int vh_free(void* ptr);
+/* Synchronous copies, ordered after the stream's queued work. Replace the
+ * write (cuda:114-122) and read (cuda:124-132) hooks. */
+int vh_h2d(void* dst, const void* src, size_t bytes);
+int vh_d2h(void* dst, const void* src, size_t bytes);
+/* Asynchronous device-to-device copy on `stream`. */
+int vh_d2d(void* dst, const void* src, size_t bytes, void* stream);
+/* out[i] = value for i < n (a fill kernel, never hipMemset). */
+int vh_fill_f32(float* out, float value, int64_t n, void* stream);
+int vh_mem_stats_get(vh_mem_stats* out);
+/* hipFree every cached (free) block. */
+int vh_empty_cache(void);
+
+/* ---------------------------------------------------- hot path: layernorm -- */
+
+/* y = layernorm over the last dim C of x[rows, C] with weight w[C], bias b[C].
+ * Replaces BackendOps.layernorm (tensor.rs:1133; cpu:665-740; cuda:1205-1261). */
+int vh_layernorm_fwd(const float* x, const float* w, const float* b, float* y,
+                     int64_t rows, int64_t C, float eps, void* stream);
+/* dx[rows, C], dw[C], db[C] from x, w and upstream dy (bias enters only through
+ * its shape in the reference). Deterministic, atomic-free dw/db.
+ * Replaces BackendOps.layernorm_backward (tensor.rs:1135; cpu:742-858;
+ * cuda:1263-1353). scratch may be NULL (the runtime uses its arena); otherwise
+ * it must hold vh_layernorm_bwd_scratch_bytes(rows, C) bytes. */
+int vh_layernorm_bwd(const float* x, const float* w, const float* dy, float* dx,
+                     float* dw, float* db, int64_t rows, int64_t C, float eps,
+                     void* scratch, size_t scratch_bytes, void* stream);
+size_t vh_layernorm_bwd_scratch_bytes(int64_t rows, int64_t C);
+
+/* -------------------------------------------------------- hot path: gelu -- */
+
+/* y = gelu(x) elementwise, tanh form. Replaces BackendOps.gelu (tensor.rs:1129;
+ * cpu:456-497; cuda unary_op + gelu_forward, cuda:1108-1140). */
+int vh_gelu_fwd(const float* x, float* y, int64_t n, void* stream);
+/* y[r, c] = gelu(x[r, c] + bias[c]): the Linear bias add (nn lib.rs:120-128 ->
+ * BackendOps.add, cpu:160-202) fused with BackendOps.gelu. */
+int vh_gelu_bias_fwd(const float* x, const float* bias, float* y, int64_t rows,
+                     int64_t C, void* stream);
+/* dx = dy * gelu'(x): the autograd Gelu arm (autograd:542-546) -- host-side
+ * gelu_grad_mask (autograd:383-403) then BackendOps.mul -- as one kernel. */
+int vh_gelu_grad_mul(const float* x, const float* dy, float* dx, int64_t n,
+                     void* stream);
+/* dx = dy * gelu'(x + bias) and dbias = column sums of dx: the Gelu arm plus the
+ * Add arm's host reduce_to for the bias (autograd:460-469, 316-361), fused.
+ * scratch: NULL or vh_gelu_bias_bwd_scratch_bytes(rows, C) bytes. */
+int vh_gelu_bias_bwd(const float* x, const float* bias, const float* dy, float* dx,
+                     float* dbias, int64_t rows, int64_t C, void* scratch,
+                     size_t scratch_bytes, void* stream);
+size_t vh_gelu_bias_bwd_scratch_bytes(int64_t rows, int64_t C);
+
+/* ----------------------------------------------------- hot path: softmax -- */
+
+/* y = softmax over rows of length T of x[rows, T]. causal != 0 declares the
+ * rows to be T x T score blocks whose entries j > (row % T) are masked (-inf or
+ * a large negative additive mask): they are not read and y there is 0, which
+ * is the reference's exact result for such inputs. Replaces BackendOps.softmax
+ * (tensor.rs:1131; cpu:499-563; cuda:1142-1203) on the last dim. */
+int vh_softmax_fwd(const float* x, float* y, int64_t rows, int64_t T, int causal,
+                   void* stream);
+/* dx = y * (dy - sum(dy * y)) per row: the autograd Softmax arm
+ * (autograd:547-553: softmax, mul, sum, sub, mul) as one kernel. input_is_x != 0
+ * means `in` is the saved input x (y is recomputed in registers, as the arm
+ * does); otherwise `in` is y. */
+int vh_softmax_bwd(const float* in, const float* dy, float* dx, int64_t rows,
+                   int64_t T, int input_is_x, int causal, void* stream);
+
+/* --------------------------------------------------- hot path: embedding -- */
+
+/* out[i, :] = W[round(ids[i]), :] for i < n; W is [V, D]. Bit-exact copy.
+ * Replaces BackendOps.embedding (tensor.rs:1137; cpu:860-918; cuda:1355-1410). */
+int vh_embedding_fwd(const float* ids, const float* W, float* out, int64_t n,
+                     int64_t V, int64_t D, void* stream);
+/* dW[V, D] = dense scatter-add of dy[n, D] by token, written in full (rows no
+ * token hits are 0). Sort-by-token segmented sum, no float atomics, same f32
+ * order as the CPU loop. Replaces BackendOps.embedding_backward
+ * (tensor.rs:1139; cpu:920-980; cuda:1412-1464).
+ * scratch: NULL or vh_embedding_bwd_scratch_bytes(n, V) bytes. */
+int vh_embedding_bwd(const float* ids, const float* dy, float* dW, int64_t n,
+                     int64_t V, int64_t D, void* scratch, size_t scratch_bytes,
+                     void* stream);
+size_t vh_embedding_bwd_scratch_bytes(int64_t n, int64_t V);
+
+/* ----------------------------------------------- hot path: cross-entropy -- */
+
+/* loss[0] = mean over B rows of -log_softmax(logits[b])[target[b]];
+ * logits [B, V], targets [B] f32. Replaces BackendOps.cross_entropy
+ * (tensor.rs:1141; cpu:982-1051; cuda:1466-1534).
+ * scratch: NULL or vh_cross_entropy_fwd_scratch_bytes(B) bytes. */
+int vh_cross_entropy_fwd(const float* logits, const float* targets, float* loss,
+                         int64_t B, int64_t V, void* scratch, size_t scratch_bytes,
+                         void* stream);
+size_t vh_cross_entropy_fwd_scratch_bytes(int64_t B);
+/* dlogits[B, V] = go * (softmax(logits) - onehot(target)) / B, with go the
+ * device scalar grad_out[0]. Replaces BackendOps.cross_entropy_backward
+ * (tensor.rs:1143; cpu:1053-1127; cuda:1536-1592). */
+int vh_cross_entropy_bwd(const float* logits, const float* targets,
+                         const float* grad_out, float* dlogits, int64_t B, int64_t V,
+                         void* stream);
+
+/* ------------------------------------- composites the autograd arms drive -- */
+
+#define VH_OP_ADD 0
+#define VH_OP_SUB 1
+#define VH_OP_MUL 2
+#define VH_OP_DIV 3
+
+/* out = l (op) r with NumPy broadcasting over strided operands; out is
+ * contiguous with the broadcast shape. Replaces BackendOps.add/sub/mul/div
+ * (tensor.rs:1113-1119; cpu:160-238; cuda binary_op, cuda:832-899) -- the
+ * layouts travel as kernel arguments, not as a per-call H2D info array. */
+int vh_binary(int op, const float* l, const vh_layout* ll, const float* r,
+              const vh_layout* rl, float* out, void* stream);
+/* Sum (mean != 0: mean) of x over axis `dim`; out is contiguous with the
+ * reduced shape (keep_dim only changes the shape, not the data). Replaces
+ * BackendOps.sum / mean (tensor.rs:1125-1127; cpu:566-653; cuda:1012-1090). */
+int vh_reduce(int mean, const float* x, const vh_layout* xl, int dim, float* out,
+              void* stream);
+/* dst (contiguous) = src read through its layout. Device replacement for the
+ * host round-trip of Tensor::contiguous (tensor.rs:349-368). */
+int vh_strided_copy(const float* src, const vh_layout* sl, float* dst, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VEARO_HIP_H */

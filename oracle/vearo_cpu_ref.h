@@ -1,0 +1,113 @@
+/*
+ * vearo_cpu_ref.h -- CPU oracle: a C restatement of vearo-backend-cpu's hot-path
+ * functions, used ONLY as a test checker and as the timed CPU baseline.
+ *
+ * TEST INFRASTRUCTURE. Nothing in the product (libvearo_hip.so, the vearo_amd
+ * package) links, loads or calls this code. Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg may use it.
+ *
+ * Every function follows the loop order and f32 accumulation order of the Rust
+ * source it cites (paths relative to the reference checkout):
+ *   cpu:      crates/vearo-backend-cpu/src/lib.rs
+ *   autograd: crates/vearo-autograd/src/lib.rs
+ *   shape:    crates/vearo-core/src/shape.rs
+ * It is compiled with -ffp-contract=off and without fast-math, so a*b+c is two
+ * roundings exactly as in Rust (which never contracts), and it calls glibc
+ * expf/tanhf/logf/sqrtf, the libm Rust's f32::exp/tanh/ln/sqrt reach on linux-gnu.
+ *
+ * Layouts mirror vearo-core's Tensor: dims + element strides, no storage offset
+ * (views in vearo only permute/transpose strides, tensor.rs:537-620).
+ */
+#ifndef VEARO_CPU_REF_H
+#define VEARO_CPU_REF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VO_MAX_RANK 8
+
+typedef struct {
+  int32_t rank;
+  int64_t dims[VO_MAX_RANK];
+  int64_t strides[VO_MAX_RANK];
+} vo_layout;
+
+/* Return codes: 0 = ok, 1 = the reference would panic (message in err). */
+#define VO_OK 0
+#define VO_PANIC 1
+
+/* Binary broadcast ops (cpu:160-238). op: 0 add, 1 sub, 2 mul, 3 div.
+ * out_shape must be the broadcast of the two shapes; out is contiguous. */
+int vo_binary(int op, const float* lhs, const vo_layout* ll, const float* rhs,
+              const vo_layout* rl, float* out, const vo_layout* out_shape,
+              char* err, size_t errlen);
+
+/* gelu, tanh approximation (cpu:458-497). */
+void vo_gelu(const float* x, const vo_layout* xl, float* out);
+
+/* Softmax over `dim` (cpu:501-563). */
+int vo_softmax(const float* x, const vo_layout* xl, int dim, float* out,
+               char* err, size_t errlen);
+
+/* Single-axis sum / mean (cpu:566-653). out has the reduced shape. */
+int vo_sum(const float* x, const vo_layout* xl, int dim, int keep_dim, float* out,
+           char* err, size_t errlen);
+int vo_mean(const float* x, const vo_layout* xl, int dim, int keep_dim, float* out,
+            char* err, size_t errlen);
+
+/* LayerNorm forward / backward over the last dim (cpu:665-858). */
+int vo_layernorm(const float* x, const vo_layout* xl, const float* w,
+                 const vo_layout* wl, const float* b, const vo_layout* bl, float eps,
+                 float* out, char* err, size_t errlen);
+int vo_layernorm_backward(const float* x, const vo_layout* xl, const float* w,
+                          const vo_layout* wl, const vo_layout* bl, const float* go,
+                          const vo_layout* gol, float eps, float* gx, float* gw,
+                          float* gb, char* err, size_t errlen);
+
+/* Embedding forward / backward (cpu:860-980). ids are f32 (the API contract). */
+int vo_embedding(const float* ids, const vo_layout* il, const float* w,
+                 const vo_layout* wl, float* out, char* err, size_t errlen);
+int vo_embedding_backward(const float* ids, const vo_layout* il, const vo_layout* wl,
+                          const float* go, const vo_layout* gol, float* gw, char* err,
+                          size_t errlen);
+
+/* Cross-entropy forward (mean loss, one float) / backward (cpu:982-1127). */
+int vo_cross_entropy(const float* logits, const vo_layout* ll, const float* tgt,
+                     const vo_layout* tl, float* loss, char* err, size_t errlen);
+int vo_cross_entropy_backward(const float* logits, const vo_layout* ll,
+                              const float* tgt, const vo_layout* tl,
+                              const float* grad_out, int64_t grad_out_numel,
+                              float* gl, char* err, size_t errlen);
+
+/* Autograd helpers that run on the host in the reference. */
+void vo_gelu_grad_mask(const float* x_contig, int64_t n, float* mask); /* autograd:383-403 */
+int vo_reduce_to(const float* grad_contig, const vo_layout* gshape, const int64_t* target,
+                 int target_rank, float* out, char* err, size_t errlen); /* autograd:316-361 */
+
+/* Composite paths the unchanged autograd arms drive, restated end to end. */
+/* Softmax arm (autograd:547-553): y = softmax(x); s = sum(dy*y, dim, keep);
+ * dx = y * (dy - s). x and dy contiguous with the same shape. */
+int vo_softmax_backward_composite(const float* x, const float* dy, const vo_layout* xl,
+                                  int dim, float* dx, char* err, size_t errlen);
+/* Gelu arm (autograd:542-546) on a bias-add input: h = x + bias (cpu:160-202
+ * broadcast), y = gelu(h) forward; backward dh = dy * gelu_mask(h),
+ * dbias = reduce_to(dh, [C]). x, dy: [rows, C] contiguous. */
+void vo_gelu_bias_forward(const float* x, const float* bias, int64_t rows, int64_t C,
+                          float* y);
+void vo_gelu_bias_backward(const float* x, const float* bias, const float* dy,
+                           int64_t rows, int64_t C, float* dx, float* dbias);
+
+/* Shortest round-trip positional formatting of an f32, as Rust's `{}` prints it. */
+void vo_format_f32(float v, char* buf, size_t len);
+
+/* Layout helpers. */
+void vo_contiguous_layout(vo_layout* l, int rank, const int64_t* dims);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,122 @@
+"""CPU-side checks of the C ABI boundary: libvearo_hip.so loads, exports every
+function include/vearo_hip.h declares, refuses work before vh_init (no GPU
+call is made), and its embedded gfx950 code object holds every kernel name the
+host launcher can ask for."""
+import ctypes
+import os
+import re
+import struct
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "vearo_hip.h")
+LIB = os.path.join(ROOT, "vearo_amd", "lib", "libvearo_hip.so")
+CODE_OBJECT = os.path.join(ROOT, "vearo_amd", "csrc", "_build", "vearo_kernels.co")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_hot_path():
+    names = declared_functions()
+    for want in ["vh_layernorm_fwd", "vh_layernorm_bwd", "vh_softmax_fwd", "vh_softmax_bwd",
+                 "vh_gelu_fwd", "vh_gelu_bias_fwd", "vh_gelu_bias_bwd", "vh_gelu_grad_mul",
+                 "vh_embedding_fwd", "vh_embedding_bwd", "vh_cross_entropy_fwd",
+                 "vh_cross_entropy_bwd", "vh_binary", "vh_reduce", "vh_strided_copy",
+                 "vh_init", "vh_alloc", "vh_free", "vh_h2d", "vh_d2h", "vh_sync"]:
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(LIB)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_every_declared_symbol():
+    from vearo_amd import _abi
+
+    assert sorted(_abi.SIGNATURES) == declared_functions()
+
+
+def test_calls_before_init_fail_cleanly():
+    from vearo_amd import _abi
+
+    if _abi._initialised:
+        pytest.skip("runtime already initialised in this process")
+    p = ctypes.c_void_p()
+    assert _abi.lib.vh_alloc(16, 0, ctypes.byref(p)) == _abi.VH_ERR_NOT_INIT
+    assert "vh_init" in _abi.last_error()
+    assert _abi.lib.vh_layernorm_fwd(None, None, None, None, 1, 1, 1e-5, None) == _abi.VH_ERR_NOT_INIT
+    assert _abi.lib.vh_sync() == _abi.VH_ERR_NOT_INIT
+
+
+def test_scratch_size_queries_are_host_only():
+    from vearo_amd import _abi
+
+    assert _abi.lib.vh_layernorm_bwd_scratch_bytes(16384, 768) >= 2 * 768 * 4
+    assert _abi.lib.vh_layernorm_bwd_scratch_bytes(0, 768) == 0
+    assert _abi.lib.vh_gelu_bias_bwd_scratch_bytes(16384, 3072) >= 3072 * 4
+    assert _abi.lib.vh_embedding_bwd_scratch_bytes(16384, 50257) >= 4 * (4 * 16384 + 3 * 50257)
+    assert _abi.lib.vh_cross_entropy_fwd_scratch_bytes(16384) >= 16384 * 4
+
+
+def elf_symbols(path):
+    data = open(path, "rb").read()
+    assert data[:4] == b"\x7fELF" and data[4] == 2, "expected a 64-bit ELF code object"
+    shoff, = struct.unpack_from("<Q", data, 0x28)
+    shentsize, shnum = struct.unpack_from("<HH", data, 0x3A)
+    secs = [struct.unpack_from("<IIQQQQIIQQ", data, shoff + i * shentsize) for i in range(shnum)]
+    names = set()
+    for s in secs:
+        if s[1] in (2, 11):  # SHT_SYMTAB, SHT_DYNSYM
+            strtab = secs[s[6]]
+            for off in range(s[4], s[4] + s[5], 24):
+                st_name, = struct.unpack_from("<I", data, off)
+                end = data.index(b"\0", strtab[4] + st_name)
+                names.add(data[strtab[4] + st_name:end].decode())
+    return names
+
+
+def launcher_kernel_names():
+    """Every kernel name the host launcher (vearo_amd/csrc/runtime.cpp) can build."""
+    nv = [1, 2, 3, 4, 6, 8, 12, 16]
+    cfgs_all = [(16, 1), (32, 1)] + [(64, v) for v in nv] + [(1024, v) for v in nv]
+    cfgs_small = [(t, v) for t, v in cfgs_all if v <= 8]
+    names = set()
+    for vw in (1, 4):
+        for t, v in cfgs_all:
+            names |= {f"vh_ln_fwd_t{t}_n{v}_v{vw}", f"vh_sm_fwd_t{t}_n{v}_v{vw}"}
+        for t, v in cfgs_small:
+            names |= {f"vh_ln_bwd_t{t}_n{v}_v{vw}", f"vh_sm_bwd_t{t}_n{v}_v{vw}"}
+        for v in nv:
+            names |= {f"vh_gelu_bias_fwd_n{v}_v{vw}", f"vh_gelu_bias_bwd_n{v}_v{vw}"}
+        names |= {f"vh_gelu_fwd_v{vw}", f"vh_gelu_gradmul_v{vw}", f"vh_emb_fwd_v{vw}",
+                  f"vh_emb_segsum_v{vw}", f"vh_binary_contig_v{vw}"}
+    for v in [1, 2, 4, 8, 16, 24, 32, 40, 48, 50, 56, 64]:
+        names |= {f"vh_xent_fwd_n{v}", f"vh_xent_bwd_n{v}"}
+    names |= {"vh_xent_fwd_stream", "vh_xent_bwd_stream", "vh_xent_reduce", "vh_col_reduce",
+              "vh_emb_tokens", "vh_scan", "vh_emb_place", "vh_emb_sort_big", "vh_fill",
+              "vh_binary_strided_i32", "vh_binary_strided_i64", "vh_reduce_thread",
+              "vh_reduce_wave", "vh_strided_copy_i32", "vh_strided_copy_i64"}
+    return names
+
+
+def test_code_object_holds_every_launchable_kernel():
+    if not os.path.exists(CODE_OBJECT):
+        pytest.skip("code object not built in-tree")
+    syms = elf_symbols(CODE_OBJECT)
+    missing = sorted(launcher_kernel_names() - syms)
+    assert not missing, missing
+
+
+def test_embedded_code_object_matches_build():
+    if not os.path.exists(CODE_OBJECT):
+        pytest.skip("code object not built in-tree")
+    blob = open(CODE_OBJECT, "rb").read()
+    assert blob in open(LIB, "rb").read()

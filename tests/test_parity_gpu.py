@@ -1,0 +1,317 @@
+"""GPU parity: every hot-path entry point of libvearo_hip.so, called through the
+C ABI, against the CPU oracle on identical seeded inputs. Embedding forward and
+backward must be bit-exact; everything else within 1e-5 + 1e-4*|cpu|.
+Shapes cover the BASELINE configs (or a row-subset of them where the oracle
+would take minutes) plus the ragged / tiny / large-row variants of each kernel
+family. Full-size properties of the biggest configs run in test_properties_gpu.py."""
+import numpy as np
+import pytest
+
+import oracle as O
+from parity import assert_parity, dev, fetch, out
+
+pytestmark = pytest.mark.gpu
+
+
+def rng(tag):
+    return np.random.default_rng(0x5EED0000 + tag)
+
+
+# ------------------------------------------------------------------ layernorm
+LN_SHAPES = [(2048, 128), (16384, 768), (1, 5), (3, 33), (7, 64), (130, 100), (64, 1000),
+             (17, 1030), (8, 4096), (4, 20000), (5, 1)]
+
+
+@pytest.mark.parametrize("rows,C", LN_SHAPES)
+def test_layernorm_fwd_bwd(vh, rows, C):
+    print(f"layernorm rows={rows} C={C}", flush=True)
+    r = rng(0)
+    x = r.normal(size=(rows, C)).astype(np.float32)
+    w = (1 + 0.02 * r.normal(size=C)).astype(np.float32)
+    b = (0.02 * r.normal(size=C)).astype(np.float32)
+    dy = r.normal(size=(rows, C)).astype(np.float32)
+    eps = 1e-5
+    X, W, B, DY = dev(vh, x), dev(vh, w), dev(vh, b), dev(vh, dy)
+    Y, DX, DW, DB = out(vh, (rows, C)), out(vh, (rows, C)), out(vh, (C,)), out(vh, (C,))
+    vh.check(vh.lib.vh_layernorm_fwd(X.ptr, W.ptr, B.ptr, Y.ptr, rows, C, eps, None))
+    vh.check(vh.lib.vh_layernorm_bwd(X.ptr, W.ptr, DY.ptr, DX.ptr, DW.ptr, DB.ptr, rows, C, eps,
+                                     None, 0, None))
+    y_cpu = O.layernorm(x, w, b, eps)
+    dx_cpu, dw_cpu, db_cpu = O.layernorm_backward(x, w, b, dy, eps)
+    assert_parity(fetch(vh, Y, (rows, C)), y_cpu, name="y")
+    assert_parity(fetch(vh, DX, (rows, C)), dx_cpu, name="dx")
+    x64, dy64 = x.astype(np.float64), dy.astype(np.float64)
+    xh = (x64 - x64.mean(1, keepdims=True)) / np.sqrt(x64.var(1, keepdims=True) + eps)
+    assert_parity(fetch(vh, DW, (C,)), dw_cpu, (dy64 * xh).sum(0), name="dgamma")
+    assert_parity(fetch(vh, DB, (C,)), db_cpu, dy64.sum(0), name="dbeta")
+
+
+def test_layernorm_deterministic(vh):
+    r = rng(1)
+    rows, C = 4096, 768
+    x = r.normal(size=(rows, C)).astype(np.float32)
+    w = np.ones(C, np.float32)
+    dy = r.normal(size=(rows, C)).astype(np.float32)
+    X, W, DY = dev(vh, x), dev(vh, w), dev(vh, dy)
+    res = []
+    for _ in range(3):
+        DX, DW, DB = out(vh, (rows, C)), out(vh, (C,)), out(vh, (C,))
+        vh.check(vh.lib.vh_layernorm_bwd(X.ptr, W.ptr, DY.ptr, DX.ptr, DW.ptr, DB.ptr, rows, C,
+                                         1e-5, None, 0, None))
+        res.append((fetch(vh, DW, (C,)), fetch(vh, DB, (C,))))
+    for dw, db in res[1:]:
+        np.testing.assert_array_equal(dw, res[0][0])
+        np.testing.assert_array_equal(db, res[0][1])
+
+
+def test_layernorm_explicit_scratch_and_errors(vh):
+    rows, C = 300, 96
+    need = vh.lib.vh_layernorm_bwd_scratch_bytes(rows, C)
+    assert need > 0
+    r = rng(2)
+    x = r.normal(size=(rows, C)).astype(np.float32)
+    w, dy = np.ones(C, np.float32), r.normal(size=(rows, C)).astype(np.float32)
+    X, W, DY = dev(vh, x), dev(vh, w), dev(vh, dy)
+    DX, DW, DB = out(vh, (rows, C)), out(vh, (C,)), out(vh, (C,))
+    S = vh.DeviceBuffer(need)
+    rc = vh.lib.vh_layernorm_bwd(X.ptr, W.ptr, DY.ptr, DX.ptr, DW.ptr, DB.ptr, rows, C, 1e-5, S.ptr,
+                                 need - 256, None)
+    assert rc == vh.VH_ERR_INVALID and "scratch buffer too small" in vh.last_error()
+    vh.check(vh.lib.vh_layernorm_bwd(X.ptr, W.ptr, DY.ptr, DX.ptr, DW.ptr, DB.ptr, rows, C, 1e-5,
+                                     S.ptr, need, None))
+    _, dw_cpu, db_cpu = O.layernorm_backward(x, w, np.zeros(C, np.float32), dy, 1e-5)
+    assert_parity(fetch(vh, DB, (C,)), db_cpu, dy.astype(np.float64).sum(0), name="dbeta")
+    assert vh.lib.vh_layernorm_fwd(X.ptr, W.ptr, W.ptr, DX.ptr, -1, C, 1e-5, None) == vh.VH_ERR_INVALID
+
+
+# ----------------------------------------------------------------------- gelu
+@pytest.mark.parametrize("rows,C", [(16384, 3072), (3, 5), (33, 100), (7, 4096), (5, 5000)])
+def test_gelu_bias_fwd_bwd(vh, rows, C):
+    print(f"gelu_bias rows={rows} C={C}", flush=True)
+    r = rng(1)
+    x = (1.5 * r.normal(size=(rows, C))).astype(np.float32)
+    bias = (0.02 * r.normal(size=C)).astype(np.float32)
+    dy = r.normal(size=(rows, C)).astype(np.float32)
+    X, Bi, DY = dev(vh, x), dev(vh, bias), dev(vh, dy)
+    Y, DX, DB = out(vh, (rows, C)), out(vh, (rows, C)), out(vh, (C,))
+    vh.check(vh.lib.vh_gelu_bias_fwd(X.ptr, Bi.ptr, Y.ptr, rows, C, None))
+    vh.check(vh.lib.vh_gelu_bias_bwd(X.ptr, Bi.ptr, DY.ptr, DX.ptr, DB.ptr, rows, C, None, 0, None))
+    assert_parity(fetch(vh, Y, (rows, C)), O.gelu_bias_forward(x, bias), name="y")
+    dx_cpu, db_cpu = O.gelu_bias_backward(x, bias, dy)
+    assert_parity(fetch(vh, DX, (rows, C)), dx_cpu, name="dx")
+    assert_parity(fetch(vh, DB, (C,)), db_cpu, dx_cpu.astype(np.float64).sum(0), name="dbias")
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 1000003])
+def test_gelu_and_grad_mul(vh, n):
+    r = rng(3)
+    x = (2.0 * r.normal(size=n)).astype(np.float32)
+    dy = r.normal(size=n).astype(np.float32)
+    X, DY, Y, DX = dev(vh, x), dev(vh, dy), out(vh, (n,)), out(vh, (n,))
+    vh.check(vh.lib.vh_gelu_fwd(X.ptr, Y.ptr, n, None))
+    vh.check(vh.lib.vh_gelu_grad_mul(X.ptr, DY.ptr, DX.ptr, n, None))
+    assert_parity(fetch(vh, Y, (n,)), O.gelu(x), name="gelu")
+    assert_parity(fetch(vh, DX, (n,)), O.binary(2, dy, O.gelu_grad_mask(x)), name="gelu'")
+
+
+# -------------------------------------------------------------------- softmax
+def causal_scores(r, B, H, T):
+    s = (r.normal(size=(B, H, T, T)) / 8.0).astype(np.float32)
+    iu = np.triu_indices(T, 1)
+    s[:, :, iu[0], iu[1]] = -np.inf
+    return s
+
+
+@pytest.mark.parametrize("B,H,T", [(2, 12, 1024), (1, 2, 37), (2, 3, 128), (1, 1, 1000),
+                                   (1, 1, 2048), (1, 1, 5000)])
+@pytest.mark.parametrize("causal", [0, 1])
+def test_softmax_fwd_bwd(vh, B, H, T, causal):
+    print(f"softmax B={B} H={H} T={T} causal={causal}", flush=True)
+    r = rng(2)
+    x = causal_scores(r, B, H, T)
+    dy = r.normal(size=x.shape).astype(np.float32)
+    rows = B * H * T
+    X, DY, Y, DX, DX2 = dev(vh, x), dev(vh, dy), out(vh, x.shape), out(vh, x.shape), out(vh, x.shape)
+    vh.check(vh.lib.vh_softmax_fwd(X.ptr, Y.ptr, rows, T, causal, None))
+    vh.check(vh.lib.vh_softmax_bwd(Y.ptr, DY.ptr, DX.ptr, rows, T, 0, causal, None))
+    vh.check(vh.lib.vh_softmax_bwd(X.ptr, DY.ptr, DX2.ptr, rows, T, 1, causal, None))
+    y_cpu = O.softmax(x, 3)
+    dx_cpu = O.softmax_backward_composite(x, dy, 3)
+    y = fetch(vh, Y, x.shape)
+    assert_parity(y, y_cpu, name="y")
+    iu = np.triu_indices(T, 1)
+    assert np.all(y[:, :, iu[0], iu[1]] == 0.0)
+    assert_parity(fetch(vh, DX, x.shape), dx_cpu, name="dx(from y)")
+    assert_parity(fetch(vh, DX2, x.shape), dx_cpu, name="dx(from x)")
+
+
+def test_softmax_dense_rows(vh):
+    r = rng(4)
+    for rows, T in [(100, 1024), (5, 3), (9, 17), (3, 65536)]:
+        x = r.normal(size=(rows, T)).astype(np.float32) * 3
+        dy = r.normal(size=(rows, T)).astype(np.float32)
+        X, DY, Y, DX = dev(vh, x), dev(vh, dy), out(vh, x.shape), out(vh, x.shape)
+        vh.check(vh.lib.vh_softmax_fwd(X.ptr, Y.ptr, rows, T, 0, None))
+        if T <= 32768:
+            vh.check(vh.lib.vh_softmax_bwd(X.ptr, DY.ptr, DX.ptr, rows, T, 1, 0, None))
+            assert_parity(fetch(vh, DX, x.shape), O.softmax_backward_composite(x, dy, 1), name="dx")
+        assert_parity(fetch(vh, Y, x.shape), O.softmax(x, 1), name=f"y T={T}")
+
+
+# ------------------------------------------------------------------ embedding
+def zipf_ids(r, n, V, s=1.1):
+    ranks = np.arange(1, V + 1, dtype=np.float64)
+    cdf = np.cumsum(ranks ** -s)
+    cdf /= cdf[-1]
+    return np.searchsorted(cdf, r.random(n)).astype(np.float32)
+
+
+@pytest.mark.parametrize("dist", ["uniform", "zipf"])
+def test_embedding_config3_bit_exact(vh, dist):
+    print(f"embedding config3 {dist}", flush=True)
+    r = rng(3)
+    V, D, n = 50257, 768, 16384
+    W = (0.02 * r.normal(size=(V, D))).astype(np.float32)
+    ids = (r.integers(0, V, size=n).astype(np.float32) if dist == "uniform" else zipf_ids(r, n, V))
+    dy = r.normal(size=(n, D)).astype(np.float32)
+    I, Wd, DY = dev(vh, ids), dev(vh, W), dev(vh, dy)
+    OUT, DW = out(vh, (n, D)), out(vh, (V, D))
+    vh.check(vh.lib.vh_embedding_fwd(I.ptr, Wd.ptr, OUT.ptr, n, V, D, None))
+    vh.check(vh.lib.vh_embedding_bwd(I.ptr, DY.ptr, DW.ptr, n, V, D, None, 0, None))
+    np.testing.assert_array_equal(fetch(vh, OUT, (n, D)), O.embedding(ids, W))
+    # Same per-row summation order as the CPU loop: bit-exact, not just close.
+    np.testing.assert_array_equal(fetch(vh, DW, (V, D)), O.embedding_backward(ids, (V, D), dy))
+
+
+@pytest.mark.parametrize("n,V,D", [(1, 3, 2), (10, 4, 5), (300, 7, 64), (5000, 3, 33),
+                                   (9000, 2, 8), (100, 100000, 1)])
+def test_embedding_shapes(vh, n, V, D):
+    r = rng(5)
+    ids = r.integers(0, V, size=n).astype(np.float32) + r.uniform(-0.49, 0.49, size=n).astype(np.float32)
+    ids = np.clip(ids, 0, V - 1).astype(np.float32)
+    W = r.normal(size=(V, D)).astype(np.float32)
+    dy = r.normal(size=(n, D)).astype(np.float32)
+    I, Wd, DY = dev(vh, ids), dev(vh, W), dev(vh, dy)
+    OUT, DW = out(vh, (n, D)), out(vh, (V, D))
+    vh.check(vh.lib.vh_embedding_fwd(I.ptr, Wd.ptr, OUT.ptr, n, V, D, None))
+    vh.check(vh.lib.vh_embedding_bwd(I.ptr, DY.ptr, DW.ptr, n, V, D, None, 0, None))
+    np.testing.assert_array_equal(fetch(vh, OUT, (n, D)), O.embedding(ids, W))
+    np.testing.assert_array_equal(fetch(vh, DW, (V, D)), O.embedding_backward(ids, (V, D), dy))
+
+
+@pytest.mark.parametrize("bad,msg", [(-1.0, "Token ID cannot be negative: -1"),
+                                     (7.0, "Token ID 7 out of vocabulary bound 5"),
+                                     (4.5, "Token ID 5 out of vocabulary bound 5"),
+                                     (float("nan"), "Token ID cannot be negative: NaN"),
+                                     (-0.25, "Token ID cannot be negative: -0.25")])
+def test_embedding_bad_ids_report_cpu_panic(vh, bad, msg):
+    V, D = 5, 4
+    ids = np.float32([1, 2, bad, 3, -2.0])
+    I, Wd, DY = dev(vh, ids), dev(vh, np.ones((V, D))), dev(vh, np.ones((5, D)))
+    OUT, DW = out(vh, (5, D)), out(vh, (V, D))
+    for call in (lambda: vh.lib.vh_embedding_fwd(I.ptr, Wd.ptr, OUT.ptr, 5, V, D, None),
+                 lambda: vh.lib.vh_embedding_bwd(I.ptr, DY.ptr, DW.ptr, 5, V, D, None, 0, None)):
+        vh.check(call())
+        with pytest.raises(vh.DevicePanic) as ei:
+            vh.sync()
+        assert ei.value.msg == msg
+        with pytest.raises(O.Panic) as eo:
+            O.embedding(ids, np.ones((V, D), np.float32))
+        assert str(eo.value) == msg
+    vh.sync()  # the record is cleared once reported
+
+
+# -------------------------------------------------------------- cross-entropy
+@pytest.mark.parametrize("B,V", [(512, 50257), (3, 5), (64, 1000), (7, 70000), (1, 1)])
+def test_cross_entropy_fwd_bwd(vh, B, V):
+    print(f"cross_entropy B={B} V={V}", flush=True)
+    r = rng(4)
+    logits = (2.0 * r.normal(size=(B, V))).astype(np.float32)
+    tg = r.integers(0, V, size=B).astype(np.float32)
+    go = np.float32([1.3])
+    L, T, GO = dev(vh, logits), dev(vh, tg), dev(vh, go)
+    LOSS, DL = out(vh, (1,)), out(vh, (B, V))
+    vh.check(vh.lib.vh_cross_entropy_fwd(L.ptr, T.ptr, LOSS.ptr, B, V, None, 0, None))
+    vh.check(vh.lib.vh_cross_entropy_bwd(L.ptr, T.ptr, GO.ptr, DL.ptr, B, V, None))
+    assert_parity(fetch(vh, LOSS, (1,)), O.cross_entropy(logits, tg), name="loss")
+    assert_parity(fetch(vh, DL, (B, V)), O.cross_entropy_backward(logits, tg, go), name="dlogits")
+
+
+def test_cross_entropy_kats_and_panics(vh):
+    L, T = dev(vh, np.float32([[1000.0, -1000.0]])), dev(vh, np.float32([0.0]))
+    LOSS = out(vh, (1,))
+    vh.check(vh.lib.vh_cross_entropy_fwd(L.ptr, T.ptr, LOSS.ptr, 1, 2, None, 0, None))
+    assert abs(fetch(vh, LOSS, (1,))[0]) < 1e-4  # cpu lib.rs:2902-2913
+    L = dev(vh, np.zeros((2, 3), np.float32))
+    for tv, msg in [(-1.0, "Target class cannot be negative: -1"),
+                    (3.0, "Target class 3 out of vocab bounds 3")]:
+        T = dev(vh, np.float32([tv, 0.0]))
+        vh.check(vh.lib.vh_cross_entropy_fwd(L.ptr, T.ptr, LOSS.ptr, 2, 3, None, 0, None))
+        with pytest.raises(vh.DevicePanic) as ei:
+            vh.sync()
+        assert ei.value.msg == msg
+    rc = vh.lib.vh_cross_entropy_fwd(L.ptr, T.ptr, LOSS.ptr, 0, 3, None, 0, None)
+    assert rc == vh.VH_ERR_INVALID and vh.last_error() == "Batch size must be greater than 0"
+
+
+# --------------------------------------------------------- composites (a13)
+def test_binary_broadcast_and_strided(vh):
+    r = rng(6)
+    cases = [((64, 3072), (3072,)), ((3, 1, 5), (4, 1)), ((16, 12, 128, 128), (16, 12, 128, 1)),
+             ((1000,), (1000,)), ((7,), ())]
+    for ls, rs in cases:
+        a = r.normal(size=ls).astype(np.float32)
+        b = (r.normal(size=rs) + 3).astype(np.float32)
+        A, B = dev(vh, a), dev(vh, b)
+        shape = np.broadcast_shapes(ls, rs)
+        for op in range(4):
+            OUT = out(vh, shape)
+            vh.check(vh.lib.vh_binary(op, A.ptr, vh.layout(ls), B.ptr, vh.layout(rs), OUT.ptr, None))
+            np.testing.assert_array_equal(fetch(vh, OUT, shape), O.binary(op, a, b))
+    # Transposed (strided) operands, the backward's case.
+    a = np.arange(9, dtype=np.float32).reshape(3, 3) + 1
+    b = a[::-1].copy()
+    A, B = dev(vh, a), dev(vh, b)
+    OUT = out(vh, (3, 3))
+    vh.check(vh.lib.vh_binary(0, A.ptr, vh.layout((3, 3)), B.ptr, vh.layout((3, 3), (1, 3)), OUT.ptr, None))
+    np.testing.assert_array_equal(fetch(vh, OUT, (3, 3)), a + b.T)
+    rc = vh.lib.vh_binary(0, A.ptr, vh.layout((2, 3)), B.ptr, vh.layout((4,)), OUT.ptr, None)
+    assert rc == vh.VH_ERR_INVALID and vh.last_error() == "Shapes are not broadcastable"
+
+
+def test_reduce_and_strided_copy(vh):
+    r = rng(7)
+    x = r.normal(size=(4, 6, 300)).astype(np.float32)
+    X = dev(vh, x)
+    for dim in range(3):
+        for mean in (0, 1):
+            shape = tuple(s for i, s in enumerate(x.shape) if i != dim)
+            OUT = out(vh, shape)
+            vh.check(vh.lib.vh_reduce(mean, X.ptr, vh.layout(x.shape), dim, OUT.ptr, None))
+            assert_parity(fetch(vh, OUT, shape), O.reduce(x, dim, mean=bool(mean)),
+                          x.astype(np.float64).mean(dim) if mean else x.astype(np.float64).sum(dim))
+    # A transposed view [300, 6, 4] of the same buffer.
+    dims, strides = (300, 6, 4), (1, 300, 1800)
+    xt = np.transpose(x, (2, 1, 0))
+    OUT = out(vh, xt.shape)
+    vh.check(vh.lib.vh_strided_copy(X.ptr, vh.layout(dims, strides), OUT.ptr, None))
+    np.testing.assert_array_equal(fetch(vh, OUT, xt.shape), np.ascontiguousarray(xt))
+    OUT = out(vh, (300, 4))
+    vh.check(vh.lib.vh_reduce(0, X.ptr, vh.layout(dims, strides), 1, OUT.ptr, None))
+    np.testing.assert_array_equal(fetch(vh, OUT, (300, 4)), O.reduce(xt, 1))
+
+
+def test_arena_reuse_and_zeroing(vh):
+    before = vh.mem_stats()
+    bufs = [vh.DeviceBuffer(1 << 20, zero=True) for _ in range(4)]
+    for b in bufs:
+        assert not fetch(vh, b, (1 << 18,)).any()
+        b.upload(np.ones(1 << 18, np.float32))
+    for b in bufs:
+        b.close()
+    again = vh.DeviceBuffer(1 << 20, zero=True)
+    assert not fetch(vh, again, (1 << 18,)).any()  # reused block comes back zeroed
+    again.close()
+    after = vh.mem_stats()
+    assert after.live_bytes == before.live_bytes
+    assert after.hip_bytes <= before.hip_bytes + 4 * (1 << 20)

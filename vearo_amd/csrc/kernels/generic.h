@@ -1,0 +1,96 @@
+// generic.h -- the strided / broadcast building blocks the unchanged autograd
+// composes around the hot path: binary elementwise with broadcasting
+// (vearo-backend-cpu elementwise_op, crates/vearo-backend-cpu/src/lib.rs:160-238),
+// single-axis sum / mean (lib.rs:566-653), strided gather to contiguous (the
+// device replacement for Tensor::contiguous, crates/vearo-core/src/tensor.rs:345-486)
+// and a fill kernel (zeroing without hipMemset, so it is safe inside graphs).
+#pragma once
+#include "common.h"
+
+VH_DEV float apply_op(int op, float a, float b) {
+  switch (op) {
+    case 0: return a + b;
+    case 1: return a - b;
+    case 2: return a * b;
+    default: return a / b;
+  }
+}
+
+// Offset of flat output index `i` under `l`'s strides, decomposed over `o`'s dims.
+template <typename IT>
+VH_DEV int64_t strided_offset(IT i, const StridedLayout& o, const StridedLayout& l) {
+  int64_t off = 0;
+  for (int d = o.rank - 1; d >= 0; --d) {
+    const IT dim = (IT)o.dims[d];
+    const IT c = i % dim;
+    i /= dim;
+    off += (int64_t)c * l.strides[d];
+  }
+  return off;
+}
+
+template <int VW>
+VH_DEV void binary_contig_impl(const BinaryArgs& a) {
+  const int64_t nu = a.n / VW;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < nu; u += stride) {
+    const Unit<VW> l = load_unit<VW>(a.l + u * VW);
+    const Unit<VW> r = load_unit<VW>(a.r + u * VW);
+    Unit<VW> o;
+#pragma unroll
+    for (int j = 0; j < VW; ++j) o.v[j] = apply_op(a.op, l.v[j], r.v[j]);
+    store_unit<VW>(a.out + u * VW, o);
+  }
+}
+
+template <typename IT>
+VH_DEV void binary_strided_impl(const BinaryArgs& a) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride) {
+    const float l = a.l[strided_offset<IT>((IT)i, a.ol, a.ll)];
+    const float r = a.r[strided_offset<IT>((IT)i, a.ol, a.rl)];
+    a.out[i] = apply_op(a.op, l, r);
+  }
+}
+
+// One thread per output; the reduced axis is walked in index order, which is the
+// CPU's accumulation order for each output element (bit-exact).
+VH_DEV void reduce_thread_impl(const ReduceArgs& a) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < a.n_out; o += stride) {
+    const float* p = a.x + strided_offset<int64_t>(o, a.ol, a.ol);
+    float s = 0.0f;
+    for (int64_t k = 0; k < a.red_len; ++k) s += p[k * a.red_stride];
+    a.out[o] = a.mean ? s / (float)a.red_len : s;
+  }
+}
+
+// One wave per output for a unit-stride reduced axis (coalesced); per-lane
+// sequential partials then a fixed wave tree.
+VH_DEV void reduce_wave_impl(const ReduceArgs& a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t o = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (o >= a.n_out) return;
+  const float* p = a.x + strided_offset<int64_t>(o, a.ol, a.ol);
+  float s = 0.0f;
+  for (int64_t k = lane; k < a.red_len; k += 64) s += p[k];
+  s = group_sum<64>(s);
+  if (lane == 0) a.out[o] = a.mean ? s / (float)a.red_len : s;
+}
+
+template <typename IT>
+VH_DEV void strided_copy_impl(const CopyArgs& a) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride)
+    a.dst[i] = a.src[strided_offset<IT>((IT)i, a.sl, a.sl)];
+}
+
+VH_DEV void fill_impl(const FillArgs& a) {
+  const int64_t n4 = (reinterpret_cast<uintptr_t>(a.p) & 15) ? 0 : a.n / 4;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const float v = a.value;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int64_t u = tid; u < n4; u += stride)
+    *reinterpret_cast<float4*>(a.p + u * 4) = make_float4(v, v, v, v);
+  for (int64_t i = n4 * 4 + tid; i < a.n; i += stride) a.p[i] = v;
+}

@@ -1,0 +1,118 @@
+// vearo_kernels.hip -- the single translation unit compiled to the gfx950 code
+// object (hipcc --genco) that libvearo_hip.so embeds and loads with
+// hipModuleLoadData. Every kernel is extern "C" with one argument struct; the
+// host looks kernels up by these names (see vearo_amd/csrc/runtime.cpp).
+//
+// Row-engine kernels are instantiated per (TEAM, NV, VW):
+//   TEAM lanes own one row, each lane holds NV units of VW floats.
+#include "common.h"
+#include "embedding.h"
+#include "gelu.h"
+#include "generic.h"
+#include "layernorm.h"
+#include "softmax.h"
+#include "xent.h"
+
+#define BS_OF(T) ((T) > 256 ? (T) : 256)
+
+// (TEAM, NV) pairs; NV <= 8 are also used by the backward kernels.
+#define ROW_CFG_SMALL(M, VW) \
+  M(16, 1, VW) M(32, 1, VW) M(64, 1, VW) M(64, 2, VW) M(64, 3, VW) M(64, 4, VW) \
+  M(64, 6, VW) M(64, 8, VW) M(1024, 1, VW) M(1024, 2, VW) M(1024, 3, VW) \
+  M(1024, 4, VW) M(1024, 6, VW) M(1024, 8, VW)
+#define ROW_CFG_BIG(M, VW) M(64, 12, VW) M(64, 16, VW) M(1024, 12, VW) M(1024, 16, VW)
+#define ROW_CFG_ALL(M, VW) ROW_CFG_SMALL(M, VW) ROW_CFG_BIG(M, VW)
+
+#define K_LN_FWD(T, N, VW)                                                        \
+  extern "C" __global__ void __launch_bounds__(BS_OF(T))                          \
+      vh_ln_fwd_t##T##_n##N##_v##VW(LnFwdArgs a) {                                \
+    ln_fwd_impl<T, N, VW>(a);                                                     \
+  }
+ROW_CFG_ALL(K_LN_FWD, 1)
+ROW_CFG_ALL(K_LN_FWD, 4)
+
+#define K_LN_BWD(T, N, VW)                                                        \
+  extern "C" __global__ void __launch_bounds__(BS_OF(T))                          \
+      vh_ln_bwd_t##T##_n##N##_v##VW(LnBwdArgs a) {                                \
+    extern __shared__ float dyn_lds[];                                            \
+    ln_bwd_impl<T, N, VW>(a, dyn_lds);                                            \
+  }
+ROW_CFG_SMALL(K_LN_BWD, 1)
+ROW_CFG_SMALL(K_LN_BWD, 4)
+
+#define K_SM_FWD(T, N, VW)                                                        \
+  extern "C" __global__ void __launch_bounds__(BS_OF(T))                          \
+      vh_sm_fwd_t##T##_n##N##_v##VW(SoftmaxArgs a) {                              \
+    softmax_fwd_impl<T, N, VW>(a);                                                \
+  }
+ROW_CFG_ALL(K_SM_FWD, 1)
+ROW_CFG_ALL(K_SM_FWD, 4)
+
+#define K_SM_BWD(T, N, VW)                                                        \
+  extern "C" __global__ void __launch_bounds__(BS_OF(T))                          \
+      vh_sm_bwd_t##T##_n##N##_v##VW(SoftmaxArgs a) {                              \
+    softmax_bwd_impl<T, N, VW>(a);                                                \
+  }
+ROW_CFG_SMALL(K_SM_BWD, 1)
+ROW_CFG_SMALL(K_SM_BWD, 4)
+
+extern "C" __global__ void __launch_bounds__(1024) vh_col_reduce(ColReduceArgs a) {
+  col_reduce_impl(a);
+}
+
+// GELU
+extern "C" __global__ void __launch_bounds__(256) vh_gelu_fwd_v1(EltArgs a) { gelu_flat_impl<0, 1>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_gelu_fwd_v4(EltArgs a) { gelu_flat_impl<0, 4>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_gelu_gradmul_v1(EltArgs a) { gelu_flat_impl<1, 1>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_gelu_gradmul_v4(EltArgs a) { gelu_flat_impl<1, 4>(a); }
+
+#define GB_CFG(M, VW) M(1, VW) M(2, VW) M(3, VW) M(4, VW) M(6, VW) M(8, VW) M(12, VW) M(16, VW)
+#define K_GB_FWD(N, VW)                                                           \
+  extern "C" __global__ void __launch_bounds__(256)                               \
+      vh_gelu_bias_fwd_n##N##_v##VW(GeluBiasBwdArgs a) {                          \
+    gelu_bias_fwd_impl<N, VW>(a);                                                 \
+  }
+#define K_GB_BWD(N, VW)                                                           \
+  extern "C" __global__ void __launch_bounds__(256)                               \
+      vh_gelu_bias_bwd_n##N##_v##VW(GeluBiasBwdArgs a) {                          \
+    gelu_bias_bwd_impl<N, VW>(a);                                                 \
+  }
+GB_CFG(K_GB_FWD, 1)
+GB_CFG(K_GB_FWD, 4)
+GB_CFG(K_GB_BWD, 1)
+GB_CFG(K_GB_BWD, 4)
+
+// Embedding
+extern "C" __global__ void __launch_bounds__(256) vh_emb_fwd_v1(EmbFwdArgs a) { emb_fwd_impl<1>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_emb_fwd_v4(EmbFwdArgs a) { emb_fwd_impl<4>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_emb_tokens(EmbTokArgs a) { emb_tokens_impl(a); }
+extern "C" __global__ void __launch_bounds__(1024) vh_scan(ScanArgs a) { scan_impl(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_emb_place(EmbPlaceArgs a) { emb_place_impl(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_emb_sort_big(EmbSortArgs a) { emb_sort_big_impl(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_emb_segsum_v1(EmbSegArgs a) { emb_segsum_impl<1>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_emb_segsum_v4(EmbSegArgs a) { emb_segsum_impl<4>(a); }
+
+// Cross-entropy
+#define XE_CFG(M) M(1) M(2) M(4) M(8) M(16) M(24) M(32) M(40) M(48) M(50) M(56) M(64)
+#define K_XE(N)                                                                   \
+  extern "C" __global__ void __launch_bounds__(1024) vh_xent_fwd_n##N(XentArgs a) { \
+    xent_cached_impl<N, false>(a);                                                \
+  }                                                                               \
+  extern "C" __global__ void __launch_bounds__(1024) vh_xent_bwd_n##N(XentArgs a) { \
+    xent_cached_impl<N, true>(a);                                                 \
+  }
+XE_CFG(K_XE)
+extern "C" __global__ void __launch_bounds__(1024) vh_xent_fwd_stream(XentArgs a) { xent_stream_impl<false>(a); }
+extern "C" __global__ void __launch_bounds__(1024) vh_xent_bwd_stream(XentArgs a) { xent_stream_impl<true>(a); }
+extern "C" __global__ void __launch_bounds__(1024) vh_xent_reduce(XentReduceArgs a) { xent_reduce_impl(a); }
+
+// Generic building blocks
+extern "C" __global__ void __launch_bounds__(256) vh_binary_contig_v1(BinaryArgs a) { binary_contig_impl<1>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_binary_contig_v4(BinaryArgs a) { binary_contig_impl<4>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_binary_strided_i32(BinaryArgs a) { binary_strided_impl<uint32_t>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_binary_strided_i64(BinaryArgs a) { binary_strided_impl<uint64_t>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_reduce_thread(ReduceArgs a) { reduce_thread_impl(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_reduce_wave(ReduceArgs a) { reduce_wave_impl(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_strided_copy_i32(CopyArgs a) { strided_copy_impl<uint32_t>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_strided_copy_i64(CopyArgs a) { strided_copy_impl<uint64_t>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_fill(FillArgs a) { fill_impl(a); }

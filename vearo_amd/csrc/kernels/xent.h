@@ -1,0 +1,114 @@
+// xent.h -- cross-entropy forward / backward over [B, V] logits for gfx950.
+//
+// Semantics: vearo-backend-cpu cross_entropy (crates/vearo-backend-cpu/src/lib.rs:982-1051):
+// per row max (from -inf), sum of exp(l - max), log_softmax = l[t] - max - ln(sum);
+// loss = -(sum over rows of log_softmax) / B, returned as one float.
+// cross_entropy_backward (lib.rs:1053-1127): dl = go * (p - 1[c == t]) / B with
+// p = exp(l - max) / sum. Targets are f32 class ids, rounded like Rust's round().
+//
+// Layout: logits / dlogits [B, V] row-major, targets [B], one 1024-thread
+// workgroup (16 waves) per row. When V <= 1024*NV the row is held in VGPRs and
+// read from HBM once (fwd 4 B/elem read; bwd 4 B read + 4 B write). Longer rows
+// take the streaming variant: one online max/sum pass, plus a write pass in bwd.
+// The scalar per-row log_softmax values are reduced by xent_reduce in a fixed
+// order, so the loss is deterministic.
+#pragma once
+#include "common.h"
+
+VH_DEV int32_t xent_target(const XentArgs& a, int64_t row) {
+  const float tv = a.targets[row];
+  const int32_t t = checked_index(tv, a.V);
+  if (t < 0 && threadIdx.x == 0) {
+    atomicMin(&a.err->target, err_pack(row, tv));
+    a.err->target_bound = (unsigned)a.V;
+  }
+  return t;
+}
+
+template <int NV, bool BWD>
+VH_DEV void xent_cached_impl(const XentArgs& a) {
+  __shared__ float red[16];
+  const int64_t row = blockIdx.x;
+  const int V = a.V;
+  const float* lr = a.logits + row * V;
+  float v[NV];
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = threadIdx.x + k * 1024;
+    v[k] = c < V ? lr[c] : -INFINITY;
+    if (v[k] > m) m = v[k];
+  }
+  m = team_max<1024>(m, red);
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = threadIdx.x + k * 1024;
+    const float e = c < V ? expf(v[k] - m) : 0.0f;
+    v[k] = e;
+    s += e;
+  }
+  s = team_sum<1024>(s, red);
+  const int32_t t = xent_target(a, row);
+  if constexpr (!BWD) {
+    if (threadIdx.x == 0) a.out[row] = t >= 0 ? lr[t] - m - logf(s) : 0.0f;
+  } else {
+    const float go = *a.grad_out;
+    const float Bf = (float)a.B;
+    float* o = a.out + row * V;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c = threadIdx.x + k * 1024;
+      if (c < V) {
+        const float p = v[k] / s;
+        const float ind = c == t ? 1.0f : 0.0f;
+        o[c] = go * (p - ind) / Bf;
+      }
+    }
+  }
+}
+
+// Any V: per-thread online max / rescaled sum, merged across the workgroup.
+template <bool BWD>
+VH_DEV void xent_stream_impl(const XentArgs& a) {
+  __shared__ float red[16];
+  const int64_t row = blockIdx.x;
+  const int V = a.V;
+  const float* lr = a.logits + row * V;
+  float m = -INFINITY, s = 0.0f;
+  for (int c = threadIdx.x; c < V; c += 1024) {
+    const float x = lr[c];
+    if (x > m) {
+      s = s * expf(m - x) + 1.0f;
+      m = x;
+    } else if (x != -INFINITY) {
+      s += expf(x - m);
+    }
+  }
+  const float M = team_max<1024>(m, red);
+  s = (m == -INFINITY) ? 0.0f : s * expf(m - M);
+  s = team_sum<1024>(s, red);
+  const int32_t t = xent_target(a, row);
+  if constexpr (!BWD) {
+    if (threadIdx.x == 0) a.out[row] = t >= 0 ? lr[t] - M - logf(s) : 0.0f;
+  } else {
+    const float go = *a.grad_out;
+    const float Bf = (float)a.B;
+    float* o = a.out + row * V;
+    for (int c = threadIdx.x; c < V; c += 1024) {
+      const float p = expf(lr[c] - M) / s;
+      const float ind = c == t ? 1.0f : 0.0f;
+      o[c] = go * (p - ind) / Bf;
+    }
+  }
+}
+
+// loss = -(sum of per-row log_softmax) / B; one 1024-thread workgroup, each
+// thread sums a strided subset in order, then a fixed tree.
+VH_DEV void xent_reduce_impl(const XentReduceArgs& a) {
+  __shared__ float red[16];
+  float s = 0.0f;
+  for (int64_t i = threadIdx.x; i < a.B; i += 1024) s += a.row_loss[i];
+  s = team_sum<1024>(s, red);
+  if (threadIdx.x == 0) a.loss[0] = -s / (float)a.B;
+}

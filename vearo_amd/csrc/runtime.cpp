@@ -1,0 +1,864 @@
+// runtime.cpp -- host side of libvearo_hip.so: device init, the gfx950 code
+// object loaded with hipModuleLoadData, kernel lookup and launch through
+// hipModuleLaunchKernel, the caching arena over hipMalloc, the device error
+// record, and every C-ABI entry point declared in include/vearo_hip.h.
+//
+// Launch shapes are chosen here from the operand sizes, and every shape / size /
+// alignment assumption a kernel makes is checked before it is launched.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <charconv>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/vearo_hip.h"
+#include "vh_kargs.h"
+
+extern "C" const unsigned char vh_code_object_start[];
+extern "C" const unsigned char vh_code_object_end[];
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+#define VH_HIP(expr)                                                                   \
+  do {                                                                                 \
+    hipError_t e_ = (expr);                                                            \
+    if (e_ != hipSuccess)                                                              \
+      return fail(VH_ERR_HIP, std::string(#expr) + " failed: " + hipGetErrorString(e_)); \
+  } while (0)
+
+#define VH_TRY(expr)        \
+  do {                      \
+    int rc_ = (expr);       \
+    if (rc_ != VH_OK) return rc_; \
+  } while (0)
+
+struct Runtime {
+  bool ready = false;
+  int device = -1;
+  int cu_count = 0;
+  hipStream_t stream = nullptr;
+  hipModule_t module = nullptr;
+  VhErrRecord* err = nullptr;  // device memory
+  std::mutex fn_mu;
+  std::unordered_map<std::string, hipFunction_t> fns;
+};
+
+Runtime g_rt;
+std::mutex g_init_mu;
+
+hipStream_t S(void* s) { return s ? static_cast<hipStream_t>(s) : g_rt.stream; }
+
+int require_init() {
+  if (!g_rt.ready) return fail(VH_ERR_NOT_INIT, "vh_init has not been called");
+  return VH_OK;
+}
+
+int get_fn(const std::string& name, hipFunction_t* out) {
+  std::lock_guard<std::mutex> lk(g_rt.fn_mu);
+  auto it = g_rt.fns.find(name);
+  if (it != g_rt.fns.end()) {
+    *out = it->second;
+    return VH_OK;
+  }
+  hipFunction_t f = nullptr;
+  hipError_t e = hipModuleGetFunction(&f, g_rt.module, name.c_str());
+  if (e != hipSuccess)
+    return fail(VH_ERR_HIP, "kernel " + name + " not found in code object: " + hipGetErrorString(e));
+  g_rt.fns.emplace(name, f);
+  *out = f;
+  return VH_OK;
+}
+
+template <typename A>
+int launch(const std::string& name, unsigned gx, unsigned gy, unsigned block, unsigned shmem,
+           hipStream_t s, A args) {
+  if (gx == 0 || gy == 0) return VH_OK;
+  hipFunction_t f;
+  VH_TRY(get_fn(name, &f));
+  void* params[] = {&args};
+  VH_HIP(hipModuleLaunchKernel(f, gx, gy, 1, block, 1, 1, shmem, s, params, nullptr));
+  return VH_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ------------------------------------------------------------------ arena --
+// Exact-size free lists keyed by a rounded size (512 B granularity below 1 MiB,
+// 2 MiB above), 256-byte aligned blocks straight from hipMalloc. Freed blocks are
+// reused in stream order on the runtime stream.
+struct Arena {
+  std::mutex mu;
+  std::map<size_t, std::vector<void*>> free_lists;
+  std::unordered_map<void*, size_t> live;
+  size_t live_bytes = 0, cached_bytes = 0, peak_bytes = 0, hip_bytes = 0;
+
+  static size_t rounded(size_t b) {
+    if (b == 0) b = 1;
+    if (b <= (1u << 20)) return (b + 511) & ~size_t(511);
+    const size_t g = size_t(2) << 20;
+    return (b + g - 1) / g * g;
+  }
+
+  int release_all_cached() {
+    for (auto& kv : free_lists)
+      for (void* p : kv.second) {
+        hipError_t e = hipFree(p);
+        if (e != hipSuccess) return fail(VH_ERR_HIP, std::string("hipFree: ") + hipGetErrorString(e));
+        hip_bytes -= kv.first;
+      }
+    free_lists.clear();
+    cached_bytes = 0;
+    return VH_OK;
+  }
+
+  int alloc(size_t bytes, void** out) {
+    const size_t r = rounded(bytes);
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = free_lists.find(r);
+    void* p = nullptr;
+    if (it != free_lists.end() && !it->second.empty()) {
+      p = it->second.back();
+      it->second.pop_back();
+      cached_bytes -= r;
+    } else {
+      hipError_t e = hipMalloc(&p, r);
+      if (e != hipSuccess) {
+        (void)hipGetLastError();
+        // Give the cache back to the driver and retry once.
+        int rc = release_all_cached();
+        if (rc != VH_OK) return rc;
+        e = hipMalloc(&p, r);
+        if (e != hipSuccess) {
+          (void)hipGetLastError();
+          return fail(VH_ERR_OOM, "hipMalloc of " + std::to_string(r) + " bytes failed: " +
+                                      hipGetErrorString(e));
+        }
+      }
+      hip_bytes += r;
+    }
+    live.emplace(p, r);
+    live_bytes += r;
+    peak_bytes = std::max(peak_bytes, live_bytes);
+    *out = p;
+    return VH_OK;
+  }
+
+  int free(void* p) {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = live.find(p);
+    if (it == live.end()) return fail(VH_ERR_INVALID, "vh_free: pointer not allocated by vh_alloc");
+    const size_t r = it->second;
+    live.erase(it);
+    live_bytes -= r;
+    free_lists[r].push_back(p);
+    cached_bytes += r;
+    return VH_OK;
+  }
+};
+
+Arena g_arena;
+
+// Scratch buffer for one call: the caller's, or a block from the arena that is
+// returned (stream-ordered) when the call's launches are queued.
+struct Scratch {
+  void* p = nullptr;
+  bool owned = false;
+  ~Scratch() {
+    if (owned && p) g_arena.free(p);
+  }
+  int get(void* user, size_t user_bytes, size_t need) {
+    if (need == 0) return VH_OK;
+    if (user) {
+      if (user_bytes < need)
+        return fail(VH_ERR_INVALID, "scratch buffer too small: need " + std::to_string(need) +
+                                        " bytes, got " + std::to_string(user_bytes));
+      if (!aligned16(user)) return fail(VH_ERR_INVALID, "scratch buffer must be 16-byte aligned");
+      p = user;
+      return VH_OK;
+    }
+    VH_TRY(g_arena.alloc(need, &p));
+    owned = true;
+    return VH_OK;
+  }
+};
+
+size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+
+int fill(void* p, float value, int64_t n, hipStream_t s) {
+  if (n <= 0) return VH_OK;
+  FillArgs a{static_cast<float*>(p), n, value};
+  const int64_t blocks = std::min<int64_t>(cdiv(cdiv(n, 4), 256), 8192);
+  return launch("vh_fill", (unsigned)blocks, 1, 256, 0, s, a);
+}
+
+// --------------------------------------------------------- row engine cfg --
+struct RowCfg {
+  int team, nv, vw;
+};
+
+const int kNV[] = {1, 2, 3, 4, 6, 8, 12, 16};
+
+int pick_nv(int64_t need, int cap) {
+  for (int v : kNV)
+    if (v >= need && v <= cap) return v;
+  return -1;
+}
+
+// Units of VW floats per row: TEAM 16/32 for short rows, a wave64 up to 64*cap
+// units, a 1024-thread workgroup up to 1024*cap units.
+bool pick_row_cfg(int64_t C, bool vec_ok, int cap, RowCfg* out) {
+  const int vw = (vec_ok && C % 4 == 0) ? 4 : 1;
+  const int64_t U = C / vw;
+  if (U <= 16) {
+    *out = {16, 1, vw};
+    return true;
+  }
+  if (U <= 32) {
+    *out = {32, 1, vw};
+    return true;
+  }
+  int nv = pick_nv(cdiv(U, 64), cap);
+  if (nv > 0) {
+    *out = {64, nv, vw};
+    return true;
+  }
+  nv = pick_nv(cdiv(U, 1024), cap);
+  if (nv > 0) {
+    *out = {1024, nv, vw};
+    return true;
+  }
+  return false;
+}
+
+std::string row_kernel(const char* base, const RowCfg& c) {
+  return std::string(base) + "_t" + std::to_string(c.team) + "_n" + std::to_string(c.nv) + "_v" +
+         std::to_string(c.vw);
+}
+
+int block_of(const RowCfg& c) { return c.team > 256 ? c.team : 256; }
+
+// LayerNorm backward workgroup count: fixed caps (independent of the device) so
+// the scratch size and the reduction order depend on (rows, C) only.
+int64_t ln_bwd_blocks(int64_t rows, const RowCfg& c) {
+  const int groups = block_of(c) / c.team;
+  const int64_t cap = c.team > 256 ? 512 : 1024;
+  int64_t G = std::min<int64_t>(cdiv(rows, groups), cap);
+  if (G < 1) G = 1;
+  const int64_t rpb = cdiv(rows, G);
+  return cdiv(rows, rpb);
+}
+
+int64_t gb_blocks(int64_t rows) { return std::max<int64_t>(1, std::min<int64_t>(rows, 1024)); }
+
+// ----------------------------------------------------- device error record --
+std::string fmt_f32(float v) {
+  if (std::isnan(v)) return "NaN";
+  if (std::isinf(v)) return v < 0 ? "-inf" : "inf";
+  char buf[128];
+  auto r = std::to_chars(buf, buf + sizeof buf, v, std::chars_format::fixed);
+  return std::string(buf, r.ptr);
+}
+
+unsigned long long round_usize(float v) {
+  const float r = std::round(v);
+  if (!(r > 0.0f)) return 0;
+  if ((double)r >= 18446744073709551616.0) return ~0ull;
+  return (unsigned long long)r;
+}
+
+int check_error_record() {
+  VhErrRecord h;
+  VH_HIP(hipStreamSynchronize(g_rt.stream));
+  VH_HIP(hipMemcpy(&h, g_rt.err, sizeof h, hipMemcpyDeviceToHost));
+  if (h.token == VH_ERR_NONE && h.target == VH_ERR_NONE) return VH_OK;
+  VhErrRecord clean{VH_ERR_NONE, VH_ERR_NONE, 0, 0};
+  VH_HIP(hipMemcpy(g_rt.err, &clean, sizeof clean, hipMemcpyHostToDevice));
+  auto value_of = [](unsigned long long packed) {
+    uint32_t bits = (uint32_t)(packed & 0xFFFFFFFFu);
+    float v;
+    std::memcpy(&v, &bits, 4);
+    return v;
+  };
+  if (h.token != VH_ERR_NONE) {
+    const float v = value_of(h.token);
+    if (!(v >= 0.0f)) return fail(VH_ERR_DEVICE_PANIC, "Token ID cannot be negative: " + fmt_f32(v));
+    return fail(VH_ERR_DEVICE_PANIC, "Token ID " + std::to_string(round_usize(v)) +
+                                         " out of vocabulary bound " + std::to_string(h.token_bound));
+  }
+  const float v = value_of(h.target);
+  if (!(v >= 0.0f)) return fail(VH_ERR_DEVICE_PANIC, "Target class cannot be negative: " + fmt_f32(v));
+  return fail(VH_ERR_DEVICE_PANIC, "Target class " + std::to_string(round_usize(v)) +
+                                       " out of vocab bounds " + std::to_string(h.target_bound));
+}
+
+StridedLayout to_kl(const vh_layout& l) {
+  StridedLayout k{};
+  k.rank = l.rank;
+  for (int i = 0; i < l.rank; ++i) {
+    k.dims[i] = l.dims[i];
+    k.strides[i] = l.strides[i];
+  }
+  return k;
+}
+
+int check_layout(const vh_layout* l, const char* what) {
+  if (!l) return fail(VH_ERR_INVALID, std::string(what) + ": null layout");
+  if (l->rank < 0 || l->rank > VH_MAX_RANK)
+    return fail(VH_ERR_INVALID, std::string(what) + ": rank must be in [0, 8]");
+  for (int i = 0; i < l->rank; ++i)
+    if (l->dims[i] < 0 || l->strides[i] < 0)
+      return fail(VH_ERR_INVALID, std::string(what) + ": negative dim or stride");
+  return VH_OK;
+}
+
+int64_t numel(const vh_layout* l) {
+  int64_t n = 1;
+  for (int i = 0; i < l->rank; ++i) n *= l->dims[i];
+  return n;
+}
+
+bool is_contig(const vh_layout* l) {
+  int64_t acc = 1;
+  for (int i = l->rank - 1; i >= 0; --i) {
+    if (l->dims[i] != 1 && l->strides[i] != acc) return false;
+    acc *= l->dims[i];
+  }
+  return true;
+}
+
+}  // namespace
+
+// ===================================================================== ABI ==
+extern "C" {
+
+int vh_init(int device) {
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  if (g_rt.ready) {
+    if (device != g_rt.device)
+      return fail(VH_ERR_INVALID, "vh_init: already initialised on device " + std::to_string(g_rt.device));
+    return VH_OK;
+  }
+  int count = 0;
+  VH_HIP(hipGetDeviceCount(&count));
+  if (device < 0 || device >= count)
+    return fail(VH_ERR_INVALID, "vh_init: device " + std::to_string(device) + " not present (" +
+                                    std::to_string(count) + " devices)");
+  VH_HIP(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  VH_HIP(hipGetDeviceProperties(&prop, device));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(VH_ERR_UNSUPPORTED, std::string("vh_init: code object is built for gfx950, device is ") +
+                                        prop.gcnArchName);
+  VH_HIP(hipDeviceGetAttribute(&g_rt.cu_count, hipDeviceAttributeMultiprocessorCount, device));
+  VH_HIP(hipStreamCreateWithFlags(&g_rt.stream, hipStreamNonBlocking));
+  VH_HIP(hipModuleLoadData(&g_rt.module, vh_code_object_start));
+  void* e = nullptr;
+  VH_HIP(hipMalloc(&e, sizeof(VhErrRecord)));
+  g_rt.err = static_cast<VhErrRecord*>(e);
+  VhErrRecord clean{VH_ERR_NONE, VH_ERR_NONE, 0, 0};
+  VH_HIP(hipMemcpy(g_rt.err, &clean, sizeof clean, hipMemcpyHostToDevice));
+  g_rt.device = device;
+  g_rt.ready = true;
+  return VH_OK;
+}
+
+int vh_shutdown(void) {
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  if (!g_rt.ready) return VH_OK;
+  VH_HIP(hipStreamSynchronize(g_rt.stream));
+  {
+    std::lock_guard<std::mutex> al(g_arena.mu);
+    VH_TRY(g_arena.release_all_cached());
+    for (auto& kv : g_arena.live) (void)hipFree(kv.first);
+    g_arena.live.clear();
+    g_arena.live_bytes = 0;
+    g_arena.hip_bytes = 0;
+  }
+  VH_HIP(hipFree(g_rt.err));
+  VH_HIP(hipModuleUnload(g_rt.module));
+  VH_HIP(hipStreamDestroy(g_rt.stream));
+  g_rt.fns.clear();
+  g_rt.ready = false;
+  g_rt.device = -1;
+  return VH_OK;
+}
+
+const char* vh_last_error(void) { return g_last_error.c_str(); }
+
+void* vh_stream(void) { return g_rt.stream; }
+
+int vh_device_cu_count(void) { return g_rt.cu_count; }
+
+int vh_sync(void) {
+  VH_TRY(require_init());
+  return check_error_record();
+}
+
+int vh_check_device_error(void) {
+  VH_TRY(require_init());
+  return check_error_record();
+}
+
+int vh_alloc(size_t bytes, int zero, void** out) {
+  VH_TRY(require_init());
+  if (!out) return fail(VH_ERR_INVALID, "vh_alloc: null out");
+  VH_TRY(g_arena.alloc(bytes, out));
+  if (zero) VH_TRY(fill(*out, 0.0f, (int64_t)(Arena::rounded(bytes) / 4), g_rt.stream));
+  return VH_OK;
+}
+
+int vh_free(void* ptr) {
+  if (!ptr) return VH_OK;
+  VH_TRY(require_init());
+  return g_arena.free(ptr);
+}
+
+int vh_h2d(void* dst, const void* src, size_t bytes) {
+  VH_TRY(require_init());
+  if (bytes == 0) return VH_OK;
+  VH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_rt.stream));
+  VH_HIP(hipStreamSynchronize(g_rt.stream));
+  return VH_OK;
+}
+
+int vh_d2h(void* dst, const void* src, size_t bytes) {
+  VH_TRY(require_init());
+  if (bytes == 0) return VH_OK;
+  VH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_rt.stream));
+  VH_HIP(hipStreamSynchronize(g_rt.stream));
+  return VH_OK;
+}
+
+int vh_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+  VH_TRY(require_init());
+  if (bytes == 0) return VH_OK;
+  VH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, S(stream)));
+  return VH_OK;
+}
+
+int vh_fill_f32(float* out, float value, int64_t n, void* stream) {
+  VH_TRY(require_init());
+  if (n < 0 || (n > 0 && !out)) return fail(VH_ERR_INVALID, "vh_fill_f32: bad arguments");
+  return fill(out, value, n, S(stream));
+}
+
+int vh_mem_stats_get(vh_mem_stats* out) {
+  if (!out) return fail(VH_ERR_INVALID, "vh_mem_stats_get: null out");
+  std::lock_guard<std::mutex> lk(g_arena.mu);
+  out->live_bytes = g_arena.live_bytes;
+  out->cached_bytes = g_arena.cached_bytes;
+  out->peak_bytes = g_arena.peak_bytes;
+  out->hip_bytes = g_arena.hip_bytes;
+  return VH_OK;
+}
+
+int vh_empty_cache(void) {
+  VH_TRY(require_init());
+  VH_HIP(hipStreamSynchronize(g_rt.stream));
+  std::lock_guard<std::mutex> lk(g_arena.mu);
+  return g_arena.release_all_cached();
+}
+
+// ------------------------------------------------------------- layernorm --
+
+int vh_layernorm_fwd(const float* x, const float* w, const float* b, float* y, int64_t rows,
+                     int64_t C, float eps, void* stream) {
+  VH_TRY(require_init());
+  if (rows < 0 || C < 0) return fail(VH_ERR_INVALID, "vh_layernorm_fwd: negative size");
+  if (rows == 0 || C == 0) return VH_OK;
+  if (!x || !w || !b || !y) return fail(VH_ERR_INVALID, "vh_layernorm_fwd: null pointer");
+  if (C > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_fwd: C too large");
+  RowCfg c;
+  const bool vec = aligned16(x) && aligned16(w) && aligned16(b) && aligned16(y);
+  if (!pick_row_cfg(C, vec, 16, &c))
+    return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_fwd: C=" + std::to_string(C) + " exceeds 65536");
+  const int bs = block_of(c);
+  const int64_t rpb = bs / c.team;
+  LnFwdArgs a{x, w, b, y, rows, (int32_t)C, eps};
+  return launch(row_kernel("vh_ln_fwd", c), (unsigned)cdiv(rows, rpb), 1, bs, 0, S(stream), a);
+}
+
+size_t vh_layernorm_bwd_scratch_bytes(int64_t rows, int64_t C) {
+  // The largest need over the vector and scalar configurations (the one used
+  // depends on operand alignment).
+  if (rows <= 0 || C <= 0) return 0;
+  size_t need = 0;
+  for (bool vec : {true, false}) {
+    RowCfg c;
+    if (pick_row_cfg(C, vec, 8, &c))
+      need = std::max(need, align256((size_t)ln_bwd_blocks(rows, c) * 2 * (size_t)C * sizeof(float)));
+  }
+  return need;
+}
+
+int vh_layernorm_bwd(const float* x, const float* w, const float* dy, float* dx, float* dw,
+                     float* db, int64_t rows, int64_t C, float eps, void* scratch,
+                     size_t scratch_bytes, void* stream) {
+  VH_TRY(require_init());
+  if (rows < 0 || C < 0) return fail(VH_ERR_INVALID, "vh_layernorm_bwd: negative size");
+  hipStream_t s = S(stream);
+  if (C == 0) return VH_OK;
+  if (!dw || !db) return fail(VH_ERR_INVALID, "vh_layernorm_bwd: null pointer");
+  if (rows == 0) {  // reference returns zero gradients (cpu:752-758)
+    VH_TRY(fill(dw, 0.0f, C, s));
+    return fill(db, 0.0f, C, s);
+  }
+  if (!x || !w || !dy || !dx) return fail(VH_ERR_INVALID, "vh_layernorm_bwd: null pointer");
+  RowCfg c;
+  const bool vec = aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx);
+  if (!pick_row_cfg(C, vec, 8, &c))
+    return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_bwd: C=" + std::to_string(C) + " exceeds 32768");
+  const int64_t G = ln_bwd_blocks(rows, c);
+  const size_t need = align256((size_t)G * 2 * (size_t)C * sizeof(float));
+  Scratch sc;
+  VH_TRY(sc.get(scratch, scratch_bytes, need));
+  const int bs = block_of(c);
+  const int groups = bs / c.team;
+  const unsigned shmem = groups > 1 ? (unsigned)((groups / 2) * 2 * C * sizeof(float)) : 0;
+  if (shmem > 64 * 1024) return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_bwd: LDS budget exceeded");
+  const int64_t rpb = cdiv(rows, G);
+  LnBwdArgs a{x, w, dy, dx, static_cast<float*>(sc.p), rows, rpb, (int32_t)C, eps};
+  VH_TRY(launch(row_kernel("vh_ln_bwd", c), (unsigned)G, 1, bs, shmem, s, a));
+  ColReduceArgs r{static_cast<float*>(sc.p), dw, db, (int32_t)G, (int32_t)C, 2};
+  return launch("vh_col_reduce", (unsigned)cdiv(C, 64), 2, 1024, 0, s, r);
+}
+
+// ------------------------------------------------------------------ gelu --
+
+static int gelu_flat(const char* base, const float* x, const float* dy, float* y, int64_t n,
+                     hipStream_t s) {
+  const bool vec = n % 4 == 0 && aligned16(x) && aligned16(y) && (!dy || aligned16(dy));
+  const int vw = vec ? 4 : 1;
+  EltArgs a{x, nullptr, dy, y, n, 0};
+  const int64_t blocks = std::min<int64_t>(cdiv(n / vw, 256), 16384);
+  return launch(std::string(base) + (vec ? "_v4" : "_v1"), (unsigned)blocks, 1, 256, 0, s, a);
+}
+
+int vh_gelu_fwd(const float* x, float* y, int64_t n, void* stream) {
+  VH_TRY(require_init());
+  if (n < 0) return fail(VH_ERR_INVALID, "vh_gelu_fwd: negative size");
+  if (n == 0) return VH_OK;
+  if (!x || !y) return fail(VH_ERR_INVALID, "vh_gelu_fwd: null pointer");
+  return gelu_flat("vh_gelu_fwd", x, nullptr, y, n, S(stream));
+}
+
+int vh_gelu_grad_mul(const float* x, const float* dy, float* dx, int64_t n, void* stream) {
+  VH_TRY(require_init());
+  if (n < 0) return fail(VH_ERR_INVALID, "vh_gelu_grad_mul: negative size");
+  if (n == 0) return VH_OK;
+  if (!x || !dy || !dx) return fail(VH_ERR_INVALID, "vh_gelu_grad_mul: null pointer");
+  return gelu_flat("vh_gelu_gradmul", x, dy, dx, n, S(stream));
+}
+
+static bool gb_cfg(int64_t C, bool vec, int* nv, int* vw) {
+  *vw = (vec && C % 4 == 0) ? 4 : 1;
+  *nv = pick_nv(cdiv(C / *vw, 256), 16);
+  return *nv > 0;
+}
+
+int vh_gelu_bias_fwd(const float* x, const float* bias, float* y, int64_t rows, int64_t C,
+                     void* stream) {
+  VH_TRY(require_init());
+  if (rows < 0 || C < 0) return fail(VH_ERR_INVALID, "vh_gelu_bias_fwd: negative size");
+  if (rows == 0 || C == 0) return VH_OK;
+  if (!x || !bias || !y) return fail(VH_ERR_INVALID, "vh_gelu_bias_fwd: null pointer");
+  int nv, vw;
+  if (!gb_cfg(C, aligned16(x) && aligned16(bias) && aligned16(y), &nv, &vw))
+    return fail(VH_ERR_UNSUPPORTED, "vh_gelu_bias_fwd: C too large");
+  const int64_t G = std::max<int64_t>(1, std::min<int64_t>(rows, 4096));
+  const int64_t rpb = cdiv(rows, G);
+  GeluBiasBwdArgs a{x, bias, nullptr, y, nullptr, rows, rpb, (int32_t)C};
+  return launch("vh_gelu_bias_fwd_n" + std::to_string(nv) + "_v" + std::to_string(vw),
+                (unsigned)cdiv(rows, rpb), 1, 256, 0, S(stream), a);
+}
+
+size_t vh_gelu_bias_bwd_scratch_bytes(int64_t rows, int64_t C) {
+  if (rows <= 0 || C <= 0) return 0;
+  return align256((size_t)gb_blocks(rows) * (size_t)C * sizeof(float));
+}
+
+int vh_gelu_bias_bwd(const float* x, const float* bias, const float* dy, float* dx, float* dbias,
+                     int64_t rows, int64_t C, void* scratch, size_t scratch_bytes, void* stream) {
+  VH_TRY(require_init());
+  if (rows < 0 || C < 0) return fail(VH_ERR_INVALID, "vh_gelu_bias_bwd: negative size");
+  hipStream_t s = S(stream);
+  if (C == 0) return VH_OK;
+  if (!dbias) return fail(VH_ERR_INVALID, "vh_gelu_bias_bwd: null pointer");
+  if (rows == 0) return fill(dbias, 0.0f, C, s);
+  if (!x || !bias || !dy || !dx) return fail(VH_ERR_INVALID, "vh_gelu_bias_bwd: null pointer");
+  int nv, vw;
+  if (!gb_cfg(C, aligned16(x) && aligned16(bias) && aligned16(dy) && aligned16(dx), &nv, &vw))
+    return fail(VH_ERR_UNSUPPORTED, "vh_gelu_bias_bwd: C too large");
+  const int64_t G0 = gb_blocks(rows);
+  const int64_t rpb = cdiv(rows, G0);
+  const int64_t G = cdiv(rows, rpb);
+  Scratch sc;
+  VH_TRY(sc.get(scratch, scratch_bytes, align256((size_t)G0 * (size_t)C * sizeof(float))));
+  GeluBiasBwdArgs a{x, bias, dy, dx, static_cast<float*>(sc.p), rows, rpb, (int32_t)C};
+  VH_TRY(launch("vh_gelu_bias_bwd_n" + std::to_string(nv) + "_v" + std::to_string(vw),
+                (unsigned)G, 1, 256, 0, s, a));
+  ColReduceArgs r{static_cast<float*>(sc.p), dbias, nullptr, (int32_t)G, (int32_t)C, 1};
+  return launch("vh_col_reduce", (unsigned)cdiv(C, 64), 1, 1024, 0, s, r);
+}
+
+// --------------------------------------------------------------- softmax --
+
+static int softmax_common(const char* base, int cap, const float* in, const float* dy, float* out,
+                          int64_t rows, int64_t T, int causal, int input_is_x, hipStream_t s) {
+  RowCfg c;
+  const bool vec = aligned16(in) && aligned16(out) && (!dy || aligned16(dy));
+  if (!pick_row_cfg(T, vec, cap, &c))
+    return fail(VH_ERR_UNSUPPORTED, std::string(base) + ": T=" + std::to_string(T) + " too large");
+  const int bs = block_of(c);
+  const int64_t rpb = bs / c.team;
+  SoftmaxArgs a{in, dy, out, rows, (int32_t)T, causal ? 1 : 0, input_is_x ? 1 : 0};
+  return launch(row_kernel(base, c), (unsigned)cdiv(rows, rpb), 1, bs, 0, s, a);
+}
+
+int vh_softmax_fwd(const float* x, float* y, int64_t rows, int64_t T, int causal, void* stream) {
+  VH_TRY(require_init());
+  if (rows < 0 || T < 0) return fail(VH_ERR_INVALID, "vh_softmax_fwd: negative size");
+  if (rows == 0 || T == 0) return VH_OK;
+  if (!x || !y) return fail(VH_ERR_INVALID, "vh_softmax_fwd: null pointer");
+  if (T > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_softmax_fwd: T too large");
+  return softmax_common("vh_sm_fwd", 16, x, nullptr, y, rows, T, causal, 0, S(stream));
+}
+
+int vh_softmax_bwd(const float* in, const float* dy, float* dx, int64_t rows, int64_t T,
+                   int input_is_x, int causal, void* stream) {
+  VH_TRY(require_init());
+  if (rows < 0 || T < 0) return fail(VH_ERR_INVALID, "vh_softmax_bwd: negative size");
+  if (rows == 0 || T == 0) return VH_OK;
+  if (!in || !dy || !dx) return fail(VH_ERR_INVALID, "vh_softmax_bwd: null pointer");
+  if (T > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_softmax_bwd: T too large");
+  return softmax_common("vh_sm_bwd", 8, in, dy, dx, rows, T, causal, input_is_x, S(stream));
+}
+
+// ------------------------------------------------------------- embedding --
+
+int vh_embedding_fwd(const float* ids, const float* W, float* out, int64_t n, int64_t V, int64_t D,
+                     void* stream) {
+  VH_TRY(require_init());
+  if (n < 0 || V < 0 || D < 0) return fail(VH_ERR_INVALID, "vh_embedding_fwd: negative size");
+  if (n == 0) return VH_OK;
+  // D == 0 still launches: the ids are validated as the reference does.
+  if (!ids || (D > 0 && !out) || (V > 0 && D > 0 && !W))
+    return fail(VH_ERR_INVALID, "vh_embedding_fwd: null pointer");
+  if (V > INT32_MAX || D > INT32_MAX || n > INT32_MAX)
+    return fail(VH_ERR_UNSUPPORTED, "vh_embedding_fwd: size exceeds int32");
+  const bool vec = D % 4 == 0 && aligned16(W) && aligned16(out);
+  EmbFwdArgs a{ids, W, out, g_rt.err, n, (int32_t)V, (int32_t)D};
+  return launch(vec ? "vh_emb_fwd_v4" : "vh_emb_fwd_v1", (unsigned)cdiv(n, 4), 1, 256, 0, S(stream), a);
+}
+
+namespace {
+struct EmbScratchLayout {
+  size_t tok, counts, cursor, pos, gbuf, big, nbig, total;
+};
+EmbScratchLayout emb_layout(int64_t n, int64_t V) {
+  EmbScratchLayout L;
+  size_t o = 0;
+  auto take = [&](size_t ints) {
+    size_t at = o;
+    o += align256(ints * sizeof(int32_t));
+    return at;
+  };
+  L.tok = take((size_t)n);
+  L.counts = take((size_t)V + 1);
+  L.cursor = take((size_t)V);
+  L.nbig = take(1);
+  L.pos = take((size_t)n);
+  L.gbuf = take(2 * (size_t)n);
+  L.big = take((size_t)V);
+  L.total = o;
+  return L;
+}
+}  // namespace
+
+size_t vh_embedding_bwd_scratch_bytes(int64_t n, int64_t V) {
+  if (n <= 0 || V < 0) return 0;
+  return emb_layout(n, V).total;
+}
+
+int vh_embedding_bwd(const float* ids, const float* dy, float* dW, int64_t n, int64_t V, int64_t D,
+                     void* scratch, size_t scratch_bytes, void* stream) {
+  VH_TRY(require_init());
+  if (n < 0 || V < 0 || D < 0) return fail(VH_ERR_INVALID, "vh_embedding_bwd: negative size");
+  hipStream_t s = S(stream);
+  if (V * D > 0 && !dW) return fail(VH_ERR_INVALID, "vh_embedding_bwd: null pointer");
+  if (n == 0) return fill(dW, 0.0f, V * D, s);
+  if (!ids || (D > 0 && !dy)) return fail(VH_ERR_INVALID, "vh_embedding_bwd: null pointer");
+  if (V >= INT32_MAX || D > INT32_MAX || n >= INT32_MAX / 2)
+    return fail(VH_ERR_UNSUPPORTED, "vh_embedding_bwd: size exceeds int32");
+  const EmbScratchLayout L = emb_layout(n, V);
+  Scratch sc;
+  VH_TRY(sc.get(scratch, scratch_bytes, L.total));
+  char* base = static_cast<char*>(sc.p);
+  int32_t* tok = reinterpret_cast<int32_t*>(base + L.tok);
+  int32_t* counts = reinterpret_cast<int32_t*>(base + L.counts);
+  int32_t* cursor = reinterpret_cast<int32_t*>(base + L.cursor);
+  int32_t* nbig = reinterpret_cast<int32_t*>(base + L.nbig);
+  int32_t* pos = reinterpret_cast<int32_t*>(base + L.pos);
+  int32_t* gbuf = reinterpret_cast<int32_t*>(base + L.gbuf);
+  int32_t* big = reinterpret_cast<int32_t*>(base + L.big);
+  // counts, cursor and nbig are contiguous: one fill of zeros (0.0f bits == int 0).
+  VH_TRY(fill(counts, 0.0f, (int64_t)((L.pos - L.counts) / 4), s));
+  EmbTokArgs k1{ids, tok, counts, g_rt.err, n, (int32_t)V};
+  VH_TRY(launch("vh_emb_tokens", (unsigned)cdiv(n, 256), 1, 256, 0, s, k1));
+  if (V == 0 || D == 0) return VH_OK;  // ids validated, nothing to write
+  ScanArgs k2{counts, big, nbig, (int32_t)V};
+  VH_TRY(launch("vh_scan", 1, 1, 1024, 0, s, k2));
+  EmbPlaceArgs k3{tok, counts, cursor, pos, n};
+  VH_TRY(launch("vh_emb_place", (unsigned)cdiv(n, 256), 1, 256, 0, s, k3));
+  EmbSortArgs k4{counts, pos, gbuf, big, nbig};
+  VH_TRY(launch("vh_emb_sort_big", 64, 1, 256, 0, s, k4));
+  const bool vec = D % 4 == 0 && aligned16(dy) && aligned16(dW);
+  EmbSegArgs k5{counts, pos, dy, dW, (int32_t)V, (int32_t)D};
+  return launch(vec ? "vh_emb_segsum_v4" : "vh_emb_segsum_v1", (unsigned)cdiv(V, 4), 1, 256, 0, s, k5);
+}
+
+// --------------------------------------------------------- cross-entropy --
+
+static const int kXE[] = {1, 2, 4, 8, 16, 24, 32, 40, 48, 50, 56, 64};
+
+static std::string xent_kernel(const char* dir, int64_t V) {
+  const int64_t need = cdiv(V, 1024);
+  for (int v : kXE)
+    if (v >= need) return std::string("vh_xent_") + dir + "_n" + std::to_string(v);
+  return std::string("vh_xent_") + dir + "_stream";
+}
+
+size_t vh_cross_entropy_fwd_scratch_bytes(int64_t B) {
+  return B <= 0 ? 0 : align256((size_t)B * sizeof(float));
+}
+
+int vh_cross_entropy_fwd(const float* logits, const float* targets, float* loss, int64_t B,
+                         int64_t V, void* scratch, size_t scratch_bytes, void* stream) {
+  VH_TRY(require_init());
+  if (B <= 0) return fail(VH_ERR_INVALID, "Batch size must be greater than 0");
+  if (V <= 0) return fail(VH_ERR_INVALID, "vh_cross_entropy_fwd: vocabulary must be > 0");
+  if (!logits || !targets || !loss) return fail(VH_ERR_INVALID, "vh_cross_entropy_fwd: null pointer");
+  if (V > INT32_MAX || B > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_cross_entropy_fwd: size exceeds int32");
+  hipStream_t s = S(stream);
+  Scratch sc;
+  VH_TRY(sc.get(scratch, scratch_bytes, vh_cross_entropy_fwd_scratch_bytes(B)));
+  XentArgs a{logits, targets, nullptr, static_cast<float*>(sc.p), g_rt.err, B, (int32_t)V};
+  VH_TRY(launch(xent_kernel("fwd", V), (unsigned)B, 1, 1024, 0, s, a));
+  XentReduceArgs r{static_cast<float*>(sc.p), loss, B};
+  return launch("vh_xent_reduce", 1, 1, 1024, 0, s, r);
+}
+
+int vh_cross_entropy_bwd(const float* logits, const float* targets, const float* grad_out,
+                         float* dlogits, int64_t B, int64_t V, void* stream) {
+  VH_TRY(require_init());
+  if (B <= 0) return fail(VH_ERR_INVALID, "Batch size must be greater than 0");
+  if (V <= 0) return fail(VH_ERR_INVALID, "vh_cross_entropy_bwd: vocabulary must be > 0");
+  if (!logits || !targets || !grad_out || !dlogits)
+    return fail(VH_ERR_INVALID, "vh_cross_entropy_bwd: null pointer");
+  if (V > INT32_MAX || B > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_cross_entropy_bwd: size exceeds int32");
+  XentArgs a{logits, targets, grad_out, dlogits, g_rt.err, B, (int32_t)V};
+  return launch(xent_kernel("bwd", V), (unsigned)B, 1, 1024, 0, S(stream), a);
+}
+
+// ------------------------------------------------------------ composites --
+
+int vh_binary(int op, const float* l, const vh_layout* ll, const float* r, const vh_layout* rl,
+              float* out, void* stream) {
+  VH_TRY(require_init());
+  if (op < 0 || op > 3) return fail(VH_ERR_INVALID, "vh_binary: unknown op");
+  VH_TRY(check_layout(ll, "vh_binary lhs"));
+  VH_TRY(check_layout(rl, "vh_binary rhs"));
+  const int R = std::max(ll->rank, rl->rank);
+  StridedLayout ol{}, lk{}, rk{};
+  ol.rank = lk.rank = rk.rank = R;
+  for (int i = 0; i < R; ++i) {
+    const int li = ll->rank - R + i, ri = rl->rank - R + i;
+    const int64_t ld = li >= 0 ? ll->dims[li] : 1, rd = ri >= 0 ? rl->dims[ri] : 1;
+    int64_t od;
+    if (ld == rd) od = ld;
+    else if (ld == 1) od = rd;
+    else if (rd == 1) od = ld;
+    else return fail(VH_ERR_INVALID, "Shapes are not broadcastable");
+    ol.dims[i] = od;
+    lk.dims[i] = rk.dims[i] = od;
+    lk.strides[i] = (li >= 0 && ll->dims[li] != 1) ? ll->strides[li] : 0;
+    rk.strides[i] = (ri >= 0 && rl->dims[ri] != 1) ? rl->strides[ri] : 0;
+  }
+  int64_t n = 1;
+  for (int i = 0; i < R; ++i) n *= ol.dims[i];
+  if (n == 0) return VH_OK;
+  if (!l || !r || !out) return fail(VH_ERR_INVALID, "vh_binary: null pointer");
+  bool same = ll->rank == rl->rank;
+  for (int i = 0; same && i < ll->rank; ++i) same = ll->dims[i] == rl->dims[i];
+  BinaryArgs a{l, r, out, ol, lk, rk, n, op, 0};
+  hipStream_t s = S(stream);
+  if (same && is_contig(ll) && is_contig(rl)) {
+    const bool vec = n % 4 == 0 && aligned16(l) && aligned16(r) && aligned16(out);
+    const int64_t blocks = std::min<int64_t>(cdiv(n / (vec ? 4 : 1), 256), 16384);
+    return launch(vec ? "vh_binary_contig_v4" : "vh_binary_contig_v1", (unsigned)blocks, 1, 256, 0, s, a);
+  }
+  const int64_t blocks = std::min<int64_t>(cdiv(n, 256), 16384);
+  return launch(n < INT32_MAX ? "vh_binary_strided_i32" : "vh_binary_strided_i64", (unsigned)blocks, 1,
+                256, 0, s, a);
+}
+
+int vh_reduce(int mean, const float* x, const vh_layout* xl, int dim, float* out, void* stream) {
+  VH_TRY(require_init());
+  VH_TRY(check_layout(xl, "vh_reduce"));
+  if (dim < 0 || dim >= xl->rank) return fail(VH_ERR_INVALID, "Reduction dim out of range");
+  StridedLayout ol{};
+  ol.rank = xl->rank - 1;
+  int64_t n_out = 1;
+  for (int i = 0, j = 0; i < xl->rank; ++i) {
+    if (i == dim) continue;
+    ol.dims[j] = xl->dims[i];
+    ol.strides[j] = xl->strides[i];
+    n_out *= xl->dims[i];
+    ++j;
+  }
+  if (n_out == 0) return VH_OK;
+  if (!x || !out) return fail(VH_ERR_INVALID, "vh_reduce: null pointer");
+  const int64_t red_len = xl->dims[dim];
+  const int64_t red_stride = xl->strides[dim];
+  ReduceArgs a{x, out, ol, n_out, red_len, red_stride, mean ? 1 : 0};
+  hipStream_t s = S(stream);
+  if ((red_stride == 1 || red_len == 1) && red_len >= 128)
+    return launch("vh_reduce_wave", (unsigned)cdiv(n_out, 4), 1, 256, 0, s, a);
+  const int64_t blocks = std::min<int64_t>(cdiv(n_out, 256), 16384);
+  return launch("vh_reduce_thread", (unsigned)blocks, 1, 256, 0, s, a);
+}
+
+int vh_strided_copy(const float* src, const vh_layout* sl, float* dst, void* stream) {
+  VH_TRY(require_init());
+  VH_TRY(check_layout(sl, "vh_strided_copy"));
+  const int64_t n = numel(sl);
+  if (n == 0) return VH_OK;
+  if (!src || !dst) return fail(VH_ERR_INVALID, "vh_strided_copy: null pointer");
+  hipStream_t s = S(stream);
+  if (is_contig(sl)) {
+    VH_HIP(hipMemcpyAsync(dst, src, (size_t)n * sizeof(float), hipMemcpyDeviceToDevice, s));
+    return VH_OK;
+  }
+  CopyArgs a{src, dst, to_kl(*sl), n};
+  const int64_t blocks = std::min<int64_t>(cdiv(n, 256), 16384);
+  return launch(n < INT32_MAX ? "vh_strided_copy_i32" : "vh_strided_copy_i64", (unsigned)blocks, 1, 256, 0,
+                s, a);
+}
+
+}  // extern "C"

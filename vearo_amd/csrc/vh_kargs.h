@@ -1,0 +1,192 @@
+// vh_kargs.h -- kernel argument blocks shared by the host runtime and the gfx950
+// code object. Every kernel takes exactly one of these structs by value, so the
+// host (hipModuleLaunchKernel with a one-element kernelParams array) and the
+// device always agree on the parameter layout.
+#pragma once
+#include <stdint.h>
+
+#define VH_MAX_RANK 8
+
+// Device-side error record (one per device, zeroed at init). Kernels that meet an
+// input the CPU backend would panic on fold (index << 32 | value bits) into the
+// record with an atomic min, so the host reports the FIRST offending element in
+// row-major order, as the CPU's sequential loop does.
+struct VhErrRecord {
+  unsigned long long token;   // embedding fwd/bwd: bad token id
+  unsigned long long target;  // cross-entropy fwd/bwd: bad target class
+  unsigned int token_bound;   // vocabulary size of the failing embedding launch
+  unsigned int target_bound;  // vocabulary size of the failing cross-entropy launch
+};
+#define VH_ERR_NONE 0xFFFFFFFFFFFFFFFFull
+
+struct LnFwdArgs {
+  const float* x;
+  const float* w;
+  const float* b;
+  float* y;
+  int64_t rows;
+  int32_t C;
+  float eps;
+};
+
+struct LnBwdArgs {
+  const float* x;
+  const float* w;
+  const float* dy;
+  float* dx;
+  float* part;  // [nblocks][2][C] per-block dgamma / dbeta partials
+  int64_t rows;
+  int64_t rows_per_block;
+  int32_t C;
+  float eps;
+};
+
+// Column reduction of [P][2][C] partials into dw[C], db[C] (fixed order).
+struct ColReduceArgs {
+  const float* part;
+  float* out0;  // component 0 (dgamma / dbias)
+  float* out1;  // component 1 (dbeta); unused when ncomp == 1
+  int32_t P;
+  int32_t C;
+  int32_t ncomp;
+};
+
+struct SoftmaxArgs {
+  const float* x;   // fwd: scores; bwd: y (or x when input_is_x)
+  const float* dy;  // bwd only
+  float* y;         // fwd: probabilities; bwd: dx
+  int64_t rows;
+  int32_t T;        // row length
+  int32_t causal;   // 1: row r keeps columns [0, r % T], the rest are known masked
+  int32_t input_is_x;
+};
+
+struct EltArgs {
+  const float* x;
+  const float* bias;  // [C] or null
+  const float* dy;
+  float* y;
+  int64_t n;
+  int32_t C;          // bias period (row length) when bias != null
+};
+
+struct GeluBiasBwdArgs {
+  const float* x;
+  const float* bias;
+  const float* dy;
+  float* dx;
+  float* part;  // [nblocks][C] dbias partials
+  int64_t rows;
+  int64_t rows_per_block;
+  int32_t C;
+};
+
+struct EmbFwdArgs {
+  const float* ids;
+  const float* W;
+  float* out;
+  VhErrRecord* err;
+  int64_t n;
+  int32_t V;
+  int32_t D;
+};
+
+// Embedding backward: sort-by-token CSR build + segmented gather-sum.
+struct EmbTokArgs {
+  const float* ids;
+  int32_t* tok;      // [n] validated token ids (-1 on error)
+  int32_t* counts;   // [V + 1] histogram, later exclusive offsets
+  VhErrRecord* err;
+  int64_t n;
+  int32_t V;
+};
+
+struct ScanArgs {
+  int32_t* data;  // in-place exclusive scan of [n] int32, total written to data[n]
+  int32_t* big;   // optional: receives the indices whose count exceeds 64
+  int32_t* nbig;  // optional: number of entries written to big (zeroed by the host)
+  int32_t n;
+};
+
+struct EmbPlaceArgs {
+  const int32_t* tok;
+  const int32_t* offsets;  // [V + 1]
+  int32_t* cursor;         // [V] zeroed
+  int32_t* pos;            // [n] positions grouped by token
+  int64_t n;
+};
+
+struct EmbSortArgs {
+  const int32_t* offsets;  // [V + 1]
+  int32_t* pos;            // [n] grouped by token
+  int32_t* gbuf;           // [2n] staging for segments too long for LDS
+  const int32_t* big;      // long segments listed by the scan
+  const int32_t* nbig;
+};
+
+struct EmbSegArgs {
+  const int32_t* offsets;  // [V + 1]
+  const int32_t* pos;      // [n] grouped by token (unordered within a group)
+  const float* dy;
+  float* dW;
+  int32_t V;
+  int32_t D;
+};
+
+struct XentArgs {
+  const float* logits;
+  const float* targets;
+  const float* grad_out;  // bwd: device scalar
+  float* out;             // fwd: per-row losses [B]; bwd: dlogits [B, V]
+  VhErrRecord* err;
+  int64_t B;
+  int32_t V;
+};
+
+struct XentReduceArgs {
+  const float* row_loss;  // [B]
+  float* loss;            // [1]
+  int64_t B;
+};
+
+struct StridedLayout {
+  int32_t rank;
+  int32_t pad;
+  int64_t dims[VH_MAX_RANK];
+  int64_t strides[VH_MAX_RANK];
+};
+
+struct BinaryArgs {
+  const float* l;
+  const float* r;
+  float* out;
+  StridedLayout ol;  // output dims, contiguous strides
+  StridedLayout ll;  // lhs strides aligned to the output rank (0 for broadcast dims)
+  StridedLayout rl;  // rhs strides aligned to the output rank
+  int64_t n;
+  int32_t op;        // 0 add, 1 sub, 2 mul, 3 div
+  int32_t contiguous;
+};
+
+struct ReduceArgs {
+  const float* x;
+  float* out;
+  StridedLayout ol;  // outer (kept) dims with input strides, dim removed
+  int64_t n_out;
+  int64_t red_len;
+  int64_t red_stride;
+  int32_t mean;
+};
+
+struct CopyArgs {
+  const float* src;
+  float* dst;
+  StridedLayout sl;  // dims + source strides
+  int64_t n;
+};
+
+struct FillArgs {
+  float* p;
+  int64_t n;
+  float value;
+};
