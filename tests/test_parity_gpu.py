@@ -75,7 +75,7 @@ def test_layernorm_explicit_scratch_and_errors(vh):
     DX, DW, DB = out(vh, (rows, C)), out(vh, (C,)), out(vh, (C,))
     S = vh.DeviceBuffer(need)
     rc = vh.lib.vh_layernorm_bwd(X.ptr, W.ptr, DY.ptr, DX.ptr, DW.ptr, DB.ptr, rows, C, 1e-5, S.ptr,
-                                 need - 256, None)
+                                 256, None)
     assert rc == vh.VH_ERR_INVALID and "scratch buffer too small" in vh.last_error()
     vh.check(vh.lib.vh_layernorm_bwd(X.ptr, W.ptr, DY.ptr, DX.ptr, DW.ptr, DB.ptr, rows, C, 1e-5,
                                      S.ptr, need, None))
