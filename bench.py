@@ -3,7 +3,7 @@
 A step is one pass of the path over one synthetic batch at GPT-2-small shape:
   layernorm forward    x [16384, 768]                 (cfg[4] shape; cfg[0'] in SURVEY)
   causal softmax fwd   scores [16, 12, 1024, 1024]    (cfg[2])
-  causal softmax bwd   (from y, dy)
+  causal softmax bwd   (from the saved input x and dy, as the autograd arm)
   layernorm backward   (x, w, dy -> dx, dgamma, dbeta)
 issued in that order on the runtime stream, as a training step meets them
 (forward, then backward in reverse). Inputs are resident in HBM before timing;
@@ -49,7 +49,7 @@ def sm_bytes(B, H, T):
     live = B * H * T * (T + 1) // 2       # causal lower triangle incl. diagonal
     n = rows * T
     fwd = 4 * live + 4 * n                # R live x, W all y
-    bwd = 4 * live * 2 + 4 * n            # R live y, R live dy, W all dx
+    bwd = 4 * live * 2 + 4 * n            # R live x (or y), R live dy, W all dx
     return fwd, bwd
 
 
@@ -167,7 +167,9 @@ def main():
         L = ln_sets[i % 2]
         yield lambda: vh.lib.vh_layernorm_fwd(L["x"].ptr, W.ptr, Bi.ptr, L["y"].ptr, LN_ROWS, LN_C, 1e-5, None)
         yield lambda: vh.lib.vh_softmax_fwd(S.ptr, P.ptr, rows_sm, SM_T, 1, None)
-        yield lambda: vh.lib.vh_softmax_bwd(P.ptr, G.ptr, DS.ptr, rows_sm, SM_T, 0, 1, None)
+        # The autograd Softmax arm saves the input x and recomputes y from it
+        # (crates/vearo-autograd/src/lib.rs:547-553); the fused kernel does the same.
+        yield lambda: vh.lib.vh_softmax_bwd(S.ptr, G.ptr, DS.ptr, rows_sm, SM_T, 1, 1, None)
         yield lambda: vh.lib.vh_layernorm_bwd(L["x"].ptr, W.ptr, L["dy"].ptr, L["dx"].ptr, L["dw"].ptr,
                                               L["db"].ptr, LN_ROWS, LN_C, 1e-5, LNS.ptr, ln_scratch_bytes, None)
 

@@ -89,11 +89,17 @@ def launcher_kernel_names():
     cfgs_all = [(16, 1), (32, 1)] + [(64, v) for v in nv] + [(1024, v) for v in nv]
     cfgs_small = [(t, v) for t, v in cfgs_all if v <= 8]
     names = set()
+    multi = [(16, 1), (32, 1), (64, 1), (64, 2), (64, 3), (64, 4)]
     for vw in (1, 4):
         for t, v in cfgs_all:
-            names |= {f"vh_ln_fwd_t{t}_n{v}_v{vw}", f"vh_sm_fwd_t{t}_n{v}_v{vw}"}
+            names |= {f"vh_ln_fwd_t{t}_n{v}_v{vw}_r1", f"vh_sm_fwd_t{t}_n{v}_v{vw}_r1"}
         for t, v in cfgs_small:
-            names |= {f"vh_ln_bwd_t{t}_n{v}_v{vw}", f"vh_sm_bwd_t{t}_n{v}_v{vw}"}
+            names |= {f"vh_ln_bwd_t{t}_n{v}_v{vw}_b{max(t, 256)}", f"vh_sm_bwd_t{t}_n{v}_v{vw}_r1"}
+        for t, v in multi:
+            names |= {f"vh_ln_fwd_t{t}_n{v}_v{vw}_r2", f"vh_ln_fwd_t{t}_n{v}_v{vw}_r4",
+                      f"vh_sm_fwd_t{t}_n{v}_v{vw}_r2", f"vh_sm_bwd_t{t}_n{v}_v{vw}_r2"}
+        for v in (1, 2, 3, 4):
+            names.add(f"vh_ln_bwd_t64_n{v}_v{vw}_b1024")
         for v in nv:
             names |= {f"vh_gelu_bias_fwd_n{v}_v{vw}", f"vh_gelu_bias_bwd_n{v}_v{vw}"}
         names |= {f"vh_gelu_fwd_v{vw}", f"vh_gelu_gradmul_v{vw}", f"vh_emb_fwd_v{vw}",

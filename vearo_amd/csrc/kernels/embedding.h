@@ -35,11 +35,11 @@ VH_DEV void emb_fwd_impl(const EmbFwdArgs& a) {
       atomicMin(&a.err->token, err_pack(i, tv));
       a.err->token_bound = (unsigned)a.V;
     }
-    for (int u = lane; u < U; u += 64) store_unit<VW>(o + u * VW, zero_unit<VW>());
+    for (int u = lane; u < U; u += 64) store_stream<VW>(o + u * VW, zero_unit<VW>());
     return;
   }
   const float* w = a.W + (int64_t)t * a.D;
-  for (int u = lane; u < U; u += 64) store_unit<VW>(o + u * VW, load_unit<VW>(w + u * VW));
+  for (int u = lane; u < U; u += 64) store_stream<VW>(o + u * VW, load_unit<VW>(w + u * VW));
 }
 
 VH_DEV void emb_tokens_impl(const EmbTokArgs& a) {
@@ -185,7 +185,7 @@ VH_DEV void emb_segsum_impl(const EmbSegArgs& a) {
       for (int q = 0; q < 4; ++q) {
         const int u = u0 + lane + q * 64;
         if (u < U) {
-          const Unit<VW> d = load_unit<VW>(src + u * VW);
+          const Unit<VW> d = load_stream<VW>(src + u * VW);
 #pragma unroll
           for (int j = 0; j < VW; ++j) acc[q].v[j] += d.v[j];
         }
@@ -194,7 +194,7 @@ VH_DEV void emb_segsum_impl(const EmbSegArgs& a) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int u = u0 + lane + q * 64;
-      if (u < U) store_unit<VW>(o + u * VW, acc[q]);
+      if (u < U) store_stream<VW>(o + u * VW, acc[q]);
     }
   }
 }

@@ -38,17 +38,17 @@ VH_DEV void gelu_flat_impl(const EltArgs& a) {
   const int64_t nu = a.n / VW;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < nu; u += stride) {
-    const Unit<VW> x = load_unit<VW>(a.x + u * VW);
+    const Unit<VW> x = load_stream<VW>(a.x + u * VW);
     Unit<VW> o;
     if constexpr (MODE == 0) {
 #pragma unroll
       for (int j = 0; j < VW; ++j) o.v[j] = gelu_f(x.v[j]);
     } else {
-      const Unit<VW> g = load_unit<VW>(a.dy + u * VW);
+      const Unit<VW> g = load_stream<VW>(a.dy + u * VW);
 #pragma unroll
       for (int j = 0; j < VW; ++j) o.v[j] = g.v[j] * gelu_mask_f(x.v[j]);
     }
-    store_unit<VW>(a.y + u * VW, o);
+    store_stream<VW>(a.y + u * VW, o);
   }
 }
 
@@ -73,11 +73,11 @@ VH_DEV void gelu_bias_fwd_impl(const GeluBiasBwdArgs& a) {
     for (int k = 0; k < NV; ++k) {
       const int u = threadIdx.x + k * 256;
       if (u < U) {
-        const Unit<VW> x = load_unit<VW>(xr + u * VW);
+        const Unit<VW> x = load_stream<VW>(xr + u * VW);
         Unit<VW> o;
 #pragma unroll
         for (int j = 0; j < VW; ++j) o.v[j] = gelu_f(x.v[j] + b[k].v[j]);
-        store_unit<VW>(yr + u * VW, o);
+        store_stream<VW>(yr + u * VW, o);
       }
     }
   }
@@ -107,15 +107,15 @@ VH_DEV void gelu_bias_bwd_impl(const GeluBiasBwdArgs& a) {
     for (int k = 0; k < NV; ++k) {
       const int u = threadIdx.x + k * 256;
       if (u < U) {
-        const Unit<VW> x = load_unit<VW>(xr + u * VW);
-        const Unit<VW> g = load_unit<VW>(gr + u * VW);
+        const Unit<VW> x = load_stream<VW>(xr + u * VW);
+        const Unit<VW> g = load_stream<VW>(gr + u * VW);
         Unit<VW> o;
 #pragma unroll
         for (int j = 0; j < VW; ++j) {
           o.v[j] = g.v[j] * gelu_mask_f(x.v[j] + b[k].v[j]);
           acc[k].v[j] += o.v[j];
         }
-        store_unit<VW>(dr + u * VW, o);
+        store_stream<VW>(dr + u * VW, o);
       }
     }
   }

@@ -34,12 +34,12 @@ VH_DEV void binary_contig_impl(const BinaryArgs& a) {
   const int64_t nu = a.n / VW;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < nu; u += stride) {
-    const Unit<VW> l = load_unit<VW>(a.l + u * VW);
-    const Unit<VW> r = load_unit<VW>(a.r + u * VW);
+    const Unit<VW> l = load_stream<VW>(a.l + u * VW);
+    const Unit<VW> r = load_stream<VW>(a.r + u * VW);
     Unit<VW> o;
 #pragma unroll
     for (int j = 0; j < VW; ++j) o.v[j] = apply_op(a.op, l.v[j], r.v[j]);
-    store_unit<VW>(a.out + u * VW, o);
+    store_stream<VW>(a.out + u * VW, o);
   }
 }
 

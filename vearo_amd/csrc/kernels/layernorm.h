@@ -7,70 +7,84 @@
 // dgamma = sum_rows go*x_hat, dbeta = sum_rows go.
 //
 // Layout: x, y, dy, dx are [rows, C] row-major in HBM; w, b are [C].
-// Forward: a TEAM of lanes owns one row, the row lives in VGPRs (NV units of VW
-// floats per lane), so x is read exactly once and y written once (8 B/elem).
-// Backward: x and dy read once, dx written once (12 B/elem). dgamma/dbeta are
-// deterministic and atomic-free: each lane accumulates its fixed columns over the
-// rows its team visits, the row-groups of a workgroup are folded in a fixed LDS
+// Forward: a TEAM of lanes owns a row held in VGPRs (NV units of VW floats per
+// lane); each team takes RPW rows and issues all their loads before any math,
+// so x is read once and y written once (8 B/elem) with enough bytes in flight.
+// Backward: x and dy read once, dx written once (12 B/elem); the next row of a
+// team is prefetched while the current one is reduced. dgamma/dbeta are
+// deterministic and atomic-free: each lane accumulates its fixed columns over
+// the rows its team visits, the G row-groups of a workgroup fold in a fixed LDS
 // tree, one partial row per workgroup goes to scratch, and col_reduce sums the
 // partials in a fixed order.
 #pragma once
 #include "common.h"
 
-template <int TEAM, int NV, int VW>
+template <int TEAM, int NV, int VW, int RPW>
 VH_DEV void ln_fwd_impl(const LnFwdArgs& a) {
   constexpr int BS = TEAM > 256 ? TEAM : 256;
-  constexpr int RPB = BS / TEAM;
+  constexpr int TPB = BS / TEAM;  // teams per block
   __shared__ float red[16];
   const int lane = threadIdx.x % TEAM;
-  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TEAM;
-  const bool active = row < a.rows;
+  const int64_t row0 = ((int64_t)blockIdx.x * TPB + threadIdx.x / TEAM) * RPW;
   const int C = a.C;
   const int U = C / VW;
-  const float* xr = a.x + (active ? row : 0) * (int64_t)C;
-
-  Unit<VW> v[NV];
-  float s = 0.0f;
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int u = lane + k * TEAM;
-    v[k] = (active && u < U) ? load_unit<VW>(xr + u * VW) : zero_unit<VW>();
-#pragma unroll
-    for (int j = 0; j < VW; ++j) s += v[k].v[j];
-  }
-  s = team_sum<TEAM>(s, red);
   const float Cf = (float)C;
-  const float mean = s / Cf;
-  float q = 0.0f;
+
+  Unit<VW> v[RPW][NV];
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int u = lane + k * TEAM;
-    if (u < U) {
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t row = row0 + r;
+    const bool active = row < a.rows;
+    const float* xr = a.x + (active ? row : 0) * (int64_t)C;
 #pragma unroll
-      for (int j = 0; j < VW; ++j) {
-        const float d = v[k].v[j] - mean;
-        q += d * d;
-      }
+    for (int k = 0; k < NV; ++k) {
+      const int u = lane + k * TEAM;
+      v[r][k] = (active && u < U) ? load_stream<VW>(xr + u * VW) : zero_unit<VW>();
     }
   }
-  q = team_sum<TEAM>(q, red);
-  const float var = q / Cf;
-  const float inv_std = 1.0f / sqrtf(var + a.eps);
-  if (!active) return;
-  float* yr = a.y + row * (int64_t)C;
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int u = lane + k * TEAM;
-    if (u < U) {
-      const Unit<VW> w = load_unit<VW>(a.w + u * VW);
-      const Unit<VW> b = load_unit<VW>(a.b + u * VW);
-      Unit<VW> o;
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t row = row0 + r;
+    float s = 0.0f;
 #pragma unroll
-      for (int j = 0; j < VW; ++j) {
-        const float xh = (v[k].v[j] - mean) * inv_std;
-        o.v[j] = xh * w.v[j] + b.v[j];
+    for (int k = 0; k < NV; ++k) {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) s += v[r][k].v[j];
+    }
+    s = team_sum<TEAM>(s, red);
+    const float mean = s / Cf;
+    float q = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int u = lane + k * TEAM;
+      if (u < U) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) {
+          const float d = v[r][k].v[j] - mean;
+          q += d * d;
+        }
       }
-      store_unit<VW>(yr + u * VW, o);
+    }
+    q = team_sum<TEAM>(q, red);
+    const float var = q / Cf;
+    const float inv_std = 1.0f / sqrtf(var + a.eps);
+    if (row < a.rows) {
+      float* yr = a.y + row * (int64_t)C;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int u = lane + k * TEAM;
+        if (u < U) {
+          const Unit<VW> w = load_unit<VW>(a.w + u * VW);
+          const Unit<VW> b = load_unit<VW>(a.b + u * VW);
+          Unit<VW> o;
+#pragma unroll
+          for (int j = 0; j < VW; ++j) {
+            const float xh = (v[r][k].v[j] - mean) * inv_std;
+            o.v[j] = xh * w.v[j] + b.v[j];
+          }
+          store_stream<VW>(yr + u * VW, o);
+        }
+      }
     }
   }
 }
@@ -78,9 +92,9 @@ VH_DEV void ln_fwd_impl(const LnFwdArgs& a) {
 // Backward stage 1. Workgroup = BS threads = G row-groups of TEAM lanes. The
 // workgroup owns rows [blockIdx.x*rows_per_block, +rows_per_block); group g
 // visits rows g, g+G, ... of that range. Dynamic LDS: (G/2)*2*C floats.
-template <int TEAM, int NV, int VW>
+template <int TEAM, int NV, int VW, int BS>
 VH_DEV void ln_bwd_impl(const LnBwdArgs& a, float* lds) {
-  constexpr int BS = TEAM > 256 ? TEAM : 256;
+  static_assert(BS >= TEAM && BS % TEAM == 0, "block must hold whole teams");
   constexpr int G = BS / TEAM;
   __shared__ float red[16];
   const int lane = threadIdx.x % TEAM;
@@ -99,21 +113,34 @@ VH_DEV void ln_bwd_impl(const LnBwdArgs& a, float* lds) {
     gb[k] = zero_unit<VW>();
   }
 
-  for (int64_t row = r0 + g; row < r1; row += G) {
-    const float* xr = a.x + row * (int64_t)C;
-    const float* dyr = a.dy + row * (int64_t)C;
-    Unit<VW> xv[NV], gv[NV];
-    float s = 0.0f;
+  // Row `row` of this group: x and dy into registers (zeros past the range).
+  auto load_row = [&](int64_t row, Unit<VW>* xv, Unit<VW>* gv) {
+    const bool ok = row < r1;
+    const float* xr = a.x + (ok ? row : 0) * (int64_t)C;
+    const float* dyr = a.dy + (ok ? row : 0) * (int64_t)C;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int u = lane + k * TEAM;
-      if (u < U) {
-        xv[k] = load_unit<VW>(xr + u * VW);
-        gv[k] = load_unit<VW>(dyr + u * VW);
+      if (ok && u < U) {
+        xv[k] = load_stream<VW>(xr + u * VW);
+        gv[k] = load_stream<VW>(dyr + u * VW);
       } else {
         xv[k] = zero_unit<VW>();
         gv[k] = zero_unit<VW>();
       }
+    }
+  };
+
+  Unit<VW> xv[NV], gv[NV];
+  int64_t row = r0 + g;
+  load_row(row, xv, gv);
+  for (; row < r1; row += G) {
+    Unit<VW> xn[NV], gn[NV];
+    load_row(row + G, xn, gn);  // prefetch: in flight while this row is reduced
+
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
 #pragma unroll
       for (int j = 0; j < VW; ++j) s += xv[k].v[j];
     }
@@ -167,8 +194,13 @@ VH_DEV void ln_bwd_impl(const LnBwdArgs& a, float* lds) {
           const float t1 = Cf * gv[k].v[j] * w.v[j];
           o.v[j] = (t1 - sgw - xh * sgwx) * inv_std / Cf;
         }
-        store_unit<VW>(dxr + u * VW, o);
+        store_stream<VW>(dxr + u * VW, o);
       }
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      xv[k] = xn[k];
+      gv[k] = gn[k];
     }
   }
 
@@ -222,8 +254,10 @@ VH_DEV void ln_bwd_impl(const LnBwdArgs& a, float* lds) {
   }
 }
 
-// Stage 2: out_c[col] = sum over p of part[p][c][col], p ascending within each of
-// 16 waves (wave w takes p = w, w+16, ...), then the 16 wave sums in order.
+// Stage 2: out_c[col] = sum over p of part[p][c][col]. Wave w of the 16 owns the
+// contiguous partial range [w*per, (w+1)*per) and sums it in order with up to 16
+// loads in flight; the 16 wave sums are then added in wave order, so the result
+// is the partials summed in index order with a fixed grouping (deterministic).
 // Grid: (ceil(C/64), ncomp), 1024 threads.
 VH_DEV void col_reduce_impl(const ColReduceArgs& a) {
   __shared__ float red[16][64];
@@ -231,22 +265,21 @@ VH_DEV void col_reduce_impl(const ColReduceArgs& a) {
   const int w = threadIdx.x >> 6;
   const int comp = blockIdx.y;
   const int col = blockIdx.x * 64 + lane;
+  const int per = (a.P + 15) / 16;
+  const int p0 = w * per;
+  const int p1 = min(p0 + per, a.P);
   float s = 0.0f;
   if (col < a.C) {
     const float* base = a.part + (size_t)comp * a.C + col;
     const size_t pstride = (size_t)a.ncomp * a.C;
-    int p = w;
-    for (; p + 48 < a.P; p += 64) {
-      const float v0 = base[(size_t)p * pstride];
-      const float v1 = base[(size_t)(p + 16) * pstride];
-      const float v2 = base[(size_t)(p + 32) * pstride];
-      const float v3 = base[(size_t)(p + 48) * pstride];
-      s += v0;
-      s += v1;
-      s += v2;
-      s += v3;
+    for (int p = p0; p < p1; p += 16) {
+      float v[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = (p + k < p1) ? base[(size_t)(p + k) * pstride] : 0.0f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if (p + k < p1) s += v[k];
     }
-    for (; p < a.P; p += 16) s += base[(size_t)p * pstride];
   }
   red[w][lane] = s;
   __syncthreads();

@@ -22,39 +22,64 @@
   M(1024, 4, VW) M(1024, 6, VW) M(1024, 8, VW)
 #define ROW_CFG_BIG(M, VW) M(64, 12, VW) M(64, 16, VW) M(1024, 12, VW) M(1024, 16, VW)
 #define ROW_CFG_ALL(M, VW) ROW_CFG_SMALL(M, VW) ROW_CFG_BIG(M, VW)
+// Sub-wave / wave teams with short rows also come in 2- and 4-rows-per-team forms.
+#define ROW_CFG_MULTI(M, VW) \
+  M(16, 1, VW) M(32, 1, VW) M(64, 1, VW) M(64, 2, VW) M(64, 3, VW) M(64, 4, VW)
 
-#define K_LN_FWD(T, N, VW)                                                        \
+#define K_LN_FWD_R(T, N, VW, R)                                                   \
   extern "C" __global__ void __launch_bounds__(BS_OF(T))                          \
-      vh_ln_fwd_t##T##_n##N##_v##VW(LnFwdArgs a) {                                \
-    ln_fwd_impl<T, N, VW>(a);                                                     \
+      vh_ln_fwd_t##T##_n##N##_v##VW##_r##R(LnFwdArgs a) {                         \
+    ln_fwd_impl<T, N, VW, R>(a);                                                  \
   }
+#define K_LN_FWD(T, N, VW) K_LN_FWD_R(T, N, VW, 1)
+#define K_LN_FWD_M(T, N, VW) K_LN_FWD_R(T, N, VW, 2) K_LN_FWD_R(T, N, VW, 4)
 ROW_CFG_ALL(K_LN_FWD, 1)
 ROW_CFG_ALL(K_LN_FWD, 4)
+ROW_CFG_MULTI(K_LN_FWD_M, 1)
+ROW_CFG_MULTI(K_LN_FWD_M, 4)
 
-#define K_LN_BWD(T, N, VW)                                                        \
-  extern "C" __global__ void __launch_bounds__(BS_OF(T))                          \
-      vh_ln_bwd_t##T##_n##N##_v##VW(LnBwdArgs a) {                                \
+#define K_LN_BWD_B(T, N, VW, BS)                                                  \
+  extern "C" __global__ void __launch_bounds__(BS)                                \
+      vh_ln_bwd_t##T##_n##N##_v##VW##_b##BS(LnBwdArgs a) {                        \
     extern __shared__ float dyn_lds[];                                            \
-    ln_bwd_impl<T, N, VW>(a, dyn_lds);                                            \
+    ln_bwd_impl<T, N, VW, BS>(a, dyn_lds);                                        \
   }
+#define BSLIT_16 256
+#define BSLIT_32 256
+#define BSLIT_64 256
+#define BSLIT_1024 1024
+#define K_LN_BWD_X(T, N, VW, BS) K_LN_BWD_B(T, N, VW, BS)  // expands BS before pasting
+#define K_LN_BWD(T, N, VW) K_LN_BWD_X(T, N, VW, BSLIT_##T)
+#define K_LN_BWD_1024(T, N, VW) K_LN_BWD_B(T, N, VW, 1024)
 ROW_CFG_SMALL(K_LN_BWD, 1)
 ROW_CFG_SMALL(K_LN_BWD, 4)
+// Wave teams with rows up to 1024 units: 16 row-groups per workgroup.
+K_LN_BWD_1024(64, 1, 1) K_LN_BWD_1024(64, 2, 1) K_LN_BWD_1024(64, 3, 1) K_LN_BWD_1024(64, 4, 1)
+K_LN_BWD_1024(64, 1, 4) K_LN_BWD_1024(64, 2, 4) K_LN_BWD_1024(64, 3, 4) K_LN_BWD_1024(64, 4, 4)
 
-#define K_SM_FWD(T, N, VW)                                                        \
+#define K_SM_FWD_R(T, N, VW, R)                                                   \
   extern "C" __global__ void __launch_bounds__(BS_OF(T))                          \
-      vh_sm_fwd_t##T##_n##N##_v##VW(SoftmaxArgs a) {                              \
-    softmax_fwd_impl<T, N, VW>(a);                                                \
+      vh_sm_fwd_t##T##_n##N##_v##VW##_r##R(SoftmaxArgs a) {                       \
+    softmax_fwd_impl<T, N, VW, R>(a);                                             \
   }
+#define K_SM_FWD(T, N, VW) K_SM_FWD_R(T, N, VW, 1)
+#define K_SM_FWD_M(T, N, VW) K_SM_FWD_R(T, N, VW, 2)
 ROW_CFG_ALL(K_SM_FWD, 1)
 ROW_CFG_ALL(K_SM_FWD, 4)
+ROW_CFG_MULTI(K_SM_FWD_M, 1)
+ROW_CFG_MULTI(K_SM_FWD_M, 4)
 
-#define K_SM_BWD(T, N, VW)                                                        \
+#define K_SM_BWD_R(T, N, VW, R)                                                   \
   extern "C" __global__ void __launch_bounds__(BS_OF(T))                          \
-      vh_sm_bwd_t##T##_n##N##_v##VW(SoftmaxArgs a) {                              \
-    softmax_bwd_impl<T, N, VW>(a);                                                \
+      vh_sm_bwd_t##T##_n##N##_v##VW##_r##R(SoftmaxArgs a) {                       \
+    softmax_bwd_impl<T, N, VW, R>(a);                                             \
   }
+#define K_SM_BWD(T, N, VW) K_SM_BWD_R(T, N, VW, 1)
+#define K_SM_BWD_M(T, N, VW) K_SM_BWD_R(T, N, VW, 2)
 ROW_CFG_SMALL(K_SM_BWD, 1)
 ROW_CFG_SMALL(K_SM_BWD, 4)
+ROW_CFG_MULTI(K_SM_BWD_M, 1)
+ROW_CFG_MULTI(K_SM_BWD_M, 4)
 
 extern "C" __global__ void __launch_bounds__(1024) vh_col_reduce(ColReduceArgs a) {
   col_reduce_impl(a);

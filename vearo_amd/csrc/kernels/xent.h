@@ -36,7 +36,7 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int c = threadIdx.x + k * 1024;
-    v[k] = c < V ? lr[c] : -INFINITY;
+    v[k] = c < V ? __builtin_nontemporal_load(lr + c) : -INFINITY;
     if (v[k] > m) m = v[k];
   }
   m = team_max<1024>(m, red);
@@ -62,7 +62,7 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
       if (c < V) {
         const float p = v[k] / s;
         const float ind = c == t ? 1.0f : 0.0f;
-        o[c] = go * (p - ind) / Bf;
+        __builtin_nontemporal_store(go * (p - ind) / Bf, o + c);
       }
     }
   }

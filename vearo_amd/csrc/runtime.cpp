@@ -210,7 +210,15 @@ int fill(void* p, float value, int64_t n, hipStream_t s) {
 // --------------------------------------------------------- row engine cfg --
 struct RowCfg {
   int team, nv, vw;
+  int rpw = 1;  // rows per team (forward kernels)
+  int bs = 0;   // workgroup size (0: max(team, 256))
 };
+
+// Rows per team for short rows (wave or sub-wave teams holding <= 4 units per
+// lane): chosen from kernel timings on MI355X at the GPT-2 shapes.
+constexpr int kLnFwdRpw = 4;
+constexpr int kSmFwdRpw = 1;
+constexpr int kSmBwdRpw = 1;
 
 const int kNV[] = {1, 2, 3, 4, 6, 8, 12, 16};
 
@@ -246,18 +254,26 @@ bool pick_row_cfg(int64_t C, bool vec_ok, int cap, RowCfg* out) {
   return false;
 }
 
-std::string row_kernel(const char* base, const RowCfg& c) {
+int block_of(const RowCfg& c) { return c.bs ? c.bs : (c.team > 256 ? c.team : 256); }
+
+std::string row_base(const char* base, const RowCfg& c) {
   return std::string(base) + "_t" + std::to_string(c.team) + "_n" + std::to_string(c.nv) + "_v" +
          std::to_string(c.vw);
 }
+// Forward kernels carry the rows-per-team suffix, backward LayerNorm the block size.
+std::string fwd_kernel(const char* base, const RowCfg& c) { return row_base(base, c) + "_r" + std::to_string(c.rpw); }
+std::string bwd_kernel(const char* base, const RowCfg& c) { return row_base(base, c) + "_b" + std::to_string(block_of(c)); }
 
-int block_of(const RowCfg& c) { return c.team > 256 ? c.team : 256; }
+// Multi-row variants exist for teams <= 64 lanes holding <= 4 units per lane.
+void set_rpw(RowCfg* c, int rpw) { c->rpw = (c->team <= 64 && c->nv <= 4) ? rpw : 1; }
+// LayerNorm backward runs wave teams of short rows 16 to a 1024-thread workgroup.
+void set_ln_bwd_bs(RowCfg* c) { c->bs = (c->team == 64 && c->nv <= 4) ? 1024 : 0; }
 
 // LayerNorm backward workgroup count: fixed caps (independent of the device) so
 // the scratch size and the reduction order depend on (rows, C) only.
 int64_t ln_bwd_blocks(int64_t rows, const RowCfg& c) {
   const int groups = block_of(c) / c.team;
-  const int64_t cap = c.team > 256 ? 512 : 1024;
+  const int64_t cap = block_of(c) >= 1024 ? 256 : 1024;
   int64_t G = std::min<int64_t>(cdiv(rows, groups), cap);
   if (G < 1) G = 1;
   const int64_t rpb = cdiv(rows, G);
@@ -488,10 +504,11 @@ int vh_layernorm_fwd(const float* x, const float* w, const float* b, float* y, i
   const bool vec = aligned16(x) && aligned16(w) && aligned16(b) && aligned16(y);
   if (!pick_row_cfg(C, vec, 16, &c))
     return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_fwd: C=" + std::to_string(C) + " exceeds 65536");
+  set_rpw(&c, kLnFwdRpw);
   const int bs = block_of(c);
-  const int64_t rpb = bs / c.team;
+  const int64_t rpb = (int64_t)(bs / c.team) * c.rpw;
   LnFwdArgs a{x, w, b, y, rows, (int32_t)C, eps};
-  return launch(row_kernel("vh_ln_fwd", c), (unsigned)cdiv(rows, rpb), 1, bs, 0, S(stream), a);
+  return launch(fwd_kernel("vh_ln_fwd", c), (unsigned)cdiv(rows, rpb), 1, bs, 0, S(stream), a);
 }
 
 size_t vh_layernorm_bwd_scratch_bytes(int64_t rows, int64_t C) {
@@ -501,8 +518,10 @@ size_t vh_layernorm_bwd_scratch_bytes(int64_t rows, int64_t C) {
   size_t need = 0;
   for (bool vec : {true, false}) {
     RowCfg c;
-    if (pick_row_cfg(C, vec, 8, &c))
+    if (pick_row_cfg(C, vec, 8, &c)) {
+      set_ln_bwd_bs(&c);
       need = std::max(need, align256((size_t)ln_bwd_blocks(rows, c) * 2 * (size_t)C * sizeof(float)));
+    }
   }
   return need;
 }
@@ -524,6 +543,7 @@ int vh_layernorm_bwd(const float* x, const float* w, const float* dy, float* dx,
   const bool vec = aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx);
   if (!pick_row_cfg(C, vec, 8, &c))
     return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_bwd: C=" + std::to_string(C) + " exceeds 32768");
+  set_ln_bwd_bs(&c);
   const int64_t G = ln_bwd_blocks(rows, c);
   const size_t need = align256((size_t)G * 2 * (size_t)C * sizeof(float));
   Scratch sc;
@@ -534,7 +554,7 @@ int vh_layernorm_bwd(const float* x, const float* w, const float* dy, float* dx,
   if (shmem > 64 * 1024) return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_bwd: LDS budget exceeded");
   const int64_t rpb = cdiv(rows, G);
   LnBwdArgs a{x, w, dy, dx, static_cast<float*>(sc.p), rows, rpb, (int32_t)C, eps};
-  VH_TRY(launch(row_kernel("vh_ln_bwd", c), (unsigned)G, 1, bs, shmem, s, a));
+  VH_TRY(launch(bwd_kernel("vh_ln_bwd", c), (unsigned)G, 1, bs, shmem, s, a));
   ColReduceArgs r{static_cast<float*>(sc.p), dw, db, (int32_t)G, (int32_t)C, 2};
   return launch("vh_col_reduce", (unsigned)cdiv(C, 64), 2, 1024, 0, s, r);
 }
@@ -619,16 +639,17 @@ int vh_gelu_bias_bwd(const float* x, const float* bias, const float* dy, float* 
 
 // --------------------------------------------------------------- softmax --
 
-static int softmax_common(const char* base, int cap, const float* in, const float* dy, float* out,
-                          int64_t rows, int64_t T, int causal, int input_is_x, hipStream_t s) {
+static int softmax_common(const char* base, int cap, int rpw, const float* in, const float* dy,
+                          float* out, int64_t rows, int64_t T, int causal, int input_is_x, hipStream_t s) {
   RowCfg c;
   const bool vec = aligned16(in) && aligned16(out) && (!dy || aligned16(dy));
   if (!pick_row_cfg(T, vec, cap, &c))
     return fail(VH_ERR_UNSUPPORTED, std::string(base) + ": T=" + std::to_string(T) + " too large");
+  set_rpw(&c, rpw);
   const int bs = block_of(c);
-  const int64_t rpb = bs / c.team;
+  const int64_t rpb = (int64_t)(bs / c.team) * c.rpw;
   SoftmaxArgs a{in, dy, out, rows, (int32_t)T, causal ? 1 : 0, input_is_x ? 1 : 0};
-  return launch(row_kernel(base, c), (unsigned)cdiv(rows, rpb), 1, bs, 0, s, a);
+  return launch(fwd_kernel(base, c), (unsigned)cdiv(rows, rpb), 1, bs, 0, s, a);
 }
 
 int vh_softmax_fwd(const float* x, float* y, int64_t rows, int64_t T, int causal, void* stream) {
@@ -637,7 +658,7 @@ int vh_softmax_fwd(const float* x, float* y, int64_t rows, int64_t T, int causal
   if (rows == 0 || T == 0) return VH_OK;
   if (!x || !y) return fail(VH_ERR_INVALID, "vh_softmax_fwd: null pointer");
   if (T > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_softmax_fwd: T too large");
-  return softmax_common("vh_sm_fwd", 16, x, nullptr, y, rows, T, causal, 0, S(stream));
+  return softmax_common("vh_sm_fwd", 16, kSmFwdRpw, x, nullptr, y, rows, T, causal, 0, S(stream));
 }
 
 int vh_softmax_bwd(const float* in, const float* dy, float* dx, int64_t rows, int64_t T,
@@ -647,7 +668,7 @@ int vh_softmax_bwd(const float* in, const float* dy, float* dx, int64_t rows, in
   if (rows == 0 || T == 0) return VH_OK;
   if (!in || !dy || !dx) return fail(VH_ERR_INVALID, "vh_softmax_bwd: null pointer");
   if (T > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_softmax_bwd: T too large");
-  return softmax_common("vh_sm_bwd", 8, in, dy, dx, rows, T, causal, input_is_x, S(stream));
+  return softmax_common("vh_sm_bwd", 8, kSmBwdRpw, in, dy, dx, rows, T, causal, input_is_x, S(stream));
 }
 
 // ------------------------------------------------------------- embedding --
