@@ -125,6 +125,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 4 device-to-device copies of 256 MiB (a copy kernel of known "
+                         "size, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box has one GPU); "
@@ -136,6 +139,14 @@ def main():
     vh.init(0)
     hip = Hip()
     stream = vh.lib.vh_stream()
+    if args.calibrate_copy:
+        nb = 256 << 20
+        src, dst = vh.DeviceBuffer(nb, zero=True), vh.DeviceBuffer(nb)
+        for _ in range(4):
+            vh.check(vh.lib.vh_d2d(dst.ptr, src.ptr, nb, None))
+        vh.sync()
+        print(json.dumps({"calibrate_copy_bytes": nb, "copies": 4}), flush=True)
+        return
     r = np.random.default_rng(0x5EED0000 + 4)
 
     # ---- inputs, resident in HBM before the timed region
