@@ -220,8 +220,20 @@ def main():
     ms_per_step = wall / K * 1e3
     value = step_bytes / (wall / K) / 1e9
     dom = max(names, key=lambda n: per[n])
+    # HBM traffic per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # passes over this same workload, scaled by the counters' reading of a copy of
+    # known size (profiles/pmc_traffic_bench.json); null when absent.
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "pmc_traffic_bench.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            tk = json.load(f).get("kernels", {})
+        for n in names:
+            if n in tk:
+                kernels[n]["traffic_bytes"] = tk[n]["traffic_bytes"]
+        traffic = tk.get(dom, {}).get("traffic_bytes")
     roofline = {"bound": "hbm", "kernel": dom, "achieved": kernels[dom]["gbps"], "peak": PEAK_GBPS,
-                "unit": "GB/s", "frac": kernels[dom]["frac"], "traffic": None}
+                "unit": "GB/s", "frac": kernels[dom]["frac"], "traffic": traffic}
     res = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
