@@ -1,0 +1,318 @@
+// test_backend_ops.cpp -- the HIP BackendOps mirror exercised the way the
+// reference's own tests exercise its CUDA backend
+// (crates/vearo-backend-cuda/src/lib.rs:1638-1826): CPU <-> device parity on
+// small known inputs, every hot op on a non-contiguous input against the same
+// op on `.contiguous()`, panics with the CPU backend's messages, empty tensors,
+// the autograd arms, and a memory-regression loop (crates/vearo/tests/memory_regression.rs).
+// The CPU oracle (oracle/vearo_cpu_ref.c) is the checker. Needs a gfx950 GPU.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "../../include/vearo_hip.h"
+#include "vearo_backend.h"
+#include "vearo_cpu_ref.h"
+
+using namespace vearo_hip;
+
+static int g_fail = 0, g_pass = 0;
+static std::string g_where;
+
+#define CHECK(cond, msg)                                                                         \
+  do {                                                                                           \
+    if (!(cond)) throw std::runtime_error(std::string("check failed: ") + (msg) + " [" #cond "]"); \
+  } while (0)
+
+static void run(const char* name, const std::function<void()>& f) {
+  std::printf("[ run ] %s\n", name);
+  std::fflush(stdout);
+  try {
+    f();
+    ++g_pass;
+    std::printf("[  ok ] %s\n", name);
+  } catch (const std::exception& e) {
+    ++g_fail;
+    std::printf("[FAIL] %s: %s\n", name, e.what());
+  }
+  std::fflush(stdout);
+}
+
+static vo_layout contig(const std::vector<int64_t>& dims) {
+  vo_layout l;
+  vo_contiguous_layout(&l, (int)dims.size(), dims.data());
+  return l;
+}
+
+// |gpu - cpu| <= 1e-5 + 1e-4 |cpu| elementwise.
+static void expect_close(const std::vector<float>& gpu, const std::vector<float>& cpu, const char* what,
+                         double atol = 1e-5, double rtol = 1e-4) {
+  CHECK(gpu.size() == cpu.size(), std::string(what) + ": size mismatch");
+  for (size_t i = 0; i < gpu.size(); ++i) {
+    const double d = std::fabs((double)gpu[i] - (double)cpu[i]);
+    if (!(d <= atol + rtol * std::fabs((double)cpu[i])) && !(gpu[i] == cpu[i])) {
+      char buf[256];
+      std::snprintf(buf, sizeof buf, "%s: element %zu gpu=%.9g cpu=%.9g", what, i, gpu[i], cpu[i]);
+      throw std::runtime_error(buf);
+    }
+  }
+}
+
+static double maxdiff(const std::vector<float>& a, const std::vector<float>& b) {
+  double m = 0;
+  for (size_t i = 0; i < a.size(); ++i) m = std::max(m, (double)std::fabs(a[i] - b[i]));
+  return m;
+}
+
+template <typename F>
+static void expect_panic(F&& f, const std::string& substr) {
+  try {
+    f();
+  } catch (const Panic& p) {
+    CHECK(std::string(p.what()).find(substr) != std::string::npos,
+          "panic text '" + std::string(p.what()) + "' lacks '" + substr + "'");
+    return;
+  }
+  throw std::runtime_error("expected a panic containing '" + substr + "'");
+}
+
+static std::vector<float> randn(size_t n, unsigned seed, float scale = 1.0f) {
+  std::vector<float> v(n);
+  unsigned long long s = 0x9E3779B97F4A7C15ull * (seed + 1);
+  for (size_t i = 0; i < n; ++i) {
+    // SplitMix64 -> two uniforms -> Box-Muller.
+    auto next = [&]() {
+      unsigned long long z = (s += 0x9E3779B97F4A7C15ull);
+      z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+      z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+      return ((z ^ (z >> 31)) >> 11) * (1.0 / 9007199254740992.0);
+    };
+    const double u1 = next() + 1e-300, u2 = next();
+    v[i] = (float)(std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2)) * scale;
+  }
+  return v;
+}
+
+int main() {
+  init(0);
+
+  run("dispatch_registry", [] {
+    CHECK(get_backend_ops(Device::hip()) != nullptr, "HIP backend registered");
+    CHECK(get_backend_ops(Device{Device::Cpu, 0}) == nullptr, "no CPU backend in this process");
+    CHECK(Device::hip().backend_idx() == 2, "HIP uses the reserved backend slot 2");
+    init(0);  // idempotent (first registration wins, tensor.rs:1186-1190)
+  });
+
+  // crates/vearo-backend-cuda/src/lib.rs:1643-1673 (elementwise add, exact).
+  run("test_hip_parity", [] {
+    Tensor a = Tensor::from_f32({1, 2, 3, 4}, Shape{2, 2});
+    Tensor b = Tensor::from_f32({5, 6, 7, 8}, Shape{2, 2});
+    const std::vector<float> c = a.add(b).to_vec_f32();
+    CHECK((c == std::vector<float>{6, 8, 10, 12}), "add");
+    const std::vector<float> d = a.div(b).to_vec_f32();
+    CHECK(d[0] == 1.0f / 5.0f && d[3] == 4.0f / 8.0f, "div");
+  });
+
+  // crates/vearo-backend-cuda/src/lib.rs:1715-1826: every op on a non-contiguous input
+  // against the same op on .contiguous() (tol 1e-3), and against the CPU oracle.
+  run("test_hip_noncontiguous_parity", [] {
+    std::vector<std::string> fails;
+    auto check = [&](const char* name, const Tensor& nc, const Tensor& c) {
+      const auto a = nc.to_vec_f32(), b = c.to_vec_f32();
+      bool bad = false;
+      for (float v : a) bad |= !std::isfinite(v);
+      const double m = a.size() == b.size() ? maxdiff(a, b) : 1e30;
+      if (bad || m > 1e-3) fails.push_back(std::string(name) + " maxdiff=" + std::to_string(m));
+    };
+    Tensor a = Tensor::from_f32({1, 2, 3, 4, 5, 6, 7, 8, 9}, Shape{3, 3});
+    Tensor b = Tensor::from_f32({9, 8, 7, 6, 5, 4, 3, 2, 1}, Shape{3, 3});
+    Tensor bt = b.transpose(0, 1);
+    check("add(rhs_nc)", a.add(bt), a.add(bt.contiguous()));
+    check("sub(rhs_nc)", a.sub(bt), a.sub(bt.contiguous()));
+    check("mul(rhs_nc)", a.mul(bt), a.mul(bt.contiguous()));
+    check("div(rhs_nc)", a.div(bt), a.div(bt.contiguous()));
+    Tensor at = a.transpose(0, 1);
+    check("add(lhs_nc)", at.add(b), at.contiguous().add(b));
+
+    Tensor x = Tensor::from_f32({-2, -1, 0.5, 1, 2, 3, -0.5, 4, -3, 0, 1.5, -1.5}, Shape{3, 4});
+    Tensor xt = x.transpose(0, 1);
+    check("gelu(nc)", xt.gelu(), xt.contiguous().gelu());
+    check("sum(nc,d0)", xt.sum(0, false), xt.contiguous().sum(0, false));
+    check("sum(nc,d1)", xt.sum(1, true), xt.contiguous().sum(1, true));
+    check("mean(nc,d0)", xt.mean(0, false), xt.contiguous().mean(0, false));
+    check("softmax(nc,d0)", xt.softmax(0), xt.contiguous().softmax(0));
+    check("softmax(nc,d1)", xt.softmax(1), xt.contiguous().softmax(1));
+
+    std::vector<float> lnv(24);
+    for (int i = 0; i < 24; ++i) lnv[i] = i * 0.1f;
+    Tensor ln = Tensor::from_f32(lnv, Shape{2, 3, 4});
+    Tensor lnp = ln.permute({1, 0, 2});
+    Tensor w = Tensor::from_f32({1, 0.5, 2, 1.5}, Shape{4});
+    Tensor bb = Tensor::from_f32({0.1f, -0.1f, 0.2f, 0}, Shape{4});
+    check("layernorm(nc)", lnp.layernorm(w, bb, 1e-5f), lnp.contiguous().layernorm(w, bb, 1e-5f));
+
+    Tensor idx = Tensor::from_f32({0, 2, 1, 1, 0, 2}, Shape{2, 3});
+    Tensor idxt = idx.transpose(0, 1);
+    Tensor emb_w = Tensor::from_f32({10, 11, 20, 21, 30, 31}, Shape{3, 2});
+    check("embedding(nc)", idxt.embedding(emb_w), idxt.contiguous().embedding(emb_w));
+
+    Tensor logits_base = Tensor::from_f32({1, 4, 2, 5, 3, 6}, Shape{3, 2});
+    Tensor logits_nc = logits_base.transpose(0, 1);
+    Tensor tgt = Tensor::from_f32({0, 2}, Shape{2});
+    check("cross_entropy(nc)", logits_nc.cross_entropy(tgt), logits_nc.contiguous().cross_entropy(tgt));
+    if (!fails.empty()) {
+      std::string all;
+      for (auto& f : fails) all += f + "; ";
+      throw std::runtime_error("ops that mishandle non-contiguous inputs: " + all);
+    }
+
+    // The same strided inputs through the CPU oracle.
+    std::vector<float> host = {-2, -1, 0.5, 1, 2, 3, -0.5, 4, -3, 0, 1.5, -1.5};
+    vo_layout tl;
+    tl.rank = 2;
+    tl.dims[0] = 4; tl.dims[1] = 3; tl.strides[0] = 1; tl.strides[1] = 4;
+    std::vector<float> ref(12);
+    vo_gelu(host.data(), &tl, ref.data());
+    expect_close(xt.gelu().to_vec_f32(), ref, "gelu(nc) vs oracle");
+    char err[256];
+    CHECK(vo_softmax(host.data(), &tl, 0, ref.data(), err, sizeof err) == 0, "oracle softmax");
+    expect_close(xt.softmax(0).to_vec_f32(), ref, "softmax(nc,d0) vs oracle");
+    vo_layout lp;
+    lp.rank = 3;
+    lp.dims[0] = 3; lp.dims[1] = 2; lp.dims[2] = 4;
+    lp.strides[0] = 4; lp.strides[1] = 12; lp.strides[2] = 1;
+    std::vector<float> lref(24), wv = {1, 0.5, 2, 1.5}, bv = {0.1f, -0.1f, 0.2f, 0};
+    vo_layout l4 = contig({4});
+    CHECK(vo_layernorm(lnv.data(), &lp, wv.data(), &l4, bv.data(), &l4, 1e-5f, lref.data(), err, sizeof err) == 0,
+          "oracle layernorm");
+    expect_close(lnp.layernorm(w, bb, 1e-5f).to_vec_f32(), lref, "layernorm(nc) vs oracle");
+  });
+
+  run("hot_ops_vs_oracle_gpt2_rows", [] {
+    const int rows = 512, C = 768;
+    auto xv = randn((size_t)rows * C, 1), dyv = randn((size_t)rows * C, 2);
+    auto wv = randn(C, 3, 0.02f), bv = randn(C, 4, 0.02f);
+    for (auto& v : wv) v += 1.0f;
+    Tensor x = Tensor::from_f32(xv, Shape{rows, C}), dy = Tensor::from_f32(dyv, Shape{rows, C});
+    Tensor w = Tensor::from_f32(wv, Shape{C}), b = Tensor::from_f32(bv, Shape{C});
+    auto [gx, gw, gb] = x.layernorm_backward(w, b, dy, 1e-5f);
+    vo_layout xl = contig({rows, C}), cl = contig({C});
+    std::vector<float> y(xv.size()), dx(xv.size()), dw(C), db(C);
+    char err[256];
+    CHECK(vo_layernorm(xv.data(), &xl, wv.data(), &cl, bv.data(), &cl, 1e-5f, y.data(), err, sizeof err) == 0, "ln");
+    CHECK(vo_layernorm_backward(xv.data(), &xl, wv.data(), &cl, &cl, dyv.data(), &xl, 1e-5f, dx.data(), dw.data(),
+                                db.data(), err, sizeof err) == 0, "ln bwd");
+    expect_close(x.layernorm(w, b, 1e-5f).to_vec_f32(), y, "layernorm");
+    expect_close(gx.to_vec_f32(), dx, "layernorm dx");
+    expect_close(gw.to_vec_f32(), dw, "layernorm dgamma", 1e-4, 1e-4);
+    expect_close(gb.to_vec_f32(), db, "layernorm dbeta", 1e-4, 1e-4);
+    // Softmax arm: the 5-op composite and the fused kernel agree with the oracle.
+    std::vector<float> sdx(xv.size());
+    CHECK(vo_softmax_backward_composite(xv.data(), dyv.data(), &xl, 1, sdx.data(), err, sizeof err) == 0, "sm");
+    expect_close(softmax_backward_arm(x, dy, 1).to_vec_f32(), sdx, "softmax arm (composite)");
+    expect_close(softmax_backward_fused(x, dy).to_vec_f32(), sdx, "softmax arm (fused)");
+    // Gelu arm.
+    std::vector<float> mask(xv.size()), gref(xv.size());
+    vo_gelu_grad_mask(xv.data(), (int64_t)xv.size(), mask.data());
+    for (size_t i = 0; i < xv.size(); ++i) gref[i] = dyv[i] * mask[i];
+    expect_close(gelu_backward_fused(x, dy).to_vec_f32(), gref, "gelu arm (fused)");
+  });
+
+  run("embedding_and_cross_entropy_vs_oracle", [] {
+    const int V = 1000, D = 64, n = 300;
+    std::vector<float> ids(n);
+    for (int i = 0; i < n; ++i) ids[i] = (float)((i * 7919) % V);
+    for (int i = 0; i < n; i += 5) ids[i] = 3.0f;  // a heavy token
+    auto wv = randn((size_t)V * D, 5), dyv = randn((size_t)n * D, 6);
+    Tensor I = Tensor::from_f32(ids, Shape{n}), W = Tensor::from_f32(wv, Shape{V, D});
+    Tensor DY = Tensor::from_f32(dyv, Shape{n, D});
+    vo_layout il = contig({n}), wl = contig({V, D}), gl = contig({n, D});
+    std::vector<float> out((size_t)n * D), dw((size_t)V * D);
+    char err[256];
+    CHECK(vo_embedding(ids.data(), &il, wv.data(), &wl, out.data(), err, sizeof err) == 0, "emb");
+    CHECK(vo_embedding_backward(ids.data(), &il, &wl, dyv.data(), &gl, dw.data(), err, sizeof err) == 0, "emb bwd");
+    CHECK(I.embedding(W).to_vec_f32() == out, "embedding forward is bit-exact");
+    CHECK(I.embedding_backward(W, DY).to_vec_f32() == dw, "embedding backward is bit-exact");
+
+    const int B = 33, Vc = 517;
+    auto lv = randn((size_t)B * Vc, 7, 2.0f);
+    std::vector<float> tg(B);
+    for (int i = 0; i < B; ++i) tg[i] = (float)((i * 31) % Vc);
+    Tensor L = Tensor::from_f32(lv, Shape{B, Vc}), T = Tensor::from_f32(tg, Shape{B});
+    Tensor go = Tensor::from_f32({0.7f}, Shape{1});
+    vo_layout ll = contig({B, Vc}), tl = contig({B});
+    float loss;
+    std::vector<float> dl(lv.size());
+    CHECK(vo_cross_entropy(lv.data(), &ll, tg.data(), &tl, &loss, err, sizeof err) == 0, "ce");
+    float gov = 0.7f;
+    CHECK(vo_cross_entropy_backward(lv.data(), &ll, tg.data(), &tl, &gov, 1, dl.data(), err, sizeof err) == 0,
+          "ce bwd");
+    Tensor lt = L.cross_entropy(T);
+    CHECK(lt.shape() == Shape{1}, "loss is a [1] tensor as on the CPU backend (cpu lib.rs:1050)");
+    expect_close(lt.to_vec_f32(), {loss}, "cross_entropy");
+    expect_close(L.cross_entropy_backward(T, go).to_vec_f32(), dl, "cross_entropy_backward", 1e-9, 1e-4);
+  });
+
+  // crates/vearo-backend-cpu/src/lib.rs:2866-2899 and the shape asserts.
+  run("panics_match_cpu_backend", [] {
+    Tensor W = Tensor::zeros(Shape{2, 3});
+    expect_panic([&] { Tensor::from_f32({-1, 0}, Shape{2}).embedding(W).to_vec_f32(); },
+                 "Token ID cannot be negative: -1");
+    expect_panic([&] { Tensor::from_f32({2, 0}, Shape{2}).embedding(W).to_vec_f32(); },
+                 "Token ID 2 out of vocabulary bound 2");
+    Tensor logits = Tensor::zeros(Shape{2, 3});
+    expect_panic([&] { logits.cross_entropy(Tensor::from_f32({-1, 0}, Shape{2})).to_vec_f32(); },
+                 "Target class cannot be negative: -1");
+    expect_panic([&] { logits.cross_entropy(Tensor::from_f32({3, 0}, Shape{2})).to_vec_f32(); },
+                 "Target class 3 out of vocab bounds 3");
+    expect_panic([&] { logits.cross_entropy_backward(Tensor::from_f32({0, 1}, Shape{2}), Tensor::zeros(Shape{2})); },
+                 "grad_out must be a scalar");
+    expect_panic([&] { logits.softmax(2); }, "Softmax dim out of range");
+    expect_panic([&] { logits.sum(2, false); }, "Reduction dim out of range");
+    expect_panic([&] { logits.add(Tensor::zeros(Shape{4})); }, "Shapes are not broadcastable");
+    expect_panic([&] { logits.layernorm(Tensor::zeros(Shape{4}), Tensor::zeros(Shape{3}), 1e-5f); },
+                 "Weight dimension must match norm_dim");
+    expect_panic([&] { Tensor::from_f32({1}, Shape{1}).embedding_backward(W, Tensor::zeros(Shape{1, 2})); },
+                 "grad_out shape must be x.shape() + [embedding_dim]");
+    expect_panic([&] { get_backend_ops(Device::hip())->matmul(logits, logits); },
+                 "matmul is not part of this backend");
+  });
+
+  run("empty_tensors", [] {
+    // crates/vearo-backend-cpu/src/lib.rs:2832-2864.
+    Tensor x = Tensor::zeros(Shape{2, 0, 4});
+    Tensor out = x.layernorm(Tensor::from_f32({1, 1, 1, 1}, Shape{4}), Tensor::zeros(Shape{4}), 1e-5f);
+    CHECK(out.shape() == (Shape{2, 0, 4}), "layernorm of an empty input keeps its shape");
+    Tensor z = Tensor::zeros(Shape{0, 6}).add(Tensor::zeros(Shape{0, 6}));
+    CHECK(z.shape() == (Shape{0, 6}) && z.to_vec_f32().empty(), "empty add");
+    auto [gx, gw, gb] = x.layernorm_backward(Tensor::from_f32({1, 1, 1, 1}, Shape{4}), Tensor::zeros(Shape{4}), x, 1e-5f);
+    CHECK(gw.to_vec_f32() == std::vector<float>(4, 0.0f), "empty layernorm backward gives zero dgamma");
+  });
+
+  run("memory_regression", [] {
+    // crates/vearo/tests/memory_regression.rs:103: live device memory must not grow.
+    vh_mem_stats s0, s1;
+    auto step = [] {
+      Tensor x = Tensor::from_f32(randn(64 * 96, 9), Shape{64, 96});
+      Tensor w = Tensor::from_f32(std::vector<float>(96, 1.0f), Shape{96});
+      Tensor b = Tensor::zeros(Shape{96});
+      Tensor y = x.layernorm(w, b, 1e-5f).gelu().softmax(1);
+      auto [gx, gw, gb] = x.layernorm_backward(w, b, y, 1e-5f);
+      (void)gx.sum(0, false).to_vec_f32();
+    };
+    step();
+    synchronize();
+    vh_mem_stats_get(&s0);
+    for (int i = 0; i < 25; ++i) step();
+    synchronize();
+    vh_mem_stats_get(&s1);
+    CHECK(s1.live_bytes == s0.live_bytes, "live bytes stable over 25 steps");
+    CHECK(s1.hip_bytes == s0.hip_bytes, "no new hipMalloc after the first step (arena reuse)");
+  });
+
+  std::printf("%d passed, %d failed\n", g_pass, g_fail);
+  return g_fail == 0 ? 0 : 1;
+}
