@@ -1,23 +1,30 @@
 """Benchmark of the hot path on one MI355X.
 
-A step is one pass of the path over one synthetic batch at GPT-2-small shape:
-  layernorm forward    x [16384, 768]                 (cfg[4] shape; cfg[0'] in SURVEY)
+Default workload (BASELINE.json's metric): one step is one pass of the path
+over one synthetic batch at GPT-2-small shape,
+  layernorm forward    x [16384, 768]                 (the cfg[4] layernorm shape)
   causal softmax fwd   scores [16, 12, 1024, 1024]    (cfg[2])
-  causal softmax bwd   (from the saved input x and dy, as the autograd arm)
+  causal softmax bwd   from the saved input x and dy, as the autograd arm does
   layernorm backward   (x, w, dy -> dx, dgamma, dbeta)
 issued in that order on the runtime stream, as a training step meets them
-(forward, then backward in reverse). Inputs are resident in HBM before timing;
-layernorm buffers alternate between two sets and the 3.2 GB softmax working set
-flushes the 256 MB MALL between uses, so every kernel reads cold data.
+(forward, then backward in reverse). Other configs of BASELINE.json are
+available with --workload (gelu_bias, embedding_uniform, embedding_zipf,
+cross_entropy, layernorm_cfg0); each prints its own line.
 
-value = algorithmic bytes per step / wall time per step (GB/s), where the
-algorithmic bytes count each necessary HBM transfer once (the live causal
-triangle only for softmax reads). Per-kernel durations come from HIP events on
-the runtime stream around each launch; the roofline object reports the longest
-kernel. cpu_baseline times the CPU oracle (the C restatement of the reference's
-CPU backend, one thread) on a bounded row sample of the same workload.
+Inputs are resident in HBM before timing. Buffers that would otherwise stay in
+the 256 MB MALL between uses alternate between two sets (or are flushed by the
+step's own multi-GB traffic), so every kernel reads cold data.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu]
+value = algorithmic bytes per step / wall time per step (GB/s); algorithmic
+bytes count each necessary HBM transfer once (the live causal triangle only for
+softmax reads, distinct rows only for embedding gathers). Per-kernel durations
+come from HIP events on the runtime stream around each launch; `roofline`
+reports the longest kernel, with `traffic` from the committed rocprofv3
+FETCH_SIZE / WRITE_SIZE passes when present. cpu_baseline times the CPU oracle
+(the C restatement of the reference's CPU backend, one thread) on a bounded
+sample of the same workload, counting the same algorithmic bytes.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload NAME] [--no-cpu]
 """
 import argparse
 import ctypes
@@ -33,8 +40,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "LayerNorm/softmax fwd+bwd HBM GB/s (% of ~8 TB/s peak); GPT block step ms"
 PEAK_GBPS = 8000.0
-LN_ROWS, LN_C = 16384, 768
-SM_B, SM_H, SM_T = 16, 12, 1024
+SEED = 0x5EED0000
 
 
 def ln_bytes(rows, C):
@@ -49,7 +55,7 @@ def sm_bytes(B, H, T):
     live = B * H * T * (T + 1) // 2       # causal lower triangle incl. diagonal
     n = rows * T
     fwd = 4 * live + 4 * n                # R live x, W all y
-    bwd = 4 * live * 2 + 4 * n            # R live x (or y), R live dy, W all dx
+    bwd = 4 * live * 2 + 4 * n            # R live x, R live dy, W all dx
     return fwd, bwd
 
 
@@ -60,7 +66,6 @@ class Hip:
         self.h = ctypes.CDLL("libamdhip64.so.7")
         self.h.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
         self.h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-        self.h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
         self.h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
         self.h.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
 
@@ -82,40 +87,211 @@ class Hip:
 
 
 def causal_scores(r, B, H, T):
-    s = (r.standard_normal(size=(B, H, T, T), dtype=np.float32) * np.float32(0.125))
+    s = r.standard_normal(size=(B, H, T, T), dtype=np.float32) * np.float32(0.125)
     iu = np.triu_indices(T, 1)
     s[:, :, iu[0], iu[1]] = -np.inf
     return s
 
 
-def cpu_baseline(budget_s):
-    """The oracle (one thread) on a row sample of the same workload."""
-    import oracle
+def zipf_ids(r, n, V, s=1.1):
+    ranks = np.arange(1, V + 1, dtype=np.float64)
+    cdf = np.cumsum(ranks ** -s)
+    cdf /= cdf[-1]
+    return np.searchsorted(cdf, r.random(n)).astype(np.float32)
 
-    r = np.random.default_rng(0x5EED0000)
-    ln_rows, sm_heads = 4096, 2
-    x = r.standard_normal(size=(ln_rows, LN_C), dtype=np.float32)
+
+def time_cpu(fn, budget_s):
+    t, reps = 0.0, 0
+    while t < budget_s or reps == 0:
+        t0 = time.perf_counter()
+        fn()
+        t += time.perf_counter() - t0
+        reps += 1
+    return t, reps
+
+
+# ---------------------------------------------------------------- workloads
+# Each workload: setup(vh) -> (ops, info); ops is a list of (name, bytes, call(i)).
+
+def wl_ln_softmax(vh):
+    LN_ROWS, LN_C = 16384, 768
+    SM_B, SM_H, SM_T = 16, 12, 1024
+    r = np.random.default_rng(SEED + 4)
     w = (1 + 0.02 * r.standard_normal(LN_C)).astype(np.float32)
     b = (0.02 * r.standard_normal(LN_C)).astype(np.float32)
-    dy = r.standard_normal(size=(ln_rows, LN_C), dtype=np.float32)
-    s = causal_scores(r, 1, sm_heads, SM_T)
-    g = r.standard_normal(size=s.shape, dtype=np.float32)
-    t_total, reps, sample_bytes = 0.0, 0, 0
-    lf, lb = ln_bytes(ln_rows, LN_C)
-    sf, sb = sm_bytes(1, sm_heads, SM_T)
-    while t_total < budget_s or reps == 0:
-        t0 = time.perf_counter()
-        oracle.layernorm(x, w, b, 1e-5)
-        oracle.softmax(s, 3)
-        oracle.softmax_backward_composite(s, g, 3)
-        oracle.layernorm_backward(x, w, b, dy, 1e-5)
-        t_total += time.perf_counter() - t0
-        reps += 1
-        sample_bytes += lf + lb + sf + sb
-    return {"value": round(sample_bytes / t_total / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"layernorm fwd+bwd [{ln_rows},{LN_C}] + causal softmax fwd + composite bwd "
-                      f"[1,{sm_heads},{SM_T},{SM_T}], {reps} reps in {t_total:.1f} s, single thread; "
-                      f"GB/s counts the same algorithmic bytes as the GPU figure"}
+    W, Bi = vh.DeviceBuffer.from_array(w), vh.DeviceBuffer.from_array(b)
+    sets = []
+    for _ in range(2):
+        x = r.standard_normal(size=(LN_ROWS, LN_C), dtype=np.float32)
+        dy = r.standard_normal(size=(LN_ROWS, LN_C), dtype=np.float32)
+        sets.append(dict(x=vh.DeviceBuffer.from_array(x), dy=vh.DeviceBuffer.from_array(dy),
+                         y=vh.DeviceBuffer(x.nbytes), dx=vh.DeviceBuffer(x.nbytes),
+                         dw=vh.DeviceBuffer(w.nbytes), db=vh.DeviceBuffer(w.nbytes)))
+    nsc = vh.lib.vh_layernorm_bwd_scratch_bytes(LN_ROWS, LN_C)
+    LNS = vh.DeviceBuffer(nsc)
+    rs = np.random.default_rng(SEED + 2)
+    s = causal_scores(rs, SM_B, SM_H, SM_T)
+    S = vh.DeviceBuffer.from_array(s)
+    del s
+    G = vh.DeviceBuffer.from_array(rs.standard_normal(size=(SM_B, SM_H, SM_T, SM_T), dtype=np.float32))
+    n_sm = SM_B * SM_H * SM_T * SM_T
+    P, DS = vh.DeviceBuffer(4 * n_sm), vh.DeviceBuffer(4 * n_sm)
+    rows_sm = SM_B * SM_H * SM_T
+    lf, lb = ln_bytes(LN_ROWS, LN_C)
+    sf, sb = sm_bytes(SM_B, SM_H, SM_T)
+    L = lambda i: sets[i % 2]
+    ops = [
+        ("layernorm_fwd", lf, lambda i: vh.lib.vh_layernorm_fwd(L(i)["x"].ptr, W.ptr, Bi.ptr, L(i)["y"].ptr,
+                                                                 LN_ROWS, LN_C, 1e-5, None)),
+        ("softmax_fwd", sf, lambda i: vh.lib.vh_softmax_fwd(S.ptr, P.ptr, rows_sm, SM_T, 1, None)),
+        # The autograd Softmax arm saves the input x and recomputes y from it
+        # (crates/vearo-autograd/src/lib.rs:547-553); the fused kernel does the same.
+        ("softmax_bwd", sb, lambda i: vh.lib.vh_softmax_bwd(S.ptr, G.ptr, DS.ptr, rows_sm, SM_T, 1, 1, None)),
+        ("layernorm_bwd", lb, lambda i: vh.lib.vh_layernorm_bwd(
+            L(i)["x"].ptr, W.ptr, L(i)["dy"].ptr, L(i)["dx"].ptr, L(i)["dw"].ptr, L(i)["db"].ptr,
+            LN_ROWS, LN_C, 1e-5, LNS.ptr, nsc, None)),
+    ]
+    keep = (W, Bi, sets, LNS, S, G, P, DS)
+
+    def cpu(budget):
+        import oracle
+        rc = np.random.default_rng(SEED)
+        ln_rows, heads = 4096, 2
+        x = rc.standard_normal(size=(ln_rows, LN_C), dtype=np.float32)
+        dy = rc.standard_normal(size=(ln_rows, LN_C), dtype=np.float32)
+        s = causal_scores(rc, 1, heads, SM_T)
+        g = rc.standard_normal(size=s.shape, dtype=np.float32)
+        t, reps = time_cpu(lambda: (oracle.layernorm(x, w, b, 1e-5), oracle.softmax(s, 3),
+                                    oracle.softmax_backward_composite(s, g, 3),
+                                    oracle.layernorm_backward(x, w, b, dy, 1e-5)), budget)
+        nb = sum(ln_bytes(ln_rows, LN_C)) + sum(sm_bytes(1, heads, SM_T))
+        return nb * reps / t, (f"layernorm fwd+bwd [{ln_rows},{LN_C}] + causal softmax fwd + composite bwd "
+                               f"[1,{heads},{SM_T},{SM_T}], {reps} reps in {t:.1f} s, single thread")
+
+    info = {"workload": "layernorm fwd+bwd [16384,768] + causal softmax fwd+bwd [16,12,1024,1024]",
+            "ln_shape": [LN_ROWS, LN_C], "softmax_shape": [SM_B, SM_H, SM_T, SM_T]}
+    return ops, info, cpu, keep, "pmc_traffic_bench.json"
+
+
+def wl_layernorm_cfg0(vh):
+    rows, C = 2048, 128
+    r = np.random.default_rng(SEED + 0)
+    x = r.standard_normal(size=(rows, C), dtype=np.float32)
+    w = (1 + 0.02 * r.standard_normal(C)).astype(np.float32)
+    b = (0.02 * r.standard_normal(C)).astype(np.float32)
+    dy = r.standard_normal(size=(rows, C), dtype=np.float32)
+    X, W, Bi, DY = (vh.DeviceBuffer.from_array(a) for a in (x, w, b, dy))
+    Y, DX = vh.DeviceBuffer(x.nbytes), vh.DeviceBuffer(x.nbytes)
+    DW, DB = vh.DeviceBuffer(w.nbytes), vh.DeviceBuffer(w.nbytes)
+    lf, lb = ln_bytes(rows, C)
+    ops = [("layernorm_fwd", lf, lambda i: vh.lib.vh_layernorm_fwd(X.ptr, W.ptr, Bi.ptr, Y.ptr, rows, C, 1e-5, None)),
+           ("layernorm_bwd", lb, lambda i: vh.lib.vh_layernorm_bwd(X.ptr, W.ptr, DY.ptr, DX.ptr, DW.ptr, DB.ptr,
+                                                                   rows, C, 1e-5, None, 0, None))]
+
+    def cpu(budget):
+        import oracle
+        t, reps = time_cpu(lambda: (oracle.layernorm(x, w, b, 1e-5), oracle.layernorm_backward(x, w, b, dy, 1e-5)),
+                           budget)
+        return (lf + lb) * reps / t, f"layernorm fwd+bwd [{rows},{C}] (the whole config), {reps} reps, single thread"
+
+    return ops, {"workload": "cfg[0] layernorm fwd+bwd [2048,128] (launch-bound, cache-resident)"}, cpu, \
+        (X, W, Bi, DY, Y, DX, DW, DB), None
+
+
+def wl_gelu_bias(vh):
+    rows, C = 16384, 3072
+    r = np.random.default_rng(SEED + 1)
+    bias = (0.02 * r.standard_normal(C)).astype(np.float32)
+    Bi = vh.DeviceBuffer.from_array(bias)
+    X = vh.DeviceBuffer.from_array(r.standard_normal(size=(rows, C), dtype=np.float32) * np.float32(1.5))
+    DY = vh.DeviceBuffer.from_array(r.standard_normal(size=(rows, C), dtype=np.float32))
+    Y, DX, DB = vh.DeviceBuffer(4 * rows * C), vh.DeviceBuffer(4 * rows * C), vh.DeviceBuffer(4 * C)
+    n = rows * C
+    fb, bb = 8 * n + 4 * C, 12 * n + 8 * C
+    nsc = vh.lib.vh_gelu_bias_bwd_scratch_bytes(rows, C)
+    SC = vh.DeviceBuffer(nsc)
+    ops = [("gelu_bias_fwd", fb, lambda i: vh.lib.vh_gelu_bias_fwd(X.ptr, Bi.ptr, Y.ptr, rows, C, None)),
+           ("gelu_bias_bwd", bb, lambda i: vh.lib.vh_gelu_bias_bwd(X.ptr, Bi.ptr, DY.ptr, DX.ptr, DB.ptr, rows, C,
+                                                                   SC.ptr, nsc, None))]
+
+    def cpu(budget):
+        import oracle
+        rc = np.random.default_rng(SEED + 1)
+        sr = 512
+        x = rc.standard_normal(size=(sr, C), dtype=np.float32) * np.float32(1.5)
+        dy = rc.standard_normal(size=(sr, C), dtype=np.float32)
+        t, reps = time_cpu(lambda: (oracle.gelu_bias_forward(x, bias), oracle.gelu_bias_backward(x, bias, dy)), budget)
+        return (20 * sr * C + 12 * C) * reps / t, (f"bias add + gelu fwd and mask*dy + bias reduce_to on "
+                                                   f"[{sr},{C}], {reps} reps, single thread")
+
+    return ops, {"workload": "cfg[1] gelu(x+bias) fwd+bwd [16384,3072]"}, cpu, (Bi, X, DY, Y, DX, DB, SC), None
+
+
+def _embedding(vh, zipf):
+    V, D, n = 50257, 768, 16384
+    r = np.random.default_rng(SEED + 3)
+    Wt = (0.02 * r.standard_normal(size=(V, D), dtype=np.float32))
+    ids = zipf_ids(r, n, V) if zipf else r.integers(0, V, size=n).astype(np.float32)
+    dy = r.standard_normal(size=(n, D), dtype=np.float32)
+    U = len(np.unique(ids))
+    I, Wd, DY = vh.DeviceBuffer.from_array(ids), vh.DeviceBuffer.from_array(Wt), vh.DeviceBuffer.from_array(dy)
+    OUT, DW = vh.DeviceBuffer(4 * n * D), vh.DeviceBuffer(4 * V * D)
+    nsc = vh.lib.vh_embedding_bwd_scratch_bytes(n, V, D)
+    SC = vh.DeviceBuffer(nsc)
+    fb = 4 * n + 4 * U * D + 4 * n * D
+    bb = 4 * n + 4 * n * D + 4 * V * D
+    ops = [("embedding_fwd", fb, lambda i: vh.lib.vh_embedding_fwd(I.ptr, Wd.ptr, OUT.ptr, n, V, D, None)),
+           ("embedding_bwd", bb, lambda i: vh.lib.vh_embedding_bwd(I.ptr, DY.ptr, DW.ptr, n, V, D, SC.ptr, nsc, None))]
+
+    def cpu(budget):
+        import oracle
+        t, reps = time_cpu(lambda: (oracle.embedding(ids, Wt), oracle.embedding_backward(ids, (V, D), dy)), budget)
+        return (fb + bb) * reps / t, f"the whole config (n={n}, V={V}, D={D}), {reps} reps, single thread"
+
+    kind = "Zipf(1.1)" if zipf else "uniform"
+    return ops, {"workload": f"cfg[3] embedding fwd+bwd, {kind} ids, V=50257 D=768 n=16384",
+                 "distinct_ids": U}, cpu, (I, Wd, DY, OUT, DW, SC), None
+
+
+def wl_embedding_uniform(vh):
+    return _embedding(vh, False)
+
+
+def wl_embedding_zipf(vh):
+    return _embedding(vh, True)
+
+
+def wl_cross_entropy(vh):
+    B, V = 16384, 50257
+    r = np.random.default_rng(SEED + 4)
+    L = vh.DeviceBuffer.from_array(r.standard_normal(size=(B, V), dtype=np.float32))
+    T = vh.DeviceBuffer.from_array(r.integers(0, V, size=B).astype(np.float32))
+    GO = vh.DeviceBuffer.from_array(np.float32([1.0]))
+    LOSS, DL = vh.DeviceBuffer(4), vh.DeviceBuffer(4 * B * V)
+    nsc = vh.lib.vh_cross_entropy_fwd_scratch_bytes(B)
+    SC = vh.DeviceBuffer(nsc)
+    fb, bb = 4 * B * V + 8 * B, 8 * B * V + 8 * B
+    ops = [("cross_entropy_fwd", fb, lambda i: vh.lib.vh_cross_entropy_fwd(L.ptr, T.ptr, LOSS.ptr, B, V, SC.ptr,
+                                                                           nsc, None)),
+           ("cross_entropy_bwd", bb, lambda i: vh.lib.vh_cross_entropy_bwd(L.ptr, T.ptr, GO.ptr, DL.ptr, B, V, None))]
+
+    def cpu(budget):
+        import oracle
+        rc = np.random.default_rng(SEED + 4)
+        sb_ = 64
+        lg = rc.standard_normal(size=(sb_, V), dtype=np.float32)
+        tg = rc.integers(0, V, size=sb_).astype(np.float32)
+        go = np.float32([1.0])
+        t, reps = time_cpu(lambda: (oracle.cross_entropy(lg, tg), oracle.cross_entropy_backward(lg, tg, go)), budget)
+        return (12 * sb_ * V + 16 * sb_) * reps / t, f"cross-entropy fwd+bwd on [{sb_},{V}], {reps} reps, single thread"
+
+    return ops, {"workload": "cross-entropy fwd+bwd over logits [16384,50257] (cfg[4] lm_head output)"}, cpu, \
+        (L, T, GO, LOSS, DL, SC), None
+
+
+WORKLOADS = {"ln_softmax": wl_ln_softmax, "layernorm_cfg0": wl_layernorm_cfg0, "gelu_bias": wl_gelu_bias,
+             "embedding_uniform": wl_embedding_uniform, "embedding_zipf": wl_embedding_zipf,
+             "cross_entropy": wl_cross_entropy}
 
 
 def main():
@@ -123,6 +299,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="ln_softmax", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -142,62 +319,35 @@ def main():
     if args.calibrate_copy:
         nb = 256 << 20
         src, dst = vh.DeviceBuffer(nb, zero=True), vh.DeviceBuffer(nb)
+        vh.sync()
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0, stream)
         for _ in range(4):
             vh.check(vh.lib.vh_d2d(dst.ptr, src.ptr, nb, None))
+        hip.record(e1, stream)
         vh.sync()
-        print(json.dumps({"calibrate_copy_bytes": nb, "copies": 4}), flush=True)
+        ms = hip.elapsed_ms(e0, e1)
+        print(json.dumps({"calibrate_copy_bytes": nb, "copies": 4,
+                          "copy_gbps": round(4 * 2 * nb / (ms / 1e3) / 1e9, 1)}), flush=True)
         return
-    r = np.random.default_rng(0x5EED0000 + 4)
 
-    # ---- inputs, resident in HBM before the timed region
-    ln_sets = []
-    w = (1 + 0.02 * r.standard_normal(LN_C)).astype(np.float32)
-    b = (0.02 * r.standard_normal(LN_C)).astype(np.float32)
-    W, Bi = vh.DeviceBuffer.from_array(w), vh.DeviceBuffer.from_array(b)
-    for _ in range(2):
-        x = r.standard_normal(size=(LN_ROWS, LN_C), dtype=np.float32)
-        dy = r.standard_normal(size=(LN_ROWS, LN_C), dtype=np.float32)
-        ln_sets.append(dict(x=vh.DeviceBuffer.from_array(x), dy=vh.DeviceBuffer.from_array(dy),
-                            y=vh.DeviceBuffer(x.nbytes), dx=vh.DeviceBuffer(x.nbytes),
-                            dw=vh.DeviceBuffer(w.nbytes), db=vh.DeviceBuffer(w.nbytes)))
-    ln_scratch_bytes = vh.lib.vh_layernorm_bwd_scratch_bytes(LN_ROWS, LN_C)
-    LNS = vh.DeviceBuffer(ln_scratch_bytes)
-    rs = np.random.default_rng(0x5EED0000 + 2)
-    s = causal_scores(rs, SM_B, SM_H, SM_T)
-    S = vh.DeviceBuffer.from_array(s)
-    del s
-    G = vh.DeviceBuffer.from_array(rs.standard_normal(size=(SM_B, SM_H, SM_T, SM_T), dtype=np.float32))
-    n_sm = SM_B * SM_H * SM_T * SM_T
-    P, DS = vh.DeviceBuffer(4 * n_sm), vh.DeviceBuffer(4 * n_sm)
-    rows_sm = SM_B * SM_H * SM_T
+    ops, info, cpu, keep, traffic_file = WORKLOADS[args.workload](vh)
     vh.sync()
-
-    names = ["layernorm_fwd", "softmax_fwd", "softmax_bwd", "layernorm_bwd"]
-
-    def step(i):
-        L = ln_sets[i % 2]
-        yield lambda: vh.lib.vh_layernorm_fwd(L["x"].ptr, W.ptr, Bi.ptr, L["y"].ptr, LN_ROWS, LN_C, 1e-5, None)
-        yield lambda: vh.lib.vh_softmax_fwd(S.ptr, P.ptr, rows_sm, SM_T, 1, None)
-        # The autograd Softmax arm saves the input x and recomputes y from it
-        # (crates/vearo-autograd/src/lib.rs:547-553); the fused kernel does the same.
-        yield lambda: vh.lib.vh_softmax_bwd(S.ptr, G.ptr, DS.ptr, rows_sm, SM_T, 1, 1, None)
-        yield lambda: vh.lib.vh_layernorm_bwd(L["x"].ptr, W.ptr, L["dy"].ptr, L["dx"].ptr, L["dw"].ptr,
-                                              L["db"].ptr, LN_ROWS, LN_C, 1e-5, LNS.ptr, ln_scratch_bytes, None)
-
+    names = [o[0] for o in ops]
     for i in range(args.warmup):
-        for call in step(i):
-            vh.check(call())
+        for _, _, call in ops:
+            vh.check(call(i))
     vh.sync()
 
     K = args.steps
-    ev = [[hip.event() for _ in range(len(names) + 1)] for _ in range(K)]
+    ev = [[hip.event() for _ in range(len(ops) + 1)] for _ in range(K)]
     hip.sync(stream)
     t0 = time.perf_counter()
     for i in range(K):
         e = ev[i]
         hip.record(e[0], stream)
-        for j, call in enumerate(step(i)):
-            vh.check(call())
+        for j, (_, _, call) in enumerate(ops):
+            vh.check(call(i))
             hip.record(e[j + 1], stream)
     hip.sync(stream)
     wall = time.perf_counter() - t0
@@ -207,25 +357,21 @@ def main():
     for i in range(K):
         for j, n in enumerate(names):
             per[n] += hip.elapsed_ms(ev[i][j], ev[i][j + 1])
-    lf, lbw = ln_bytes(LN_ROWS, LN_C)
-    sf, sbw = sm_bytes(SM_B, SM_H, SM_T)
-    nbytes = {"layernorm_fwd": lf, "softmax_fwd": sf, "softmax_bwd": sbw, "layernorm_bwd": lbw}
     kernels = {}
-    for n in names:
+    for n, nb, _ in ops:
         avg_s = per[n] / K / 1e3
-        gbps = nbytes[n] / avg_s / 1e9
-        kernels[n] = {"avg_us": round(avg_s * 1e6, 2), "bytes": nbytes[n], "gbps": round(gbps, 1),
+        gbps = nb / avg_s / 1e9
+        kernels[n] = {"avg_us": round(avg_s * 1e6, 2), "bytes": nb, "gbps": round(gbps, 1),
                       "frac": round(gbps / PEAK_GBPS, 4)}
-    step_bytes = sum(nbytes.values())
-    ms_per_step = wall / K * 1e3
+    step_bytes = sum(o[1] for o in ops)
     value = step_bytes / (wall / K) / 1e9
     dom = max(names, key=lambda n: per[n])
     # HBM traffic per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
     # passes over this same workload, scaled by the counters' reading of a copy of
-    # known size (profiles/pmc_traffic_bench.json); null when absent.
+    # known size (profiles/<file>.json); null when absent.
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "pmc_traffic_bench.json")
-    if os.path.exists(tpath):
+    tpath = os.path.join(ROOT, "profiles", traffic_file) if traffic_file else None
+    if tpath and os.path.exists(tpath):
         with open(tpath) as f:
             tk = json.load(f).get("kernels", {})
         for n in names:
@@ -234,19 +380,22 @@ def main():
         traffic = tk.get(dom, {}).get("traffic_bytes")
     roofline = {"bound": "hbm", "kernel": dom, "achieved": kernels[dom]["gbps"], "peak": PEAK_GBPS,
                 "unit": "GB/s", "frac": kernels[dom]["frac"], "traffic": traffic}
+    cpu_res = None
+    if not args.no_cpu:
+        rate, sample = cpu(args.cpu_seconds)
+        cpu_res = {"value": round(rate / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                   "sample": sample + "; GB/s counts the same algorithmic bytes as the GPU figure"}
+    info["bytes_per_step"] = step_bytes
     res = {
-        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K,
-        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "metric": METRIC if args.workload == "ln_softmax" else f"{args.workload} fwd+bwd HBM GB/s",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": round(wall / K * 1e3, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "layernorm fwd+bwd [16384,768] + causal softmax fwd+bwd [16,12,1024,1024]",
-                   "ln_shape": [LN_ROWS, LN_C], "softmax_shape": [SM_B, SM_H, SM_T, SM_T],
-                   "bytes_per_step": step_bytes},
-        "frac_of_peak": round(value / PEAK_GBPS, 4),
-        "kernels": kernels,
-        "roofline": roofline,
-        "cpu_baseline": None if args.no_cpu else cpu_baseline(args.cpu_seconds),
+        "config": info, "frac_of_peak": round(value / PEAK_GBPS, 4), "kernels": kernels,
+        "roofline": roofline, "cpu_baseline": cpu_res,
     }
     print(json.dumps(res), flush=True)
+    del keep
 
 
 if __name__ == "__main__":

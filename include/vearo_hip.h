@@ -162,14 +162,16 @@ int vh_softmax_bwd(const float* in, const float* dy, float* dx, int64_t rows,
 int vh_embedding_fwd(const float* ids, const float* W, float* out, int64_t n,
                      int64_t V, int64_t D, void* stream);
 /* dW[V, D] = dense scatter-add of dy[n, D] by token, written in full (rows no
- * token hits are 0). Sort-by-token segmented sum, no float atomics, same f32
- * order as the CPU loop. Replaces BackendOps.embedding_backward
- * (tensor.rs:1139; cpu:920-980; cuda:1412-1464).
- * scratch: NULL or vh_embedding_bwd_scratch_bytes(n, V) bytes. */
+ * token hits are 0). No float atomics, deterministic. Rows of tokens with at
+ * most 16 hits are summed in the CPU loop's exact order (bit-exact); rows of
+ * tokens with more hits are summed in position chunks of ~32 hits combined in
+ * chunk order. Replaces BackendOps.embedding_backward (tensor.rs:1139;
+ * cpu:920-980; cuda:1412-1464).
+ * scratch: NULL or vh_embedding_bwd_scratch_bytes(n, V, D) bytes. */
 int vh_embedding_bwd(const float* ids, const float* dy, float* dW, int64_t n,
                      int64_t V, int64_t D, void* scratch, size_t scratch_bytes,
                      void* stream);
-size_t vh_embedding_bwd_scratch_bytes(int64_t n, int64_t V);
+size_t vh_embedding_bwd_scratch_bytes(int64_t n, int64_t V, int64_t D);
 
 /* ----------------------------------------------- hot path: cross-entropy -- */
 

@@ -235,7 +235,18 @@ int main() {
     CHECK(vo_embedding(ids.data(), &il, wv.data(), &wl, out.data(), err, sizeof err) == 0, "emb");
     CHECK(vo_embedding_backward(ids.data(), &il, &wl, dyv.data(), &gl, dw.data(), err, sizeof err) == 0, "emb bwd");
     CHECK(I.embedding(W).to_vec_f32() == out, "embedding forward is bit-exact");
-    CHECK(I.embedding_backward(W, DY).to_vec_f32() == dw, "embedding backward is bit-exact");
+    // Rows of tokens with <= 16 hits are summed in the CPU's order (bit-exact);
+    // the heavy token 3 (60 hits) is summed in position chunks (tolerance).
+    const std::vector<float> gdw = I.embedding_backward(W, DY).to_vec_f32();
+    std::vector<int> hits(V, 0);
+    for (float f : ids) hits[(int)std::lround(f)]++;
+    for (int v = 0; v < V; ++v) {
+      const std::vector<float> g(gdw.begin() + v * D, gdw.begin() + (v + 1) * D);
+      const std::vector<float> c(dw.begin() + v * D, dw.begin() + (v + 1) * D);
+      if (hits[v] <= 16) CHECK(g == c, "light embedding-gradient row is bit-exact");
+      else expect_close(g, c, "heavy embedding-gradient row");
+    }
+    CHECK(hits[3] > 16, "the test covers a heavy row");
 
     const int B = 33, Vc = 517;
     auto lv = randn((size_t)B * Vc, 7, 2.0f);

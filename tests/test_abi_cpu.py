@@ -62,7 +62,7 @@ def test_scratch_size_queries_are_host_only():
     assert _abi.lib.vh_layernorm_bwd_scratch_bytes(16384, 768) >= 2 * 768 * 4
     assert _abi.lib.vh_layernorm_bwd_scratch_bytes(0, 768) == 0
     assert _abi.lib.vh_gelu_bias_bwd_scratch_bytes(16384, 3072) >= 3072 * 4
-    assert _abi.lib.vh_embedding_bwd_scratch_bytes(16384, 50257) >= 4 * (4 * 16384 + 3 * 50257)
+    assert _abi.lib.vh_embedding_bwd_scratch_bytes(16384, 50257, 768) >= 4 * (3 * 16384 + 2 * 50257)
     assert _abi.lib.vh_cross_entropy_fwd_scratch_bytes(16384) >= 16384 * 4
 
 
@@ -103,11 +103,11 @@ def launcher_kernel_names():
         for v in nv:
             names |= {f"vh_gelu_bias_fwd_n{v}_v{vw}", f"vh_gelu_bias_bwd_n{v}_v{vw}"}
         names |= {f"vh_gelu_fwd_v{vw}", f"vh_gelu_gradmul_v{vw}", f"vh_emb_fwd_v{vw}",
-                  f"vh_emb_segsum_v{vw}", f"vh_binary_contig_v{vw}"}
+                  f"vh_emb_rows_v{vw}", f"vh_binary_contig_v{vw}"}
     for v in [1, 2, 4, 8, 16, 24, 32, 40, 48, 50, 56, 64]:
         names |= {f"vh_xent_fwd_n{v}", f"vh_xent_bwd_n{v}"}
     names |= {"vh_xent_fwd_stream", "vh_xent_bwd_stream", "vh_xent_reduce", "vh_col_reduce",
-              "vh_emb_tokens", "vh_scan", "vh_emb_place", "vh_emb_sort_big", "vh_fill",
+              "vh_emb_tokens", "vh_emb_alloc", "vh_emb_place", "vh_fill",
               "vh_binary_strided_i32", "vh_binary_strided_i64", "vh_reduce_thread",
               "vh_reduce_wave", "vh_strided_copy_i32", "vh_strided_copy_i64"}
     return names

@@ -1,6 +1,7 @@
 """GPU parity: every hot-path entry point of libvearo_hip.so, called through the
-C ABI, against the CPU oracle on identical seeded inputs. Embedding forward and
-backward must be bit-exact; everything else within 1e-5 + 1e-4*|cpu|.
+C ABI, against the CPU oracle on identical seeded inputs. Embedding forward is
+bit-exact, and so are embedding-gradient rows of tokens with at most 16 hits
+(summed in the CPU's order); everything else within 1e-5 + 1e-4*|cpu|.
 Shapes cover the BASELINE configs (or a row-subset of them where the oracle
 would take minutes) plus the ragged / tiny / large-row variants of each kernel
 family. Full-size properties of the biggest configs run in test_properties_gpu.py."""
@@ -166,8 +167,24 @@ def zipf_ids(r, n, V, s=1.1):
     return np.searchsorted(cdf, r.random(n)).astype(np.float32)
 
 
+def check_embedding_grad(gpu, ids, dy, V):
+    """Rows of tokens with <= 16 hits must equal the oracle bit for bit (same f32
+    order as the CPU loop); rows of heavier tokens, summed in position chunks,
+    must be within tolerance of it (checked against float64 as well)."""
+    D = dy.shape[-1]
+    ref = O.embedding_backward(ids, (V, D), dy)
+    tok = np.floor(ids.reshape(-1).astype(np.float64) + 0.5).astype(np.int64)
+    counts = np.bincount(tok, minlength=V)
+    light = counts <= 16
+    np.testing.assert_array_equal(gpu[light], ref[light])
+    if (~light).any():
+        ref64 = np.zeros((V, D))
+        np.add.at(ref64, tok, dy.reshape(-1, D).astype(np.float64))
+        assert_parity(gpu[~light], ref[~light], ref64[~light], name="heavy rows")
+
+
 @pytest.mark.parametrize("dist", ["uniform", "zipf"])
-def test_embedding_config3_bit_exact(vh, dist):
+def test_embedding_config3(vh, dist):
     print(f"embedding config3 {dist}", flush=True)
     r = rng(3)
     V, D, n = 50257, 768, 16384
@@ -175,16 +192,18 @@ def test_embedding_config3_bit_exact(vh, dist):
     ids = (r.integers(0, V, size=n).astype(np.float32) if dist == "uniform" else zipf_ids(r, n, V))
     dy = r.normal(size=(n, D)).astype(np.float32)
     I, Wd, DY = dev(vh, ids), dev(vh, W), dev(vh, dy)
-    OUT, DW = out(vh, (n, D)), out(vh, (V, D))
+    OUT, DW, DW2 = out(vh, (n, D)), out(vh, (V, D)), out(vh, (V, D))
     vh.check(vh.lib.vh_embedding_fwd(I.ptr, Wd.ptr, OUT.ptr, n, V, D, None))
     vh.check(vh.lib.vh_embedding_bwd(I.ptr, DY.ptr, DW.ptr, n, V, D, None, 0, None))
-    np.testing.assert_array_equal(fetch(vh, OUT, (n, D)), O.embedding(ids, W))
-    # Same per-row summation order as the CPU loop: bit-exact, not just close.
-    np.testing.assert_array_equal(fetch(vh, DW, (V, D)), O.embedding_backward(ids, (V, D), dy))
+    vh.check(vh.lib.vh_embedding_bwd(I.ptr, DY.ptr, DW2.ptr, n, V, D, None, 0, None))
+    np.testing.assert_array_equal(fetch(vh, OUT, (n, D)), O.embedding(ids, W))  # forward: bit-exact
+    g = fetch(vh, DW, (V, D))
+    np.testing.assert_array_equal(g, fetch(vh, DW2, (V, D)))                     # deterministic
+    check_embedding_grad(g, ids, dy, V)
 
 
 @pytest.mark.parametrize("n,V,D", [(1, 3, 2), (10, 4, 5), (300, 7, 64), (5000, 3, 33),
-                                   (9000, 2, 8), (100, 100000, 1)])
+                                   (9000, 2, 8), (100, 100000, 1), (20000, 1, 1030), (640, 10, 4)])
 def test_embedding_shapes(vh, n, V, D):
     r = rng(5)
     ids = r.integers(0, V, size=n).astype(np.float32) + r.uniform(-0.49, 0.49, size=n).astype(np.float32)
@@ -196,7 +215,19 @@ def test_embedding_shapes(vh, n, V, D):
     vh.check(vh.lib.vh_embedding_fwd(I.ptr, Wd.ptr, OUT.ptr, n, V, D, None))
     vh.check(vh.lib.vh_embedding_bwd(I.ptr, DY.ptr, DW.ptr, n, V, D, None, 0, None))
     np.testing.assert_array_equal(fetch(vh, OUT, (n, D)), O.embedding(ids, W))
-    np.testing.assert_array_equal(fetch(vh, DW, (V, D)), O.embedding_backward(ids, (V, D), dy))
+    check_embedding_grad(fetch(vh, DW, (V, D)), ids, dy, V)
+
+
+def test_embedding_heavy_token_clustered(vh):
+    # A heavy token whose hits all sit at the end of the positions: the chunks
+    # before them hold nothing, the last chunks hold everything.
+    n, V, D = 4096, 50, 96
+    ids = np.concatenate([np.arange(n - 700) % 49 + 1, np.zeros(700)]).astype(np.float32)
+    r = rng(8)
+    dy = r.normal(size=(n, D)).astype(np.float32)
+    I, DY, DW = dev(vh, ids), dev(vh, dy), out(vh, (V, D))
+    vh.check(vh.lib.vh_embedding_bwd(I.ptr, DY.ptr, DW.ptr, n, V, D, None, 0, None))
+    check_embedding_grad(fetch(vh, DW, (V, D)), ids, dy, V)
 
 
 @pytest.mark.parametrize("bad,msg", [(-1.0, "Token ID cannot be negative: -1"),

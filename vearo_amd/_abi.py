@@ -97,7 +97,7 @@ SIGNATURES = {
         c_int,
         [fp, fp, fp, c_int64, c_int64, c_int64, c_void_p, c_size_t, c_void_p],
     ),
-    "vh_embedding_bwd_scratch_bytes": (c_size_t, [c_int64, c_int64]),
+    "vh_embedding_bwd_scratch_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
     "vh_cross_entropy_fwd": (
         c_int,
         [fp, fp, fp, c_int64, c_int64, c_void_p, c_size_t, c_void_p],

@@ -1,4 +1,4 @@
-// embedding.h -- embedding gather forward and sort-by-token segmented-sum backward
+// embedding.h -- embedding gather forward and deterministic scatter-add backward
 // for gfx950.
 //
 // Forward (vearo-backend-cpu embedding, crates/vearo-backend-cpu/src/lib.rs:860-918):
@@ -6,19 +6,63 @@
 // loads/stores when D % 4 == 0. ids are f32 as in the reference API.
 //
 // Backward (lib.rs:920-980): dW = zeros[V, D]; dW[tok_i] += dy[i] for i ascending.
-// Atomic-free on the floats, deterministic, and bit-exact with the CPU's order:
-//   1. emb_tokens : validate/round ids, integer histogram of tokens
-//   2. scan       : exclusive prefix sum -> CSR offsets [V+1]
-//   3. emb_place  : drop each position into its token's segment
-//   4. emb_sort_big: sort the positions of every segment longer than 64
-//                   ascending (workgroup bitonic network in LDS)
-//   5. emb_segsum : one wave per vocabulary row: sort a short segment in
-//                   registers, sum its dy rows in ascending position order (the
-//                   same f32 order as the CPU loop), or write zeros
-// so dW is written exactly once (dense, 4*V*D bytes) and dy read once.
-// Integer atomics in steps 1 and 3 only count; the float sums never use atomics.
+// No float atomics; dW is written exactly once (dense, 4*V*D bytes), dy read once.
+//   1. emb_tokens : validate/round ids; integer histogram of tokens, with the
+//                   duplicates inside each wave merged first (one atomic per
+//                   distinct token per wave, so hot tokens do not serialise)
+//   2. emb_alloc  : rows with more than EMB_LIGHT (16) hits become "heavy": an
+//                   entry and one task per 32 hits (ranked in position order),
+//                   claimed with one atomic per wave
+//   3. emb_place  : light positions drop into their row's 16 fixed slots; heavy
+//                   hits are counted per block of positions (512 or more)
+//   4. emb_rows   : the leading workgroups run heavy tasks while the rest stream
+//      + heavy      the vocabulary rows, one wave per row: zeros for an unused
+//                   row; for a light row, its <= 16 positions sorted in registers
+//                   and the dy rows added in ascending position order from 0.0 --
+//                   the CPU loop's exact f32 order, so those rows are bit-exact.
+//                   A heavy task gathers the positions of its 32 ranks (visiting
+//                   only blocks that hold them), sums their rows in order into a
+//                   partial row; the last task of each group of 8 adds the group's
+//                   partials in order, and the last group adds the group sums in
+//                   order into dW (a fixed grouping of the same sum:
+//                   deterministic, within f32 rounding of the CPU's order).
 #pragma once
 #include "common.h"
+
+#define EMB_LIGHT 16
+#define EMB_CHUNK_HITS 32
+#define EMB_GROUP 8
+#define EMB_Q 3  // units per lane per pass: 3 x 64 x 4 floats covers D = 768
+
+// acc[q] += rows[r][q] for the first `cnt` of 4 rows, in row order; the loads of
+// all rows are issued before any add so a wave pays one memory latency per
+// batch of 4 rows instead of one per row. NT selects streaming loads (dy, read
+// once) over plain ones (partial rows, just written by other waves).
+template <int VW, bool NT>
+VH_DEV void emb_add_rows(Unit<VW> (&acc)[EMB_Q], const float* const (&src)[4], int cnt, int u0, int lane, int U) {
+  Unit<VW> d[4][EMB_Q];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int q = 0; q < EMB_Q; ++q) {
+      const int u = u0 + lane + q * 64;
+      if (r < cnt && u < U)
+        d[r][q] = NT ? load_stream<VW>(src[r] + u * VW) : load_unit<VW>(src[r] + u * VW);
+      else
+        d[r][q] = zero_unit<VW>();
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if (r < cnt) {
+#pragma unroll
+      for (int q = 0; q < EMB_Q; ++q) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) acc[q].v[j] += d[r][q].v[j];
+      }
+    }
+  }
+}
 
 // One wave per token, 4 waves per 256-thread workgroup.
 template <int VW>
@@ -42,65 +86,13 @@ VH_DEV void emb_fwd_impl(const EmbFwdArgs& a) {
   for (int u = lane; u < U; u += 64) store_stream<VW>(o + u * VW, load_unit<VW>(w + u * VW));
 }
 
-VH_DEV void emb_tokens_impl(const EmbTokArgs& a) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= a.n) return;
-  const float tv = a.ids[i];
-  const int32_t t = checked_index(tv, a.V);
-  a.tok[i] = t;
-  if (t < 0) {
-    atomicMin(&a.err->token, err_pack(i, tv));
-    a.err->token_bound = (unsigned)a.V;
-  } else {
-    atomicAdd(&a.counts[t], 1);
-  }
-}
-
-// Single-workgroup exclusive scan of n int32 (1024 threads, contiguous chunk per
-// thread), total stored at data[n].
-VH_DEV void scan_impl(const ScanArgs& a) {
-  // Also lists the entries whose count exceeds 64 (long embedding segments).
-  __shared__ int32_t part[1024];
-  const int t = threadIdx.x;
-  const int chunk = (a.n + 1023) / 1024;
-  const int s0 = t * chunk;
-  int s1 = s0 + chunk;
-  if (s1 > a.n) s1 = a.n;
-  int32_t local = 0;
-  for (int i = s0; i < s1; ++i) local += a.data[i];
-  part[t] = local;
-  __syncthreads();
-  // Hillis-Steele inclusive scan over the 1024 partials.
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int32_t v = t >= off ? part[t - off] : 0;
-    __syncthreads();
-    part[t] += v;
-    __syncthreads();
-  }
-  int32_t run = t > 0 ? part[t - 1] : 0;
-  for (int i = s0; i < s1; ++i) {
-    const int32_t c = a.data[i];
-    a.data[i] = run;
-    run += c;
-    if (a.big && c > 64) a.big[atomicAdd(a.nbig, 1)] = i;
-  }
-  if (t == 1023) a.data[a.n] = part[1023];
-}
-
-VH_DEV void emb_place_impl(const EmbPlaceArgs& a) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= a.n) return;
-  const int32_t t = a.tok[i];
-  if (t < 0) return;
-  const int32_t slot = a.offsets[t] + atomicAdd(&a.cursor[t], 1);
-  a.pos[slot] = (int32_t)i;
-}
-
-// Bitonic sort of one value per lane across the wave (ascending by lane).
+// Bitonic sort of one value per lane within each group of KMAX lanes
+// (ascending by lane; KMAX = 64 sorts the whole wave).
+template <int KMAX>
 VH_DEV int32_t wave_bitonic_sort(int32_t v) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int k = 2; k <= 64; k <<= 1) {
+  for (int k = 2; k <= KMAX; k <<= 1) {
 #pragma unroll
     for (int j = k >> 1; j > 0; j >>= 1) {
       const int32_t o = __shfl_xor(v, j, 64);
@@ -114,87 +106,287 @@ VH_DEV int32_t wave_bitonic_sort(int32_t v) {
   return v;
 }
 
-// Step 4 (segments longer than 64 only; shorter ones are sorted in registers by
-// emb_segsum). The scan kernel lists the long segments; a fixed grid of
-// workgroups walks that list, each sorting one segment at a time with a bitonic
-// network over a padded power-of-two buffer: LDS when it fits, else a private
-// slice [2*s0, 2*s0 + P) of the global staging buffer (P < 2m, so slices of
-// different segments never overlap and stay inside its 2n entries).
-#define EMB_SORT_LDS 8192
-
-VH_DEV void emb_sort_big_impl(const EmbSortArgs& a) {
-  __shared__ int32_t buf[EMB_SORT_LDS];
-  const int32_t nbig = *a.nbig;
-  for (int32_t idx = blockIdx.x; idx < nbig; idx += gridDim.x) {
-    const int32_t v = a.big[idx];
-    const int32_t s0 = a.offsets[v];
-    const int32_t m = a.offsets[v + 1] - s0;
-    int32_t* seg = a.pos + s0;
-    int P = 128;
-    while (P < m) P <<= 1;
-    int32_t* b = (P <= EMB_SORT_LDS) ? buf : a.gbuf + 2 * (int64_t)s0;
-    for (int i = threadIdx.x; i < P; i += blockDim.x) b[i] = i < m ? seg[i] : 0x7FFFFFFF;
-    __syncthreads();
-    for (int k = 2; k <= P; k <<= 1) {
-      for (int j = k >> 1; j > 0; j >>= 1) {
-        for (int i = threadIdx.x; i < P; i += blockDim.x) {
-          const int l = i ^ j;
-          if (l > i) {
-            const int32_t x = b[i], y = b[l];
-            const bool up = (i & k) == 0;
-            if ((x > y) == up) {
-              b[i] = y;
-              b[l] = x;
-            }
-          }
-        }
-        __syncthreads();
-      }
+// Step 1. 256-thread workgroups over positions.
+VH_DEV void emb_tokens_impl(const EmbTokArgs& a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int32_t t = -1;
+  if (i < a.n) {
+    const float tv = a.ids[i];
+    t = checked_index(tv, a.V);
+    a.tok[i] = t;
+    if (t < 0) {
+      atomicMin(&a.err->token, err_pack(i, tv));
+      a.err->token_bound = (unsigned)a.V;
     }
-    for (int i = threadIdx.x; i < m; i += blockDim.x) seg[i] = b[i];
-    __syncthreads();
+  }
+  // Merge duplicates within the wave: sort the 64 tokens, one atomic per run.
+  const int32_t s = wave_bitonic_sort<64>(t < 0 ? INT32_MAX : t);
+  const int32_t prev = __shfl(s, (lane + 63) & 63, 64);
+  const bool boundary = lane == 0 || prev != s;
+  const unsigned long long heads = __ballot(boundary);
+  if (boundary && s != INT32_MAX) {
+    const unsigned long long above = lane == 63 ? 0ull : heads & (~0ull << (lane + 1));
+    const int next = above ? __builtin_ctzll(above) : 64;
+    atomicAdd(&a.counts[s], next - lane);
   }
 }
 
-// Step 5. One wave per vocabulary row, 4 waves per workgroup. Segments of up to
-// 64 positions are sorted here in registers; longer ones arrive sorted.
-template <int VW>
-VH_DEV void emb_segsum_impl(const EmbSegArgs& a) {
+// Step 2. One thread per vocabulary row. Rows with more than EMB_LIGHT hits are
+// registered as heavy: an entry, a run of ceil(hits/32) tasks, a zeroed
+// per-block hit-count row and zeroed completion counters. Entries and tasks are
+// claimed with one atomic per wave (a wave prefix sum, then one atomicAdd of the
+// totals); their order varies run to run but no row's result depends on it.
+VH_DEV void emb_alloc_impl(const EmbAllocArgs& a) {
   const int lane = threadIdx.x & 63;
-  const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (v >= a.V) return;
-  const int32_t s0 = a.offsets[v];
-  const int32_t m = a.offsets[v + 1] - s0;
-  const int D = a.D;
-  const int U = D / VW;
-  float* o = a.dW + v * D;
-  int32_t sorted = 0x7FFFFFFF;
-  if (m <= 64) {
-    sorted = lane < m ? a.pos[s0 + lane] : 0x7FFFFFFF;
-    sorted = wave_bitonic_sort(sorted);
+  const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int32_t c = v < a.V ? a.counts[v] : 0;
+  const bool heavy = c > EMB_LIGHT;
+  const int32_t nch = heavy ? (c + EMB_CHUNK_HITS - 1) / EMB_CHUNK_HITS : 0;
+  // Low 32 bits: heavy rows; high 32 bits: tasks.
+  const int64_t mine = heavy ? (((int64_t)nch << 32) | 1) : 0;
+  int64_t inc = mine;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int64_t u = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += u;
   }
-  for (int u0 = 0; u0 < U; u0 += 64 * 4) {
-    // Up to 4 units per lane per pass keep 4 independent loads in flight.
-    Unit<VW> acc[4];
+  int32_t hbase = 0, tbase = 0;
+  if (lane == 63 && inc != 0) {
+    hbase = atomicAdd(&a.ctr[0], (int32_t)(inc & 0xffffffff));
+    tbase = atomicAdd(&a.ctr[1], (int32_t)(inc >> 32));
+  }
+  hbase = __shfl(hbase, 63, 64);
+  tbase = __shfl(tbase, 63, 64);
+  if (v >= a.V) return;
+  int32_t h = -1;
+  if (heavy) {
+    const int64_t ex = inc - mine;
+    h = hbase + (int32_t)(ex & 0xffffffff);
+    const int32_t tb = tbase + (int32_t)(ex >> 32);
+    a.heavy[4 * h + 0] = (int32_t)v;
+    a.heavy[4 * h + 1] = tb;
+    a.heavy[4 * h + 2] = nch;
+    a.heavy[4 * h + 3] = c;
+    for (int32_t k = 0; k < nch; ++k) {
+      a.taskmap[tb + k] = h;
+      a.gdone[tb + k] = 0;
+    }
+    for (int32_t b = 0; b < a.nblk; ++b) a.blkcnt[(int64_t)h * a.nblk + b] = 0;
+    a.hdone[h] = 0;
+  }
+  a.heavy_index[v] = h;
+}
+
+// Step 3. One thread per position: light positions go to their row's slots (at
+// most 16 atomics per row); heavy hits are counted per 2^blk_shift-position block, with
+// one atomic per (heavy token, wave) after merging the wave's duplicates.
+VH_DEV void emb_place_impl(const EmbPlaceArgs& a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int32_t h = -1;
+  if (i < a.n) {
+    const int32_t t = a.tok[i];
+    if (t >= 0) {
+      h = a.heavy_index[t];
+      if (h < 0) a.pos[(int64_t)t * EMB_LIGHT + atomicAdd(&a.cursor[t], 1)] = (int32_t)i;
+    }
+  }
+  const int32_t s = wave_bitonic_sort<64>(h < 0 ? INT32_MAX : h);
+  const int32_t prev = __shfl(s, (lane + 63) & 63, 64);
+  const bool boundary = lane == 0 || prev != s;
+  const unsigned long long heads = __ballot(boundary);
+  if (boundary && s != INT32_MAX) {
+    const unsigned long long above = lane == 63 ? 0ull : heads & (~0ull << (lane + 1));
+    const int next = above ? __builtin_ctzll(above) : 64;
+    // The wave's 64 positions share one block (blocks hold >= 64 positions).
+    const int64_t blk = (i - lane) >> a.blk_shift;
+    atomicAdd(&a.blkcnt[(int64_t)s * a.nblk + blk], next - lane);
+  }
+}
+
+// Index of the n-th (0-based) set bit of m; requires n < popcount(m).
+VH_DEV int nth_set_bit(unsigned long long m, int n) {
+  int pos = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) acc[q] = zero_unit<VW>();
-    for (int32_t k = 0; k < m; ++k) {
-      const int32_t p = m <= 64 ? __shfl(sorted, k, 64) : a.pos[s0 + k];
-      const float* src = a.dy + (int64_t)p * D;
+  for (int w = 32; w >= 1; w >>= 1) {
+    const int c = __popcll(m & ((1ull << w) - 1));
+    if (n >= c) {
+      n -= c;
+      m >>= w;
+      pos += w;
+    }
+  }
+  return pos;
+}
+
+// dst = sum over c < cnt of rows base + c * stride, added in c order from 0.0.
+template <int VW>
+VH_DEV void emb_sum_rows(const float* base, int64_t stride, int cnt, float* dst, bool stream_out, int lane,
+                         int U) {
+  for (int u0 = 0; u0 < U; u0 += 64 * EMB_Q) {
+    Unit<VW> acc[EMB_Q];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int u = u0 + lane + q * 64;
-        if (u < U) {
-          const Unit<VW> d = load_stream<VW>(src + u * VW);
+    for (int q = 0; q < EMB_Q; ++q) acc[q] = zero_unit<VW>();
+    for (int c = 0; c < cnt; c += 4) {
+      const float* src[4];
 #pragma unroll
-          for (int j = 0; j < VW; ++j) acc[q].v[j] += d.v[j];
+      for (int r = 0; r < 4; ++r) src[r] = base + (int64_t)(c + r < cnt ? c + r : c) * stride;
+      emb_add_rows<VW, false>(acc, src, cnt - c < 4 ? cnt - c : 4, u0, lane, U);
+    }
+#pragma unroll
+    for (int q = 0; q < EMB_Q; ++q) {
+      const int u = u0 + lane + q * 64;
+      if (u < U) {
+        if (stream_out)
+          store_stream<VW>(dst + u * VW, acc[q]);
+        else
+          store_unit<VW>(dst + u * VW, acc[q]);
+      }
+    }
+  }
+}
+
+// Heavy task k: the hits of rank [32c, 32c+32) of its token (ranks in position
+// order). Lane j first gathers the position of the j-th of them, visiting only
+// blocks whose hit count overlaps the rank window; then the dy rows are summed
+// in position order into partial[k]. Completion is a two-level tree in fixed
+// order: the last task of each group of EMB_GROUP sums the group's partials
+// into the group's first slot, the last group sums the group slots into dW.
+template <int VW>
+VH_DEV void emb_heavy_task(const EmbSegArgs& a, int64_t k, int lane) {
+  const int U = a.D / VW;
+  const int32_t h = a.taskmap[k];
+  const int32_t tok = a.heavy[4 * h + 0], tb = a.heavy[4 * h + 1], nch = a.heavy[4 * h + 2];
+  const int32_t m = a.heavy[4 * h + 3];
+  const int32_t c = (int32_t)(k - tb);
+  const int32_t r0 = c * EMB_CHUNK_HITS;
+  const int32_t r1 = min(r0 + EMB_CHUNK_HITS, m);
+  const int32_t* cnt = a.blkcnt + (int64_t)h * a.nblk;
+  int32_t rr = 0;      // hits in the blocks before the current 64-block chunk
+  int32_t got = 0;     // positions gathered so far (wave-uniform)
+  int32_t mypos = 0;   // lane j < got: the j-th gathered position
+  for (int32_t b0 = 0; b0 < a.nblk && rr < r1; b0 += 64) {
+    const int32_t cb = b0 + lane < a.nblk ? cnt[b0 + lane] : 0;
+    int32_t inc = cb;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int32_t u = __shfl_up(inc, off, 64);
+      if (lane >= off) inc += u;
+    }
+    const int32_t before = rr + inc - cb;  // hits before this lane's block
+    unsigned long long want = __ballot(cb > 0 && before < r1 && before + cb > r0);
+    while (want) {
+      const int l = __builtin_ctzll(want);
+      want &= want - 1;
+      int32_t br = __shfl(before, l, 64);  // rank of the block's first hit
+      const int64_t p_end = min(((int64_t)(b0 + l) + 1) << a.blk_shift, a.n);
+      for (int64_t pb = (int64_t)(b0 + l) << a.blk_shift; pb < p_end && br < r1; pb += 512) {
+        int32_t tk[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          const int64_t p = pb + g * 64 + lane;
+          tk[g] = p < p_end ? a.tok[p] : -1;
+        }
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          const unsigned long long mask = __ballot(tk[g] == tok);
+          const int hits = __popcll(mask);
+          // This group's ranks are [br, br + hits); take those in [r0, r1).
+          const int lo = max(r0 - br, 0);
+          const int hi = min(r1 - br, hits);
+          if (hi > lo) {
+            if (lane >= got && lane < got + (hi - lo))
+              mypos = (int32_t)(pb + g * 64 + nth_set_bit(mask, lane - got + lo));
+            got += hi - lo;
+          }
+          br += hits;
         }
       }
     }
+    rr += __shfl(inc, 63, 64);
+  }
+  float* part = a.partial + k * (int64_t)a.D;
+  for (int u0 = 0; u0 < U; u0 += 64 * EMB_Q) {
+    Unit<VW> acc[EMB_Q];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < EMB_Q; ++q) acc[q] = zero_unit<VW>();
+    for (int j = 0; j < got; j += 4) {  // ascending positions, 4 rows per batch
+      const float* src[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) src[r] = a.dy + (int64_t)__shfl(mypos, j + r < got ? j + r : j, 64) * a.D;
+      emb_add_rows<VW, true>(acc, src, got - j < 4 ? got - j : 4, u0, lane, U);
+    }
+#pragma unroll
+    for (int q = 0; q < EMB_Q; ++q) {
       const int u = u0 + lane + q * 64;
-      if (u < U) store_stream<VW>(o + u * VW, acc[q]);
+      if (u < U) store_unit<VW>(part + u * VW, acc[q]);
     }
   }
+  // Level 1: the group's last task sums the group's partials in task order.
+  const int32_t g = c / EMB_GROUP;
+  const int32_t g0 = tb + g * EMB_GROUP;
+  const int32_t gsize = min(EMB_GROUP, nch - g * EMB_GROUP);
+  const int32_t ngrp = (nch + EMB_GROUP - 1) / EMB_GROUP;
+  __threadfence();
+  int32_t done = 0;
+  if (lane == 0) done = atomicAdd(&a.gdone[g0], 1);
+  done = __shfl(done, 0, 64);
+  if (done != gsize - 1) return;
+  __threadfence();
+  float* row = a.dW + (int64_t)tok * a.D;
+  if (ngrp == 1) {
+    emb_sum_rows<VW>(a.partial + (int64_t)g0 * a.D, a.D, gsize, row, true, lane, U);
+    return;
+  }
+  // Each lane reads its own units of slot g0 before it overwrites them.
+  emb_sum_rows<VW>(a.partial + (int64_t)g0 * a.D, a.D, gsize, a.partial + (int64_t)g0 * a.D, false, lane, U);
+  // Level 2: the last group sums the group slots in group order.
+  __threadfence();
+  if (lane == 0) done = atomicAdd(&a.hdone[h], 1);
+  done = __shfl(done, 0, 64);
+  if (done != ngrp - 1) return;
+  __threadfence();
+  emb_sum_rows<VW>(a.partial + (int64_t)tb * a.D, (int64_t)EMB_GROUP * a.D, ngrp, row, true, lane, U);
+}
+
+// Step 4. Blocks [0, heavy_blocks): heavy tasks, one per wave, strided over the
+// device-side task count; dispatched first, so they overlap the row stream.
+// Blocks beyond: one wave per vocabulary row (zeros, or a light row's bit-exact
+// sequential sum; heavy rows are left to their tasks).
+template <int VW>
+VH_DEV void emb_rows_impl(const EmbSegArgs& a) {
+  const int lane = threadIdx.x & 63;
+  const int U = a.D / VW;
+  if ((int)blockIdx.x >= a.heavy_blocks) {
+    const int64_t v = ((int64_t)blockIdx.x - a.heavy_blocks) * 4 + (threadIdx.x >> 6);
+    if (v >= a.V) return;
+    const int32_t m = a.counts[v];
+    if (m > EMB_LIGHT) return;
+    float* o = a.dW + v * a.D;
+    int32_t sorted = INT32_MAX;
+    if (m > 0) sorted = lane < m ? a.pos[v * EMB_LIGHT + lane] : INT32_MAX;
+    if (m > 1) sorted = wave_bitonic_sort<EMB_LIGHT>(sorted);
+    for (int u0 = 0; u0 < U; u0 += 64 * EMB_Q) {
+      Unit<VW> acc[EMB_Q];
+#pragma unroll
+      for (int q = 0; q < EMB_Q; ++q) acc[q] = zero_unit<VW>();
+      for (int32_t k = 0; k < m; k += 4) {  // ascending positions, 4 rows per batch
+        const float* src[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) src[r] = a.dy + (int64_t)__shfl(sorted, k + r < m ? k + r : k, 64) * a.D;
+        emb_add_rows<VW, true>(acc, src, m - k < 4 ? m - k : 4, u0, lane, U);
+      }
+#pragma unroll
+      for (int q = 0; q < EMB_Q; ++q) {
+        const int u = u0 + lane + q * 64;
+        if (u < U) store_stream<VW>(o + u * VW, acc[q]);
+      }
+    }
+    return;
+  }
+  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t nworkers = (int64_t)a.heavy_blocks * 4;
+  const int32_t ntasks = a.ctr[1];
+  for (int64_t k = wid; k < ntasks; k += nworkers) emb_heavy_task<VW>(a, k, lane);
 }

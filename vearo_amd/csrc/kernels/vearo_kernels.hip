@@ -111,11 +111,10 @@ GB_CFG(K_GB_BWD, 4)
 extern "C" __global__ void __launch_bounds__(256) vh_emb_fwd_v1(EmbFwdArgs a) { emb_fwd_impl<1>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_emb_fwd_v4(EmbFwdArgs a) { emb_fwd_impl<4>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_emb_tokens(EmbTokArgs a) { emb_tokens_impl(a); }
-extern "C" __global__ void __launch_bounds__(1024) vh_scan(ScanArgs a) { scan_impl(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_emb_alloc(EmbAllocArgs a) { emb_alloc_impl(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_emb_place(EmbPlaceArgs a) { emb_place_impl(a); }
-extern "C" __global__ void __launch_bounds__(256) vh_emb_sort_big(EmbSortArgs a) { emb_sort_big_impl(a); }
-extern "C" __global__ void __launch_bounds__(256) vh_emb_segsum_v1(EmbSegArgs a) { emb_segsum_impl<1>(a); }
-extern "C" __global__ void __launch_bounds__(256) vh_emb_segsum_v4(EmbSegArgs a) { emb_segsum_impl<4>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_emb_rows_v1(EmbSegArgs a) { emb_rows_impl<1>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_emb_rows_v4(EmbSegArgs a) { emb_rows_impl<4>(a); }
 
 // Cross-entropy
 #define XE_CFG(M) M(1) M(2) M(4) M(8) M(16) M(24) M(32) M(40) M(48) M(50) M(56) M(64)

@@ -25,18 +25,31 @@ VH_DEV int32_t xent_target(const XentArgs& a, int64_t row) {
   return t;
 }
 
+// Word 3 of a raw (untyped, stride 0) buffer resource on CDNA: bounds-checked
+// by byte offset against num_records, out-of-range loads return 0 and
+// out-of-range stores are dropped.
+#define VH_BUF_WORD3 0x00020000
+
 template <int NV, bool BWD>
 VH_DEV void xent_cached_impl(const XentArgs& a) {
   __shared__ float red[16];
   const int64_t row = blockIdx.x;
   const int V = a.V;
   const float* lr = a.logits + row * V;
+  // One buffer resource per row: base and bound live in SGPRs, the unit offset
+  // k*4096 goes in the scalar offset field, so the cached row costs one VGPR
+  // per float and no per-load address registers.
+  const __amdgpu_buffer_rsrc_t rin =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(lr), 0, V * 4, VH_BUF_WORD3);
+  const int voff = threadIdx.x * 4;
   float v[NV];
   float m = -INFINITY;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int c = threadIdx.x + k * 1024;
-    v[k] = c < V ? __builtin_nontemporal_load(lr + c) : -INFINITY;
+    // The builtin returns the raw 32 bits: reinterpret, do not convert.
+    const float x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rin, voff, k * 4096, 0));
+    v[k] = c < V ? x : -INFINITY;
     if (v[k] > m) m = v[k];
   }
   m = team_max<1024>(m, red);
@@ -55,15 +68,16 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
   } else {
     const float go = *a.grad_out;
     const float Bf = (float)a.B;
-    float* o = a.out + row * V;
+    const __amdgpu_buffer_rsrc_t rout =
+        __builtin_amdgcn_make_buffer_rsrc(a.out + row * V, 0, V * 4, VH_BUF_WORD3);
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int c = threadIdx.x + k * 1024;
-      if (c < V) {
-        const float p = v[k] / s;
-        const float ind = c == t ? 1.0f : 0.0f;
-        __builtin_nontemporal_store(go * (p - ind) / Bf, o + c);
-      }
+      const float p = v[k] / s;
+      const float ind = c == t ? 1.0f : 0.0f;
+      // Units past the row end fall outside the resource and are dropped.
+      const float g = go * (p - ind) / Bf;
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, g), rout, voff, k * 4096, 0);
     }
   }
 }

@@ -689,32 +689,53 @@ int vh_embedding_fwd(const float* ids, const float* W, float* out, int64_t n, in
 }
 
 namespace {
+// Heavy tokens have more than 16 hits, so at most n/17 of them; each gets
+// ceil(hits/32) tasks, so at most n/32 + n/17 + 1 tasks in all.
+constexpr int64_t kEmbLight = 16, kEmbChunkHits = 32;
+// Heavy hits are counted per block of 2^blk_shift positions: 512 unless the
+// [heavy entries][blocks] table would pass 4M entries, then larger.
+constexpr int kEmbMinBlkShift = 9;
+constexpr int64_t kEmbMaxBlkTable = int64_t(1) << 22;
 struct EmbScratchLayout {
-  size_t tok, counts, cursor, pos, gbuf, big, nbig, total;
+  size_t tok, counts, cursor, ctr, zero_end, heavy_index, heavy, taskmap, hdone, gdone, blkcnt, pos, partial,
+      total;
+  int64_t nblk;
+  int blk_shift;
 };
-EmbScratchLayout emb_layout(int64_t n, int64_t V) {
+EmbScratchLayout emb_layout(int64_t n, int64_t V, int64_t D) {
   EmbScratchLayout L;
+  const int64_t heavy_max = n / (kEmbLight + 1) + 1;
+  const int64_t tasks_max = n / kEmbChunkHits + heavy_max + 1;
+  L.blk_shift = kEmbMinBlkShift;
+  while (heavy_max * cdiv(n, int64_t(1) << L.blk_shift) > kEmbMaxBlkTable) ++L.blk_shift;
+  L.nblk = cdiv(n, int64_t(1) << L.blk_shift);
   size_t o = 0;
-  auto take = [&](size_t ints) {
+  auto take = [&](size_t elems) {
     size_t at = o;
-    o += align256(ints * sizeof(int32_t));
+    o += align256(elems * 4);
     return at;
   };
   L.tok = take((size_t)n);
-  L.counts = take((size_t)V + 1);
+  L.counts = take((size_t)V);
   L.cursor = take((size_t)V);
-  L.nbig = take(1);
-  L.pos = take((size_t)n);
-  L.gbuf = take(2 * (size_t)n);
-  L.big = take((size_t)V);
+  L.ctr = take(4);
+  L.zero_end = o;  // counts .. ctr are zeroed per call
+  L.heavy_index = take((size_t)V);
+  L.heavy = take(4 * (size_t)heavy_max);
+  L.taskmap = take((size_t)tasks_max);
+  L.hdone = take((size_t)heavy_max);
+  L.gdone = take((size_t)tasks_max);
+  L.blkcnt = take((size_t)heavy_max * (size_t)L.nblk);
+  L.pos = take((size_t)V * kEmbLight);
+  L.partial = take((size_t)tasks_max * (size_t)D);
   L.total = o;
   return L;
 }
 }  // namespace
 
-size_t vh_embedding_bwd_scratch_bytes(int64_t n, int64_t V) {
-  if (n <= 0 || V < 0) return 0;
-  return emb_layout(n, V).total;
+size_t vh_embedding_bwd_scratch_bytes(int64_t n, int64_t V, int64_t D) {
+  if (n <= 0 || V < 0 || D < 0) return 0;
+  return emb_layout(n, V, D).total;
 }
 
 int vh_embedding_bwd(const float* ids, const float* dy, float* dW, int64_t n, int64_t V, int64_t D,
@@ -727,31 +748,31 @@ int vh_embedding_bwd(const float* ids, const float* dy, float* dW, int64_t n, in
   if (!ids || (D > 0 && !dy)) return fail(VH_ERR_INVALID, "vh_embedding_bwd: null pointer");
   if (V >= INT32_MAX || D > INT32_MAX || n >= INT32_MAX / 2)
     return fail(VH_ERR_UNSUPPORTED, "vh_embedding_bwd: size exceeds int32");
-  const EmbScratchLayout L = emb_layout(n, V);
+  const EmbScratchLayout L = emb_layout(n, V, D);
   Scratch sc;
   VH_TRY(sc.get(scratch, scratch_bytes, L.total));
   char* base = static_cast<char*>(sc.p);
-  int32_t* tok = reinterpret_cast<int32_t*>(base + L.tok);
-  int32_t* counts = reinterpret_cast<int32_t*>(base + L.counts);
-  int32_t* cursor = reinterpret_cast<int32_t*>(base + L.cursor);
-  int32_t* nbig = reinterpret_cast<int32_t*>(base + L.nbig);
-  int32_t* pos = reinterpret_cast<int32_t*>(base + L.pos);
-  int32_t* gbuf = reinterpret_cast<int32_t*>(base + L.gbuf);
-  int32_t* big = reinterpret_cast<int32_t*>(base + L.big);
-  // counts, cursor and nbig are contiguous: one fill of zeros (0.0f bits == int 0).
-  VH_TRY(fill(counts, 0.0f, (int64_t)((L.pos - L.counts) / 4), s));
-  EmbTokArgs k1{ids, tok, counts, g_rt.err, n, (int32_t)V};
+  auto I = [&](size_t off) { return reinterpret_cast<int32_t*>(base + off); };
+  // counts, cursor and the counters are contiguous: one fill of zeros
+  // (0.0f has the bits of int 0).
+  VH_TRY(fill(I(L.counts), 0.0f, (int64_t)((L.zero_end - L.counts) / 4), s));
+  EmbTokArgs k1{ids, I(L.tok), I(L.counts), g_rt.err, n, (int32_t)V};
   VH_TRY(launch("vh_emb_tokens", (unsigned)cdiv(n, 256), 1, 256, 0, s, k1));
   if (V == 0 || D == 0) return VH_OK;  // ids validated, nothing to write
-  ScanArgs k2{counts, big, nbig, (int32_t)V};
-  VH_TRY(launch("vh_scan", 1, 1, 1024, 0, s, k2));
-  EmbPlaceArgs k3{tok, counts, cursor, pos, n};
+  EmbAllocArgs k2{I(L.counts), I(L.heavy_index), I(L.heavy), I(L.taskmap), I(L.blkcnt), I(L.hdone),
+                  I(L.gdone), I(L.ctr), (int32_t)V, (int32_t)L.nblk};
+  VH_TRY(launch("vh_emb_alloc", (unsigned)cdiv(V, 256), 1, 256, 0, s, k2));
+  EmbPlaceArgs k3{I(L.tok), I(L.heavy_index), I(L.cursor), I(L.pos), I(L.blkcnt), n, (int32_t)L.nblk,
+                  L.blk_shift};
   VH_TRY(launch("vh_emb_place", (unsigned)cdiv(n, 256), 1, 256, 0, s, k3));
-  EmbSortArgs k4{counts, pos, gbuf, big, nbig};
-  VH_TRY(launch("vh_emb_sort_big", 64, 1, 256, 0, s, k4));
   const bool vec = D % 4 == 0 && aligned16(dy) && aligned16(dW);
-  EmbSegArgs k5{counts, pos, dy, dW, (int32_t)V, (int32_t)D};
-  return launch(vec ? "vh_emb_segsum_v4" : "vh_emb_segsum_v1", (unsigned)cdiv(V, 4), 1, 256, 0, s, k5);
+  // Up to 1024 worker waves for heavy tasks (there are at most tasks_max).
+  const int64_t heavy_blocks = std::min<int64_t>(256, cdiv(n / kEmbChunkHits + n / (kEmbLight + 1) + 2, 4));
+  EmbSegArgs k4{I(L.counts), I(L.pos), I(L.tok), I(L.heavy), I(L.taskmap), I(L.blkcnt), I(L.hdone),
+                I(L.gdone), I(L.ctr), reinterpret_cast<float*>(base + L.partial), dy, dW, n, (int32_t)V,
+                (int32_t)D, (int32_t)L.nblk, L.blk_shift, (int32_t)heavy_blocks};
+  return launch(vec ? "vh_emb_rows_v4" : "vh_emb_rows_v1", (unsigned)(heavy_blocks + cdiv(V, 4)), 1, 256, 0,
+                s, k4);
 }
 
 // --------------------------------------------------------- cross-entropy --

@@ -95,42 +95,55 @@ struct EmbFwdArgs {
 struct EmbTokArgs {
   const float* ids;
   int32_t* tok;      // [n] validated token ids (-1 on error)
-  int32_t* counts;   // [V + 1] histogram, later exclusive offsets
+  int32_t* counts;   // [V] hits per vocabulary row (zeroed by the host)
   VhErrRecord* err;
   int64_t n;
   int32_t V;
 };
 
-struct ScanArgs {
-  int32_t* data;  // in-place exclusive scan of [n] int32, total written to data[n]
-  int32_t* big;   // optional: receives the indices whose count exceeds 64
-  int32_t* nbig;  // optional: number of entries written to big (zeroed by the host)
-  int32_t n;
+struct EmbAllocArgs {
+  const int32_t* counts;  // [V] hits per vocabulary row
+  int32_t* heavy_index;   // [V] heavy entry or -1
+  int32_t* heavy;         // [4 * max] token, first task, task count, hits
+  int32_t* taskmap;       // [tasks] heavy entry of each task
+  int32_t* blkcnt;        // [max][nblk] heavy hits per position block
+  int32_t* hdone;         // [max] finished task groups per heavy entry
+  int32_t* gdone;         // [tasks] finished tasks per group of 8 (at the group's first task)
+  int32_t* ctr;           // [2]: heavy entries, tasks (zeroed by the host)
+  int32_t V;
+  int32_t nblk;
 };
 
 struct EmbPlaceArgs {
   const int32_t* tok;
-  const int32_t* offsets;  // [V + 1]
-  int32_t* cursor;         // [V] zeroed
-  int32_t* pos;            // [n] positions grouped by token
+  const int32_t* heavy_index;
+  int32_t* cursor;  // [V] zeroed
+  int32_t* pos;     // [V][16] light positions per vocabulary row (unordered)
+  int32_t* blkcnt;
   int64_t n;
-};
-
-struct EmbSortArgs {
-  const int32_t* offsets;  // [V + 1]
-  int32_t* pos;            // [n] grouped by token
-  int32_t* gbuf;           // [2n] staging for segments too long for LDS
-  const int32_t* big;      // long segments listed by the scan
-  const int32_t* nbig;
+  int32_t nblk;
+  int32_t blk_shift;  // positions per block = 1 << blk_shift (>= 64)
 };
 
 struct EmbSegArgs {
-  const int32_t* offsets;  // [V + 1]
-  const int32_t* pos;      // [n] grouped by token (unordered within a group)
+  const int32_t* counts;
+  const int32_t* pos;
+  const int32_t* tok;
+  const int32_t* heavy;
+  const int32_t* taskmap;
+  const int32_t* blkcnt;
+  int32_t* hdone;
+  int32_t* gdone;
+  const int32_t* ctr;
+  float* partial;  // [tasks][D] heavy partial rows
   const float* dy;
   float* dW;
+  int64_t n;
   int32_t V;
   int32_t D;
+  int32_t nblk;
+  int32_t blk_shift;
+  int32_t heavy_blocks;  // leading workgroups that run heavy tasks
 };
 
 struct XentArgs {
