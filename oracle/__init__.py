@@ -29,6 +29,17 @@ class Layout(ctypes.Structure):
     ]
 
 
+class GptConfig(ctypes.Structure):
+    """vo_gpt_config: SimpleGPT with one block (B x S ids, width D, H heads,
+    MLP width F, vocabulary V, max_seq_len P)."""
+    _fields_ = [(n, c_int64) for n in ("B", "S", "D", "H", "F", "V", "P")]
+
+
+GPT_PARAM_NAMES = ("wte", "wpe", "ln1_w", "ln1_b", "q_w", "q_b", "k_w", "k_b", "v_w", "v_b",
+                   "o_w", "o_b", "ln2_w", "ln2_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b",
+                   "lnf_w", "lnf_b", "lm_w")
+
+
 class Panic(RuntimeError):
     """The reference CPU backend would panic with this message."""
 
@@ -58,13 +69,23 @@ def _load():
         "vo_gelu_bias_forward": [f, f, c_int64, c_int64, f],
         "vo_gelu_bias_backward": [f, f, f, c_int64, c_int64, f, f],
         "vo_format_f32": [c_float, c_char_p, c_size_t],
+        "vo_set_threads": [c_int],
+        "vo_matmul": [f, L, f, L, f] + err,
+        "vo_fused_attention": [f, f, f, c_int64, c_int64, c_int64, c_int64, f, L, f],
+        "vo_fused_attention_backward": [f, f, f, c_int64, c_int64, c_int64, c_int64, f, L, f, f,
+                                        f, f],
+        "vo_adamw_step": [f, f, f, f, c_int64, c_int, c_float, c_float, c_float, c_float,
+                          c_float],
+        "vo_gpt_param_numel": [POINTER(GptConfig), POINTER(c_int64)],
+        "vo_gpt_step": [POINTER(GptConfig), POINTER(c_void_p), f, f, f, POINTER(c_void_p)] + err,
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = None if name in (
             "vo_gelu", "vo_gelu_grad_mask", "vo_gelu_bias_forward",
-            "vo_gelu_bias_backward", "vo_format_f32") else c_int
+            "vo_gelu_bias_backward", "vo_format_f32", "vo_set_threads", "vo_adamw_step",
+            "vo_gpt_param_numel") else c_int
     return lib
 
 
@@ -269,3 +290,84 @@ def format_f32(v: float) -> str:
     buf = ctypes.create_string_buffer(64)
     lib.vo_format_f32(c_float(v), buf, 64)
     return buf.value.decode()
+
+
+def set_threads(n: int) -> None:
+    lib.vo_set_threads(int(n))
+
+
+def matmul(a, b):
+    """Batched matmul with broadcast batch dims (operands made contiguous first,
+    as the reference does)."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    batch = np.broadcast_shapes(a.shape[:-2], b.shape[:-2]) if a.ndim >= 2 and b.ndim >= 2 else ()
+    shape = tuple(batch) + ((a.shape[-2], b.shape[-1]) if a.ndim >= 2 and b.ndim >= 2 else ())
+    out = np.zeros(shape, np.float32)
+    ob = out if out.size else np.zeros(1, np.float32)
+    ab = a if a.size else np.zeros(1, np.float32)
+    bb = b if b.size else np.zeros(1, np.float32)
+    _call(lib.vo_matmul, _ptr(ab), layout(a.shape), _ptr(bb), layout(b.shape), _ptr(ob))
+    return out
+
+
+def _att_args(q, k, v, mask):
+    q, k, v = (np.ascontiguousarray(t, np.float32) for t in (q, k, v))
+    if mask is None:
+        return q, k, v, None, None
+    m = np.ascontiguousarray(mask, np.float32)
+    return q, k, v, m, layout(m.shape)
+
+
+def fused_attention(q, k, v, mask=None):
+    q, k, v, m, ml = _att_args(q, k, v, mask)
+    B, H, S, Dk = q.shape
+    out = np.zeros_like(q)
+    lib.vo_fused_attention(_ptr(q), _ptr(k), _ptr(v), B, H, S, Dk,
+                           _ptr(m) if m is not None else None, ml, _ptr(out))
+    return out
+
+
+def fused_attention_backward(q, k, v, mask, go):
+    q, k, v, m, ml = _att_args(q, k, v, mask)
+    go = np.ascontiguousarray(go, np.float32)
+    B, H, S, Dk = q.shape
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(q), np.zeros_like(q)
+    lib.vo_fused_attention_backward(_ptr(q), _ptr(k), _ptr(v), B, H, S, Dk,
+                                    _ptr(m) if m is not None else None, ml, _ptr(go),
+                                    _ptr(dq), _ptr(dk), _ptr(dv))
+    return dq, dk, dv
+
+
+def adamw_step(p, g, m, v, t, lr, beta1, beta2, eps, wd):
+    """In place on float32 contiguous arrays p, m, v."""
+    for a in (p, m, v):
+        assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+    g = np.ascontiguousarray(g, np.float32)
+    lib.vo_adamw_step(_ptr(p), _ptr(g), _ptr(m), _ptr(v), p.size, int(t), c_float(lr),
+                      c_float(beta1), c_float(beta2), c_float(eps), c_float(wd))
+
+
+def gpt_param_shapes(cfg: GptConfig):
+    D, F, V, P = cfg.D, cfg.F, cfg.V, cfg.P
+    return [(V, D), (P, D), (D,), (D,), (D, D), (D,), (D, D), (D,), (D, D), (D,), (D, D), (D,),
+            (D,), (D,), (F, D), (F,), (D, F), (D,), (D,), (D,), (V, D)]
+
+
+def gpt_step(cfg: GptConfig, params, ids, targets, grads: bool = True):
+    """(loss, [grad per parameter] or None) of one SimpleGPT forward(+backward)."""
+    params = [np.ascontiguousarray(p, np.float32) for p in params]
+    shapes = gpt_param_shapes(cfg)
+    assert len(params) == len(shapes)
+    for p, sh in zip(params, shapes):
+        assert p.shape == sh, (p.shape, sh)
+    ids = np.ascontiguousarray(ids, np.float32)
+    targets = np.ascontiguousarray(targets, np.float32)
+    pp = (c_void_p * len(params))(*[p.ctypes.data for p in params])
+    loss = np.zeros(1, np.float32)
+    gs = gp = None
+    if grads:
+        gs = [np.zeros(sh, np.float32) for sh in shapes]
+        gp = (c_void_p * len(gs))(*[g.ctypes.data for g in gs])
+    _call(lib.vo_gpt_step, ctypes.byref(cfg), pp, _ptr(ids), _ptr(targets), _ptr(loss), gp)
+    return float(loss[0]), gs

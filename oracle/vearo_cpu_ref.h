@@ -107,6 +107,53 @@ void vo_format_f32(float v, char* buf, size_t len);
 /* Layout helpers. */
 void vo_contiguous_layout(vo_layout* l, int rank, const int64_t* dims);
 
+/* ---- part 2 (vearo_cpu_gpt.c): matmul, fused attention, AdamW, SimpleGPT ---- */
+
+/* Threads used by the blocked loops (default: $VO_THREADS, $OMP_NUM_THREADS,
+ * else all online CPUs). Thread count never changes a result. */
+void vo_set_threads(int n);
+
+/* Batched matmul with broadcast batch dims (cpu:266-417); lhs, rhs contiguous
+ * (the reference makes them contiguous first); out contiguous
+ * [broadcast batch..., M, N]. */
+int vo_matmul(const float* lhs, const vo_layout* ll, const float* rhs, const vo_layout* rl,
+              float* out, char* err, size_t errlen);
+
+/* Fused attention forward / backward (cpu:2366-2630). q, k, v, go, out, dq,
+ * dk, dv: contiguous [B, H, S, Dk]. mask: NULL or contiguous, right-aligned to
+ * rank 4 and broadcast (cpu:2395-2404). */
+int vo_fused_attention(const float* q, const float* k, const float* v, int64_t B, int64_t H,
+                       int64_t S, int64_t Dk, const float* mask, const vo_layout* ml, float* out);
+int vo_fused_attention_backward(const float* q, const float* k, const float* v, int64_t B,
+                                int64_t H, int64_t S, int64_t Dk, const float* mask,
+                                const vo_layout* ml, const float* go, float* dq, float* dk,
+                                float* dv);
+
+/* Tensor::adamw_step on one parameter (tensor.rs:931-986), t >= 1. */
+void vo_adamw_step(float* p, const float* g, float* m, float* v, int64_t n, int t, float lr,
+                   float beta1, float beta2, float eps, float wd);
+
+/* SimpleGPT with one TransformerBlock (nn:666-791): B x S token ids, model
+ * width D, H heads, MLP width F, vocabulary V, P = max_seq_len. */
+typedef struct {
+  int64_t B, S, D, H, F, V, P;
+} vo_gpt_config;
+
+/* Parameters in SimpleGPT::parameters() order (nn:797-807). */
+enum {
+  VO_P_WTE, VO_P_WPE, VO_P_LN1_W, VO_P_LN1_B, VO_P_Q_W, VO_P_Q_B, VO_P_K_W, VO_P_K_B,
+  VO_P_V_W, VO_P_V_B, VO_P_O_W, VO_P_O_B, VO_P_LN2_W, VO_P_LN2_B, VO_P_FC1_W, VO_P_FC1_B,
+  VO_P_FC2_W, VO_P_FC2_B, VO_P_LNF_W, VO_P_LNF_B, VO_P_LM_W, VO_GPT_NPARAMS
+};
+void vo_gpt_param_numel(const vo_gpt_config* c, int64_t* numel);
+
+/* Forward (loss, the mean cross-entropy as one float) and, when grads is not
+ * NULL, the autograd backward into grads[i] (same shapes as params[i]),
+ * following the reverse tape order of autograd:429-760. The causal mask is the
+ * model's own [S, S] tensor with -1e9 above the diagonal (nn:763-771). */
+int vo_gpt_step(const vo_gpt_config* c, const float* const* params, const float* ids,
+                const float* targets, float* loss, float* const* grads, char* err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -132,5 +132,124 @@ G.update({"bin_a": f32(a), "bin_b": f32(b)})
 A, B = f32(a).astype(np.float64), f32(b).astype(np.float64)
 G.update({"bin_add": A + B, "bin_sub": A - B, "bin_mul": A * B, "bin_div": A / B})
 
+# ------------------------------------------------------------------- matmul
+# Batched matmul with broadcast batch dims (cpu:266-417): torch.matmul in f64.
+for tag, sa, sb in (("mm2", (5, 7), (7, 3)), ("mm3", (2, 5, 7), (7, 4)),
+                    ("mmb", (2, 1, 4, 6), (3, 6, 5))):
+    a, b = f32(rng.normal(size=sa)), f32(rng.normal(size=sb))
+    G.update({f"{tag}_a": a, f"{tag}_b": b,
+              f"{tag}_out": torch.matmul(t64(a), t64(b)).numpy()})
+
+
+# ---------------------------------------------------------- fused attention
+# Unfused reference formula in f64: softmax(q k^T / sqrt(dk) + mask) v, and its
+# autograd gradients for an upstream gradient go.
+def add_attention(tag, q, k, v, mask, go):
+    q, k, v, go = f32(q), f32(k), f32(v), f32(go)
+    Q, K, Vt = t64(q, True), t64(k, True), t64(v, True)
+    s = Q @ K.transpose(-1, -2) / math.sqrt(q.shape[-1])
+    if mask is not None:
+        s = s + t64(f32(mask))
+        G[f"{tag}_mask"] = f32(mask)
+    out = torch.softmax(s, -1) @ Vt
+    out.backward(t64(go))
+    G.update({f"{tag}_q": q, f"{tag}_k": k, f"{tag}_v": v, f"{tag}_go": go,
+              f"{tag}_out": out.detach().numpy(), f"{tag}_dq": Q.grad.numpy(),
+              f"{tag}_dk": K.grad.numpy(), f"{tag}_dv": Vt.grad.numpy()})
+
+
+def causal_mask(S):
+    m = np.zeros((S, S))
+    m[np.triu_indices(S, 1)] = -1e9
+    return m
+
+
+# Known-answer inputs of crates/vearo/tests/fused_attention_parity.rs:13-47:
+# B=H=2, S=4, DK=8, q/k/v = fill(n, phase), upstream grad = sin(0.19 i) + 1.5.
+def kat_fill(n, phase):
+    x = np.arange(n, dtype=np.float32)
+    return (np.sin(x * np.float32(0.37) + np.float32(phase)) * np.float32(0.5)
+            + np.cos(x * np.float32(0.11) + np.float32(phase)) * np.float32(0.25)).astype(np.float32)
+
+
+n_kat = 2 * 2 * 4 * 8
+add_attention("attkat", kat_fill(n_kat, 0.0).reshape(2, 2, 4, 8), kat_fill(n_kat, 1.3).reshape(2, 2, 4, 8),
+              kat_fill(n_kat, 2.7).reshape(2, 2, 4, 8), causal_mask(4),
+              (np.sin(np.arange(n_kat, dtype=np.float32) * np.float32(0.19)) + np.float32(1.5)).reshape(2, 2, 4, 8))
+add_attention("attc", rng.normal(size=(1, 3, 17, 16)), rng.normal(size=(1, 3, 17, 16)),
+              rng.normal(size=(1, 3, 17, 16)), causal_mask(17), rng.normal(size=(1, 3, 17, 16)))
+add_attention("attm", rng.normal(size=(2, 2, 9, 8)), rng.normal(size=(2, 2, 9, 8)),
+              rng.normal(size=(2, 2, 9, 8)), rng.normal(size=(2, 1, 9, 9)), rng.normal(size=(2, 2, 9, 8)))
+add_attention("attn", rng.normal(size=(1, 2, 6, 4)), rng.normal(size=(1, 2, 6, 4)),
+              rng.normal(size=(1, 2, 6, 4)), None, rng.normal(size=(1, 2, 6, 4)))
+
+
+# ----------------------------------------------------------- SimpleGPT step
+# nn:666-791 with one block, written independently in torch f64: loss and the
+# gradient of every parameter, then one AdamW step (tensor.rs:967-986) and the
+# loss after it.
+def gpt_forward(P, ids, targets, B, S, D, H):
+    def ln(x, w, b):
+        return torch.nn.functional.layer_norm(x, (D,), w, b, 1e-5)
+
+    def lin(x, w, b=None):
+        y = x @ w.T
+        return y + b if b is not None else y
+
+    (wte, wpe, l1w, l1b, qw, qb, kw, kb, vw, vb, ow, ob, l2w, l2b, f1w, f1b, f2w, f2b,
+     lfw, lfb, lmw) = P
+    h = wte[ids] + wpe[torch.arange(S)].unsqueeze(0)
+    x1 = ln(h, l1w, l1b)
+
+    def heads(t):
+        return t.reshape(B, S, H, D // H).transpose(1, 2)
+
+    q, k, v = heads(lin(x1, qw, qb)), heads(lin(x1, kw, kb)), heads(lin(x1, vw, vb))
+    s = q @ k.transpose(-1, -2) / math.sqrt(D // H) + torch.tensor(causal_mask(S))
+    a = (torch.softmax(s, -1) @ v).transpose(1, 2).reshape(B, S, D)
+    h = h + lin(a, ow, ob)
+    m = torch.nn.functional.gelu(lin(ln(h, l2w, l2b), f1w, f1b), approximate="tanh")
+    h = h + lin(m, f2w, f2b)
+    logits = lin(ln(h, lfw, lfb).reshape(B * S, D), lmw)
+    return torch.nn.functional.cross_entropy(logits, targets.reshape(-1))
+
+
+def add_gpt(tag, B, S, D, H, F, V, scale):
+    shapes = [(V, D), (S, D), (D,), (D,), (D, D), (D,), (D, D), (D,), (D, D), (D,), (D, D), (D,),
+              (D,), (D,), (F, D), (F,), (D, F), (D,), (D,), (D,), (V, D)]
+    params = []
+    for i, sh in enumerate(shapes):
+        if i in (2, 12, 18):
+            params.append(f32(1 + 0.1 * rng.normal(size=sh)))
+        elif i in (3, 13, 19):
+            params.append(f32(0.1 * rng.normal(size=sh)))
+        else:
+            params.append(f32(scale * rng.normal(size=sh)))
+    ids = rng.integers(0, V, size=(B, S))
+    tg = rng.integers(0, V, size=(B, S))
+    P = [t64(p, True) for p in params]
+    loss = gpt_forward(P, torch.tensor(ids), torch.tensor(tg), B, S, D, H)
+    loss.backward()
+    lr, b1, b2, eps, wd = 0.02, 0.9, 0.95, 1e-8, 0.01
+    new = []
+    for p in P:
+        g = p.grad.detach()
+        m, v = (1 - b1) * g, (1 - b2) * g * g
+        mh, vh = m / (1 - b1), v / (1 - b2)
+        q = p.detach() - lr * wd * p.detach()
+        new.append(q - lr * mh / (vh.sqrt() + eps))
+    loss1 = gpt_forward(new, torch.tensor(ids), torch.tensor(tg), B, S, D, H)
+    G[f"{tag}_cfg"] = np.array([B, S, D, H, F, V, S], np.int64)
+    G[f"{tag}_ids"] = f32(ids)
+    G[f"{tag}_targets"] = f32(tg)
+    G[f"{tag}_loss"] = np.float64(loss.item())
+    G[f"{tag}_loss1"] = np.float64(loss1.item())
+    for i, (p, t) in enumerate(zip(params, P)):
+        G[f"{tag}_p{i}"] = p
+        G[f"{tag}_g{i}"] = t.grad.numpy()
+
+
+add_gpt("gpt", B=2, S=8, D=16, H=2, F=32, V=40, scale=0.3)
+
 np.savez_compressed(OUT, **G)
 print(f"wrote {OUT} ({os.path.getsize(OUT)} bytes, {len(G)} arrays)")
