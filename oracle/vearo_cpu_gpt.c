@@ -274,7 +274,7 @@ static inline float mask_at(const att_ctx* c, int64_t b, int64_t h, int64_t i, i
  * exp and sequential sum, inv_sum = 1/(sum + 1e-9), p = e * inv_sum).
  * kT is K of this head transposed to [Dk][S] so the j loop vectorises; each
  * dot still runs d ascending. */
-__attribute__((target_clones("arch=haswell", "default"))) static void att_probs(
+__attribute__((target_clones("fma", "default"))) static void att_probs(
     const att_ctx* c, int64_t b, int64_t h, int64_t i, const float* qrow, const float* kT, float* scores) {
   const int64_t S = c->S, Dk = c->Dk;
   const float scale = 1.0f / sqrtf((float)Dk);
@@ -306,7 +306,7 @@ static void transpose_head(const float* src, int64_t S, int64_t Dk, float* dst) 
 }
 
 /* out[i][d] = sum_j p_ij.mul_add(v[j][d], .) for j ascending (cpu:2460-2468). */
-__attribute__((target_clones("arch=haswell", "default"))) static void att_out_row(const float* p,
+__attribute__((target_clones("fma", "default"))) static void att_out_row(const float* p,
                                                                                 const float* V, int64_t S,
                                                                                 int64_t Dk, float* out) {
   for (int64_t d = 0; d < Dk; ++d) out[d] = 0.0f;
@@ -338,7 +338,7 @@ static void att_fwd_task(void* p, int64_t begin, int64_t end) {
  * s = sum_j dp_j.mul_add(p_j); ds_j = p_j * (dp_j - s);
  * dq[i][d] = (sum_j ds_j.mul_add(k[j][d])) * scale;
  * dv[j][d] = p_j.mul_add(go[d], dv[j][d]); dk[j][d] = (ds_j*scale).mul_add(q[d], dk[j][d]). */
-__attribute__((target_clones("arch=haswell", "default"))) static void att_bwd_row(
+__attribute__((target_clones("fma", "default"))) static void att_bwd_row(
     const float* p, const float* gorow, const float* qrow, const float* vT, const float* K, int64_t S,
     int64_t Dk, float scale, float* dp, float* dqrow, float* dK, float* dV) {
   for (int64_t j = 0; j < S; ++j) dp[j] = 0.0f;
