@@ -212,6 +212,87 @@ int vh_reduce(int mean, const float* x, const vh_layout* xl, int dim, float* out
  * host round-trip of Tensor::contiguous (tensor.rs:349-368). */
 int vh_strided_copy(const float* src, const vh_layout* sl, float* dst, void* stream);
 
+/* Sum of the rows of x[rows, C] into out[C]: the reduce_to of a [rows, C]
+ * gradient onto a broadcast [C] bias (autograd:316-361, run on the host there).
+ * Fixed grouping (per-workgroup row chains, then a fixed-order column sum):
+ * deterministic, within f32 rounding of the CPU's single chain.
+ * scratch: NULL or vh_sum_rows_scratch_bytes(rows, C) bytes. */
+int vh_sum_rows(const float* x, int64_t rows, int64_t C, float* out, void* scratch,
+                size_t scratch_bytes, void* stream);
+size_t vh_sum_rows_scratch_bytes(int64_t rows, int64_t C);
+
+/* ------------------------------- config[4] block step: matmul and attention -- */
+
+/* vh_gemm_desc.causal: the structure of an attention score block. Skipped
+ * parts are exactly zero (or never read), so no result changes. */
+#define VH_GEMM_DENSE 0
+#define VH_GEMM_SKIP_UPPER 1 /* C[m, n] with n > m is not needed (tiles above the diagonal are skipped) */
+#define VH_GEMM_K_LE_M 2     /* A[m, k] == 0 for k > m (M == K) */
+#define VH_GEMM_K_GE_M 3     /* A[m, k] == 0 for k < m (M == K) */
+
+/* C[m, n] = (C[m, n] +) alpha * sum_k A[m, k] B[k, n] (+ E[m, n]) over two batch
+ * dims, on the f32 matrix cores. The epilogue order is v = acc*alpha;
+ * v = v + E; v = C + v, i.e. the separate scale / mask / bias-add / gradient
+ * accumulation ops the reference applies after its matmul. */
+typedef struct vh_gemm_desc {
+  int64_t M, N, K;
+  const float* a;
+  int64_t a_sm, a_sk; /* A[m, k] = a[m*a_sm + k*a_sk]; a_sm == 1 or a_sk == 1 */
+  const float* b;
+  int64_t b_sk, b_sn; /* B[k, n] = b[k*b_sk + n*b_sn]; b_sk == 1 or b_sn == 1 */
+  float* c;
+  int64_t c_sm;       /* C[m, n] = c[m*c_sm + n] */
+  int64_t batch[2];   /* batch dims (1 when unused) */
+  int64_t a_sb[2], b_sb[2], c_sb[2]; /* batch strides (0 broadcasts) */
+  const float* e;     /* optional addend, NULL for none */
+  int64_t e_sm, e_sn;
+  int64_t e_sb[2];
+  float alpha;
+  int32_t accumulate; /* 1: add into C */
+  int32_t causal;     /* VH_GEMM_* */
+} vh_gemm_desc;
+int vh_gemm(const vh_gemm_desc* d, void* stream);
+
+/* out = lhs @ rhs with broadcast batch dims; any strides (operands with no
+ * unit stride in their last two dims are copied first, as the reference makes
+ * both contiguous); out is contiguous [batch..., M, N]. Replaces
+ * BackendOps.matmul (tensor.rs:1121, 1475-1495; cpu:266-417; cuda:914-1010). */
+int vh_matmul(const float* lhs, const vh_layout* ll, const float* rhs,
+              const vh_layout* rl, float* out, void* stream);
+
+/* Scaled dot-product attention over [B, H, S, Dk] layouts (any strides, unit
+ * stride on Dk): out = softmax(q k^T / sqrt(Dk) + mask) v, with the CPU fused
+ * kernel's normalisation p = e * (1/(sum + 1e-9)). mask: NULL or any layout that
+ * broadcasts right-aligned to [B, H, S, S] (additive). causal = 1 declares that
+ * keys past the query are masked (as the model's -1e9 upper triangle does),
+ * which skips their work; it may be combined with a mask. Replaces
+ * BackendOps.fused_attention / fused_attention_backward (tensor.rs:1172-1174,
+ * 1709-1739; cpu:2366-2630; the CUDA backend runs these on the CPU,
+ * cuda:1595-1636). The backward recomputes the probabilities from q and k as
+ * the reference does. scratch: NULL or
+ * vh_fused_attention_scratch_bytes(B, H, S, backward) bytes (the score block). */
+int vh_fused_attention_fwd(const float* q, const vh_layout* ql, const float* k,
+                           const vh_layout* kl, const float* v, const vh_layout* vl,
+                           const float* mask, const vh_layout* ml, int causal, float* out,
+                           const vh_layout* ol, void* scratch, size_t scratch_bytes,
+                           void* stream);
+int vh_fused_attention_bwd(const float* q, const vh_layout* ql, const float* k,
+                           const vh_layout* kl, const float* v, const vh_layout* vl,
+                           const float* mask, const vh_layout* ml, int causal,
+                           const float* dout, const vh_layout* dol, float* dq,
+                           const vh_layout* dql, float* dk, const vh_layout* dkl, float* dv,
+                           const vh_layout* dvl, void* scratch, size_t scratch_bytes,
+                           void* stream);
+size_t vh_fused_attention_scratch_bytes(int64_t B, int64_t H, int64_t S, int backward);
+
+/* AdamW update of one parameter tensor in place, moments m and v in device
+ * memory, step count t >= 1. Replaces Tensor::adamw_step (tensor.rs:931-1023,
+ * whose device path copies the parameter to the host and back) with the same
+ * operation order. */
+int vh_adamw_step(float* param, const float* grad, float* m, float* v, int64_t n, int32_t t,
+                  float lr, float beta1, float beta2, float eps, float weight_decay,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

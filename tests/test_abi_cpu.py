@@ -64,6 +64,9 @@ def test_scratch_size_queries_are_host_only():
     assert _abi.lib.vh_gelu_bias_bwd_scratch_bytes(16384, 3072) >= 3072 * 4
     assert _abi.lib.vh_embedding_bwd_scratch_bytes(16384, 50257, 768) >= 4 * (3 * 16384 + 2 * 50257)
     assert _abi.lib.vh_cross_entropy_fwd_scratch_bytes(16384) >= 16384 * 4
+    assert _abi.lib.vh_sum_rows_scratch_bytes(16384, 768) >= 768 * 4
+    assert _abi.lib.vh_fused_attention_scratch_bytes(16, 12, 1024, 0) >= 16 * 12 * 1024 * 1024 * 4
+    assert _abi.lib.vh_fused_attention_scratch_bytes(16, 12, 1024, 1) >= 2 * 16 * 12 * 1024 * 1024 * 4
 
 
 def elf_symbols(path):
@@ -109,7 +112,11 @@ def launcher_kernel_names():
     names |= {"vh_xent_fwd_stream", "vh_xent_bwd_stream", "vh_xent_reduce", "vh_col_reduce",
               "vh_emb_tokens", "vh_emb_alloc", "vh_emb_place", "vh_fill",
               "vh_binary_strided_i32", "vh_binary_strided_i64", "vh_reduce_thread",
-              "vh_reduce_wave", "vh_strided_copy_i32", "vh_strided_copy_i64"}
+              "vh_reduce_wave", "vh_strided_copy_i32", "vh_strided_copy_i64", "vh_col_partial",
+              "vh_adamw_v1", "vh_adamw_v4"}
+    for a in ("k4", "k1", "m4", "m1"):
+        for b in ("k4", "k1", "n4", "n1"):
+            names.add(f"vh_gemm_{a}_{b}")
     return names
 
 
@@ -126,3 +133,26 @@ def test_embedded_code_object_matches_build():
         pytest.skip("code object not built in-tree")
     blob = open(CODE_OBJECT, "rb").read()
     assert blob in open(LIB, "rb").read()
+
+
+def test_gemm_desc_layout_matches_header(tmp_path):
+    """vh_gemm_desc crosses the boundary by pointer: the ctypes mirror must have
+    the C compiler's size and field offsets."""
+    import shutil
+    import subprocess
+    from vearo_amd import _abi
+    if shutil.which("gcc") is None:
+        pytest.skip("no C compiler")
+    fields = [f[0] for f in _abi.VhGemmDesc._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "vearo_hip.h"\nint main(void){\n'
+        + 'printf("%zu\\n", sizeof(vh_gemm_desc));\n'
+        + "".join(f'printf("%zu\\n", offsetof(vh_gemm_desc, {f}));\n' for f in fields)
+        + "return 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True,
+                                          text=True).stdout.split()]
+    want = [ctypes.sizeof(_abi.VhGemmDesc)] + [getattr(_abi.VhGemmDesc, f).offset for f in fields]
+    assert got == want

@@ -44,6 +44,22 @@ class VhMemStats(ctypes.Structure):
     ]
 
 
+class VhGemmDesc(ctypes.Structure):
+    """vh_gemm_desc (include/vearo_hip.h)."""
+    _fields_ = [
+        ("M", c_int64), ("N", c_int64), ("K", c_int64),
+        ("a", c_void_p), ("a_sm", c_int64), ("a_sk", c_int64),
+        ("b", c_void_p), ("b_sk", c_int64), ("b_sn", c_int64),
+        ("c", c_void_p), ("c_sm", c_int64),
+        ("batch", c_int64 * 2), ("a_sb", c_int64 * 2), ("b_sb", c_int64 * 2), ("c_sb", c_int64 * 2),
+        ("e", c_void_p), ("e_sm", c_int64), ("e_sn", c_int64), ("e_sb", c_int64 * 2),
+        ("alpha", c_float), ("accumulate", c_int32), ("causal", c_int32),
+    ]
+
+
+GEMM_DENSE, GEMM_SKIP_UPPER, GEMM_K_LE_M, GEMM_K_GE_M = 0, 1, 2, 3
+
+
 class VhError(RuntimeError):
     """A non-zero return from the C ABI; `code` is the VH_ERR_* value."""
 
@@ -107,6 +123,26 @@ SIGNATURES = {
     "vh_binary": (c_int, [c_int, fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, c_void_p]),
     "vh_reduce": (c_int, [c_int, fp, POINTER(VhLayout), c_int, fp, c_void_p]),
     "vh_strided_copy": (c_int, [fp, POINTER(VhLayout), fp, c_void_p]),
+    "vh_sum_rows": (c_int, [fp, c_int64, c_int64, fp, c_void_p, c_size_t, c_void_p]),
+    "vh_sum_rows_scratch_bytes": (c_size_t, [c_int64, c_int64]),
+    "vh_gemm": (c_int, [POINTER(VhGemmDesc), c_void_p]),
+    "vh_matmul": (c_int, [fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, c_void_p]),
+    "vh_fused_attention_fwd": (
+        c_int,
+        [fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, POINTER(VhLayout),
+         c_int, fp, POINTER(VhLayout), c_void_p, c_size_t, c_void_p],
+    ),
+    "vh_fused_attention_bwd": (
+        c_int,
+        [fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, POINTER(VhLayout),
+         c_int, fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp,
+         POINTER(VhLayout), c_void_p, c_size_t, c_void_p],
+    ),
+    "vh_fused_attention_scratch_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int]),
+    "vh_adamw_step": (
+        c_int,
+        [fp, fp, fp, fp, c_int64, c_int32, c_float, c_float, c_float, c_float, c_float, c_void_p],
+    ),
 }
 
 

@@ -1,0 +1,206 @@
+// gemm.h -- f32 matrix multiply on the gfx950 matrix cores (v_mfma_f32_32x32x2_f32).
+//
+// Semantics: vearo-backend-cpu matmul (crates/vearo-backend-cpu/src/lib.rs:266-417),
+// C[m, n] = sum_k A[m, k] * B[k, n] in f32 (the matrix core accumulates in f32;
+// the grouping of the k sum differs from the CPU's sequential mul_add chain,
+// which is within f32 rounding). The epilogue applies, in this order,
+//   v = acc * alpha;  v = v + E[m, n] (optional addend);  v = C[m, n] + v (optional)
+// which are exactly the separate ops the reference runs after a matmul:
+// `* scale` and `+ mask` in attention (cpu:2431-2449), `+ bias` in Linear
+// (nn:120-128), and gradient accumulation `existing.add(g)` (autograd:733-742).
+//
+// Tiling: a 256-thread workgroup computes a 128 x 128 tile of C; its 4 waves
+// own 64 x 64 quadrants as 2 x 2 matrix-core tiles of 32 x 32. K advances in
+// tiles of 32, double-buffered through LDS: the global loads of tile t+1 are in
+// flight while tile t is multiplied. LDS holds both operands k-contiguous
+// ([row][k], rows padded to 36 floats) whatever their layout in HBM, so each
+// lane reads its fragments as 128-bit LDS loads: lane half h (lanes 32h..32h+31)
+// takes k in [16h, 16h+16) of the tile, step s pairing k = s with k = 16 + s.
+// A operand layouts: k-contiguous (A[m, k] at m*lda + k) or m-contiguous
+// (A[m, k] at k*lda + m, a transposed view); the same for B. Global loads are
+// 128-bit when the layout allows (host-checked alignment), else 32-bit.
+//
+// Causal modes for attention's score blocks (the masked part is exactly 0 or
+// never read, so skipping it changes no result):
+//   1: skip tiles entirely above the diagonal (n > m for all elements);
+//   2: only k <= m contributes (P V and dS K: row m's weights are 0 past m);
+//   3: only k >= m contributes (P^T dO and dS^T Q).
+#pragma once
+#include "common.h"
+
+#define GM_TM VH_GEMM_TILE_M
+#define GM_TN VH_GEMM_TILE_N
+#define GM_TK 32
+#define GM_LS (GM_TK + 4)  // LDS row stride (floats): 16-byte aligned rows, staggered banks
+#define GM_GROUP 8         // tile rows per group in the launch order (L2 reuse of B)
+
+typedef float vh_f32x16 __attribute__((ext_vector_type(16)));
+
+// The [128 rows x 32 k] tile whose element (r, k) is at
+//   KC:  base[(r0 + r) * ld + k0 + k]      !KC: base[(k0 + k) * ld + r0 + r]
+// into 16 staging registers per thread; rows >= R or k >= K read as 0.
+// VEC requires 16-byte aligned base and ld, and K (KC) or R (!KC) % 4 == 0.
+template <bool KC, bool VEC>
+VH_DEV void gm_load(const float* base, int64_t ld, int64_t r0, int64_t R, int64_t k0, int64_t K, int tid,
+                    float (&st)[16]) {
+  if constexpr (KC && VEC) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = (tid >> 3) + 32 * i, k = (tid & 7) * 4;
+      vh_f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (r0 + r < R && k0 + k < K) v = *reinterpret_cast<const vh_f4*>(base + (r0 + r) * ld + k0 + k);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) st[4 * i + e] = v[e];
+    }
+  } else if constexpr (KC) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = (tid >> 5) + 8 * i, k = tid & 31;
+      st[i] = (r0 + r < R && k0 + k < K) ? base[(r0 + r) * ld + k0 + k] : 0.0f;
+    }
+  } else if constexpr (VEC) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = (tid >> 5) + 8 * i, r = (tid & 31) * 4;
+      vh_f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (k0 + k < K && r0 + r < R) v = *reinterpret_cast<const vh_f4*>(base + (k0 + k) * ld + r0 + r);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) st[4 * i + e] = v[e];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int k = (tid >> 7) + 2 * i, r = tid & 127;
+      st[i] = (k0 + k < K && r0 + r < R) ? base[(k0 + k) * ld + r0 + r] : 0.0f;
+    }
+  }
+}
+
+template <bool KC, bool VEC>
+VH_DEV void gm_store_lds(float* S, int tid, const float (&st)[16]) {
+  if constexpr (KC && VEC) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = (tid >> 3) + 32 * i, k = (tid & 7) * 4;
+      vh_f4 v = {st[4 * i], st[4 * i + 1], st[4 * i + 2], st[4 * i + 3]};
+      *reinterpret_cast<vh_f4*>(S + r * GM_LS + k) = v;
+    }
+  } else if constexpr (KC) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) S[((tid >> 5) + 8 * i) * GM_LS + (tid & 31)] = st[i];
+  } else if constexpr (VEC) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = (tid >> 5) + 8 * i, r = (tid & 31) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S[(r + e) * GM_LS + k] = st[4 * i + e];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) S[(tid & 127) * GM_LS + (tid >> 7) + 2 * i] = st[i];
+  }
+}
+
+// Workgroup -> C tile. Workgroups are dealt to the 8 XCDs round-robin; this
+// gives each XCD a contiguous run of tile ids, and runs of GM_GROUP tile rows
+// sweep the tile columns together, so an XCD's L2 sees the same B columns
+// and A rows reused.
+VH_DEV void gm_tile_of(int bid, int nblk, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int per = nblk / 8, rem = nblk % 8;
+  const int x = bid % 8, local = bid / 8;
+  const int t = x * per + (x < rem ? x : rem) + local;
+  const int span = GM_GROUP * tiles_n;
+  const int first = (t / span) * GM_GROUP;
+  const int gsize = tiles_m - first < GM_GROUP ? tiles_m - first : GM_GROUP;
+  const int in = t % span;
+  tm = first + in % gsize;
+  tn = in / gsize;
+}
+
+template <bool A_KC, bool A_VEC, bool B_KC, bool B_VEC>
+VH_DEV void gemm_f32_impl(const GemmArgs& a) {
+  __shared__ __attribute__((aligned(16))) float As[2][GM_TM * GM_LS];
+  __shared__ __attribute__((aligned(16))) float Bs[2][GM_TN * GM_LS];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int tm, tn;
+  gm_tile_of(blockIdx.x, gridDim.x, a.tiles_m, a.tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * GM_TM, n0 = (int64_t)tn * GM_TN;
+  if (a.causal == 1 && n0 > m0 + GM_TM - 1) return;  // the whole tile is masked
+
+  const int64_t b1 = blockIdx.y / a.nb2, b2 = blockIdx.y % a.nb2;
+  const float* A = a.A + b1 * a.sa1 + b2 * a.sa2;
+  const float* B = a.B + b1 * a.sb1 + b2 * a.sb2;
+  float* C = a.C + b1 * a.sc1 + b2 * a.sc2;
+
+  int64_t kb = 0, ke = a.K;
+  if (a.causal == 2) ke = m0 + GM_TM < a.K ? m0 + GM_TM : a.K;
+  if (a.causal == 3) kb = (m0 / GM_TK) * GM_TK;
+
+  vh_f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = vh_f32x16{};
+
+  const int wm = w >> 1, wn = w & 1, li = lane & 31, h = lane >> 5;
+  float sa[16], sb[16];
+  int s = 0;
+  if (kb < ke) {
+    gm_load<A_KC, A_VEC>(A, a.lda, m0, a.M, kb, a.K, tid, sa);
+    gm_load<B_KC, B_VEC>(B, a.ldb, n0, a.N, kb, a.K, tid, sb);
+    gm_store_lds<A_KC, A_VEC>(As[0], tid, sa);
+    gm_store_lds<B_KC, B_VEC>(Bs[0], tid, sb);
+    __syncthreads();
+  }
+  for (int64_t k0 = kb; k0 < ke; k0 += GM_TK) {
+    const bool more = k0 + GM_TK < ke;
+    if (more) {
+      gm_load<A_KC, A_VEC>(A, a.lda, m0, a.M, k0 + GM_TK, a.K, tid, sa);
+      gm_load<B_KC, B_VEC>(B, a.ldb, n0, a.N, k0 + GM_TK, a.K, tid, sb);
+    }
+    const float* as = As[s] + (wm * 64 + li) * GM_LS + h * 16;
+    const float* bs = Bs[s] + (wn * 64 + li) * GM_LS + h * 16;
+#pragma unroll
+    for (int kc = 0; kc < 16; kc += 4) {
+      const vh_f4 a0 = *reinterpret_cast<const vh_f4*>(as + kc);
+      const vh_f4 a1 = *reinterpret_cast<const vh_f4*>(as + 32 * GM_LS + kc);
+      const vh_f4 b0 = *reinterpret_cast<const vh_f4*>(bs + kc);
+      const vh_f4 bv1 = *reinterpret_cast<const vh_f4*>(bs + 32 * GM_LS + kc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], b0[e], acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], bv1[e], acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], b0[e], acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], bv1[e], acc[1][1], 0, 0, 0);
+      }
+    }
+    if (more) {
+      gm_store_lds<A_KC, A_VEC>(As[s ^ 1], tid, sa);
+      gm_store_lds<B_KC, B_VEC>(Bs[s ^ 1], tid, sb);
+    }
+    __syncthreads();
+    s ^= 1;
+  }
+
+  // Epilogue. Accumulator register r of a 32 x 32 tile holds row
+  // 8*(r/4) + 4*h + r%4, column li.
+  const float* E = a.E ? a.E + b1 * a.se1 + b2 * a.se2 : nullptr;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int64_t n = n0 + wn * 64 + nt * 32 + li;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (m < a.M && n < a.N) {
+          float v = acc[mt][nt][r] * a.alpha;
+          if (E) v = v + E[m * a.sem + n * a.sen];
+          float* cp = C + m * a.ldc + n;
+          if (a.accumulate) v = *cp + v;
+          *cp = v;
+        }
+      }
+    }
+  }
+}

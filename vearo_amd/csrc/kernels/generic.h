@@ -94,3 +94,25 @@ VH_DEV void fill_impl(const FillArgs& a) {
     *reinterpret_cast<float4*>(a.p + u * 4) = make_float4(v, v, v, v);
   for (int64_t i = n4 * 4 + tid; i < a.n; i += stride) a.p[i] = v;
 }
+
+// Column sums of rows [g*rpb, (g+1)*rpb) of x[rows, C]: part[g][c], summed in
+// row order. Grid (G, ceil(C/256)); one thread per column, consecutive threads
+// on consecutive columns (coalesced rows), 8 row loads in flight.
+VH_DEV void col_partial_impl(const ColPartialArgs& a) {
+  const int64_t c = (int64_t)blockIdx.y * 256 + threadIdx.x;
+  if (c >= a.C) return;
+  const int64_t r0 = (int64_t)blockIdx.x * a.rpb;
+  const int64_t r1 = r0 + a.rpb < a.rows ? r0 + a.rpb : a.rows;
+  const float* p = a.x + c;
+  float s = 0.0f;
+  int64_t r = r0;
+  for (; r + 8 <= r1; r += 8) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = p[(r + k) * a.C];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += v[k];
+  }
+  for (; r < r1; ++r) s += p[r * a.C];
+  a.part[(int64_t)blockIdx.x * a.C + c] = s;
+}

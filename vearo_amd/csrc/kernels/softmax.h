@@ -13,7 +13,11 @@
 // which is what exp() gives the reference for -inf (or -1e9 additive) entries.
 // Traffic: fwd reads the live prefix and writes the row (4f+4 B/elem, f = live
 // fraction); bwd reads the live prefix of y (or x) and dy, writes dx. All row
-// traffic is non-temporal (single use).
+// traffic is non-temporal (single use). Rows are held whole in registers before
+// anything is written, so in == out (in place) is allowed.
+// attn = 1 follows the CPU fused attention instead (cpu:2451-2458, 2583-2590):
+// p = e * inv with inv = 1/(sum + 1e-9), and the backward's sum of dy*y is a
+// fused multiply-add chain.
 #pragma once
 #include "common.h"
 
@@ -72,6 +76,7 @@ VH_DEV void softmax_fwd_impl(const SoftmaxArgs& a) {
       }
     }
     s = team_sum<TEAM>(s, red);
+    const float inv = 1.0f / (s + 1e-9f);
     if (active) {
       float* yr = a.y + row * (int64_t)T;
 #pragma unroll
@@ -80,7 +85,8 @@ VH_DEV void softmax_fwd_impl(const SoftmaxArgs& a) {
         if (u < U) {
           Unit<VW> o;
 #pragma unroll
-          for (int j = 0; j < VW; ++j) o.v[j] = (u * VW + j < L[r]) ? v[r][k].v[j] / s : 0.0f;
+          for (int j = 0; j < VW; ++j)
+            o.v[j] = (u * VW + j < L[r]) ? (a.attn ? v[r][k].v[j] * inv : v[r][k].v[j] / s) : 0.0f;
           store_stream<VW>(yr + u * VW, o);
         }
       }
@@ -142,10 +148,11 @@ VH_DEV void softmax_bwd_impl(const SoftmaxArgs& a) {
         }
       }
       s = team_sum<TEAM>(s, red);
+      const float inv = 1.0f / (s + 1e-9f);
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
 #pragma unroll
-        for (int j = 0; j < VW; ++j) y[r][k].v[j] = y[r][k].v[j] / s;
+        for (int j = 0; j < VW; ++j) y[r][k].v[j] = a.attn ? y[r][k].v[j] * inv : y[r][k].v[j] / s;
       }
     }
     float dot = 0.0f;
@@ -154,7 +161,8 @@ VH_DEV void softmax_bwd_impl(const SoftmaxArgs& a) {
       const int u = lane + k * TEAM;
 #pragma unroll
       for (int j = 0; j < VW; ++j) {
-        if (u < U && u * VW + j < L[r]) dot += g[r][k].v[j] * y[r][k].v[j];
+        if (u < U && u * VW + j < L[r])
+          dot = a.attn ? __builtin_fmaf(g[r][k].v[j], y[r][k].v[j], dot) : dot + g[r][k].v[j] * y[r][k].v[j];
       }
     }
     dot = team_sum<TEAM>(dot, red);

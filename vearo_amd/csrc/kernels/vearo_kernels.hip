@@ -8,8 +8,10 @@
 #include "common.h"
 #include "embedding.h"
 #include "gelu.h"
+#include "gemm.h"
 #include "generic.h"
 #include "layernorm.h"
+#include "optim.h"
 #include "softmax.h"
 #include "xent.h"
 
@@ -140,3 +142,33 @@ extern "C" __global__ void __launch_bounds__(256) vh_reduce_wave(ReduceArgs a) {
 extern "C" __global__ void __launch_bounds__(256) vh_strided_copy_i32(CopyArgs a) { strided_copy_impl<uint32_t>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_strided_copy_i64(CopyArgs a) { strided_copy_impl<uint64_t>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_fill(FillArgs a) { fill_impl(a); }
+
+// Matrix multiply: vh_gemm_<A><B>, each operand k-contiguous ("k") or
+// m/n-contiguous ("m"/"n"), with 128-bit ("4") or 32-bit ("1") global loads.
+#define K_GEMM(AK, AV, BK, BV, NAME)                                                            \
+  extern "C" __global__ void __launch_bounds__(256, 2) NAME(GemmArgs a) {                      \
+    gemm_f32_impl<AK, AV, BK, BV>(a);                                                           \
+  }
+K_GEMM(true, true, true, true, vh_gemm_k4_k4)
+K_GEMM(true, true, true, false, vh_gemm_k4_k1)
+K_GEMM(true, true, false, true, vh_gemm_k4_n4)
+K_GEMM(true, true, false, false, vh_gemm_k4_n1)
+K_GEMM(true, false, true, true, vh_gemm_k1_k4)
+K_GEMM(true, false, true, false, vh_gemm_k1_k1)
+K_GEMM(true, false, false, true, vh_gemm_k1_n4)
+K_GEMM(true, false, false, false, vh_gemm_k1_n1)
+K_GEMM(false, true, true, true, vh_gemm_m4_k4)
+K_GEMM(false, true, true, false, vh_gemm_m4_k1)
+K_GEMM(false, true, false, true, vh_gemm_m4_n4)
+K_GEMM(false, true, false, false, vh_gemm_m4_n1)
+K_GEMM(false, false, true, true, vh_gemm_m1_k4)
+K_GEMM(false, false, true, false, vh_gemm_m1_k1)
+K_GEMM(false, false, false, true, vh_gemm_m1_n4)
+K_GEMM(false, false, false, false, vh_gemm_m1_n1)
+
+// AdamW
+extern "C" __global__ void __launch_bounds__(256) vh_adamw_v1(AdamArgs a) { adamw_impl<1>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_adamw_v4(AdamArgs a) { adamw_impl<4>(a); }
+
+// Row sums (bias gradients): first stage; the second is vh_col_reduce.
+extern "C" __global__ void __launch_bounds__(256) vh_col_partial(ColPartialArgs a) { col_partial_impl(a); }

@@ -640,7 +640,8 @@ int vh_gelu_bias_bwd(const float* x, const float* bias, const float* dy, float* 
 // --------------------------------------------------------------- softmax --
 
 static int softmax_common(const char* base, int cap, int rpw, const float* in, const float* dy,
-                          float* out, int64_t rows, int64_t T, int causal, int input_is_x, hipStream_t s) {
+                          float* out, int64_t rows, int64_t T, int causal, int input_is_x, hipStream_t s,
+                          int attn = 0) {
   RowCfg c;
   const bool vec = aligned16(in) && aligned16(out) && (!dy || aligned16(dy));
   if (!pick_row_cfg(T, vec, cap, &c))
@@ -648,7 +649,7 @@ static int softmax_common(const char* base, int cap, int rpw, const float* in, c
   set_rpw(&c, rpw);
   const int bs = block_of(c);
   const int64_t rpb = (int64_t)(bs / c.team) * c.rpw;
-  SoftmaxArgs a{in, dy, out, rows, (int32_t)T, causal ? 1 : 0, input_is_x ? 1 : 0};
+  SoftmaxArgs a{in, dy, out, rows, (int32_t)T, causal ? 1 : 0, input_is_x ? 1 : 0, attn};
   return launch(fwd_kernel(base, c), (unsigned)cdiv(rows, rpb), 1, bs, 0, s, a);
 }
 
@@ -901,6 +902,491 @@ int vh_strided_copy(const float* src, const vh_layout* sl, float* dst, void* str
   const int64_t blocks = std::min<int64_t>(cdiv(n, 256), 16384);
   return launch(n < INT32_MAX ? "vh_strided_copy_i32" : "vh_strided_copy_i64", (unsigned)blocks, 1, 256, 0,
                 s, a);
+}
+
+
+// ---------------------------------------------------------------- row sums --
+
+static int64_t sum_rows_groups(int64_t rows) { return std::max<int64_t>(1, std::min<int64_t>(rows, 256)); }
+
+size_t vh_sum_rows_scratch_bytes(int64_t rows, int64_t C) {
+  if (rows <= 0 || C <= 0) return 0;
+  return align256((size_t)sum_rows_groups(rows) * (size_t)C * sizeof(float));
+}
+
+int vh_sum_rows(const float* x, int64_t rows, int64_t C, float* out, void* scratch, size_t scratch_bytes,
+                void* stream) {
+  VH_TRY(require_init());
+  if (rows < 0 || C < 0) return fail(VH_ERR_INVALID, "vh_sum_rows: negative size");
+  hipStream_t s = S(stream);
+  if (C == 0) return VH_OK;
+  if (!out) return fail(VH_ERR_INVALID, "vh_sum_rows: null pointer");
+  if (rows == 0) return fill(out, 0.0f, C, s);
+  if (!x) return fail(VH_ERR_INVALID, "vh_sum_rows: null pointer");
+  if (C > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_sum_rows: C too large");
+  const int64_t G0 = sum_rows_groups(rows);
+  const int64_t rpb = cdiv(rows, G0);
+  const int64_t G = cdiv(rows, rpb);
+  Scratch sc;
+  VH_TRY(sc.get(scratch, scratch_bytes, align256((size_t)G0 * (size_t)C * sizeof(float))));
+  float* part = static_cast<float*>(sc.p);
+  ColPartialArgs a{x, part, rows, rpb, (int32_t)C};
+  VH_TRY(launch("vh_col_partial", (unsigned)G, (unsigned)cdiv(C, 256), 256, 0, s, a));
+  ColReduceArgs r{part, out, nullptr, (int32_t)G, (int32_t)C, 1};
+  return launch("vh_col_reduce", (unsigned)cdiv(C, 64), 1, 1024, 0, s, r);
+}
+
+// ------------------------------------------------------------------ gemm --
+
+static bool gemm_vec_ok(const float* p, int64_t ld, int64_t ext, const int64_t* sb) {
+  return aligned16(p) && ld % 4 == 0 && ext % 4 == 0 && sb[0] % 4 == 0 && sb[1] % 4 == 0;
+}
+
+int vh_gemm(const vh_gemm_desc* d, void* stream) {
+  VH_TRY(require_init());
+  if (!d) return fail(VH_ERR_INVALID, "vh_gemm: null descriptor");
+  const int64_t M = d->M, N = d->N, K = d->K;
+  if (M < 0 || N < 0 || K < 0 || d->batch[0] < 0 || d->batch[1] < 0)
+    return fail(VH_ERR_INVALID, "vh_gemm: negative size");
+  const int64_t strides[] = {d->a_sm, d->a_sk, d->b_sk, d->b_sn, d->c_sm, d->a_sb[0], d->a_sb[1],
+                             d->b_sb[0], d->b_sb[1], d->c_sb[0], d->c_sb[1], d->e_sm, d->e_sn,
+                             d->e_sb[0], d->e_sb[1]};
+  for (int64_t st : strides)
+    if (st < 0) return fail(VH_ERR_INVALID, "vh_gemm: negative stride");
+  if (M == 0 || N == 0 || d->batch[0] == 0 || d->batch[1] == 0) return VH_OK;
+  if (!d->c || (K > 0 && (!d->a || !d->b))) return fail(VH_ERR_INVALID, "vh_gemm: null pointer");
+  if (d->causal < 0 || d->causal > 3) return fail(VH_ERR_INVALID, "vh_gemm: unknown causal mode");
+  if ((d->causal == VH_GEMM_K_LE_M || d->causal == VH_GEMM_K_GE_M) && M != K)
+    return fail(VH_ERR_INVALID, "vh_gemm: causal k ranges need M == K");
+  // A unit stride along k (k-contiguous) or along m; the same for B along k or n.
+  const bool akc = d->a_sk == 1 || K == 1;
+  const bool bkc = d->b_sk == 1 || K == 1;
+  if (!akc && d->a_sm != 1 && M != 1)
+    return fail(VH_ERR_UNSUPPORTED, "vh_gemm: A needs a unit stride along m or k");
+  if (!bkc && d->b_sn != 1 && N != 1)
+    return fail(VH_ERR_UNSUPPORTED, "vh_gemm: B needs a unit stride along k or n");
+  const int64_t lda = akc ? (M == 1 ? 0 : d->a_sm) : d->a_sk;
+  const int64_t ldb = bkc ? (N == 1 ? 0 : d->b_sn) : d->b_sk;
+  const bool avec = K > 0 && gemm_vec_ok(d->a, lda, akc ? K : M, d->a_sb);
+  const bool bvec = K > 0 && gemm_vec_ok(d->b, ldb, bkc ? K : N, d->b_sb);
+  const int64_t tiles_m = cdiv(M, VH_GEMM_TILE_M), tiles_n = cdiv(N, VH_GEMM_TILE_N);
+  if (tiles_m * tiles_n > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_gemm: too many tiles");
+  const std::string name = std::string("vh_gemm_") + (akc ? "k" : "m") + (avec ? "4" : "1") + "_" +
+                           (bkc ? "k" : "n") + (bvec ? "4" : "1");
+  hipStream_t s = S(stream);
+  // Grid y covers both batch dims; runs of the outer one keep it under 65535.
+  const int64_t outer_chunk = std::max<int64_t>(1, 65535 / d->batch[1]);
+  if (d->batch[1] > 65535) return fail(VH_ERR_UNSUPPORTED, "vh_gemm: inner batch too large");
+  for (int64_t b0 = 0; b0 < d->batch[0]; b0 += outer_chunk) {
+    const int64_t nb = std::min(outer_chunk, d->batch[0] - b0);
+    GemmArgs g{};
+    g.A = d->a ? d->a + b0 * d->a_sb[0] : nullptr;
+    g.B = d->b ? d->b + b0 * d->b_sb[0] : nullptr;
+    g.C = d->c + b0 * d->c_sb[0];
+    g.E = d->e ? d->e + b0 * d->e_sb[0] : nullptr;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.lda = lda;
+    g.ldb = ldb;
+    g.ldc = d->c_sm;
+    g.sa1 = d->a_sb[0];
+    g.sa2 = d->a_sb[1];
+    g.sb1 = d->b_sb[0];
+    g.sb2 = d->b_sb[1];
+    g.sc1 = d->c_sb[0];
+    g.sc2 = d->c_sb[1];
+    g.se1 = d->e_sb[0];
+    g.se2 = d->e_sb[1];
+    g.sem = d->e_sm;
+    g.sen = d->e_sn;
+    g.nb2 = (int32_t)d->batch[1];
+    g.tiles_m = (int32_t)tiles_m;
+    g.tiles_n = (int32_t)tiles_n;
+    g.accumulate = d->accumulate ? 1 : 0;
+    g.causal = d->causal;
+    g.alpha = d->alpha;
+    VH_TRY(launch(name, (unsigned)(tiles_m * tiles_n), (unsigned)(nb * d->batch[1]), 256, 0, s, g));
+  }
+  return VH_OK;
+}
+
+namespace {
+// A contiguous copy of a strided operand whose last two dims have no unit
+// stride (the reference makes every matmul operand contiguous, cpu:307-308).
+struct Contig {
+  void* p = nullptr;
+  ~Contig() {
+    if (p) g_arena.free(p);
+  }
+};
+
+int matmul_operand(const float* x, const vh_layout* l, Contig* tmp, const float** out, vh_layout* ol,
+                   hipStream_t s) {
+  *ol = *l;
+  *out = x;
+  const int r = l->rank;
+  const bool ok = l->strides[r - 1] == 1 || l->strides[r - 2] == 1 || l->dims[r - 1] == 1 ||
+                  l->dims[r - 2] == 1;
+  if (ok) return VH_OK;
+  const int64_t n = numel(l);
+  VH_TRY(g_arena.alloc((size_t)n * sizeof(float), &tmp->p));
+  VH_TRY(vh_strided_copy(x, l, static_cast<float*>(tmp->p), s));
+  int64_t acc = 1;
+  for (int i = r - 1; i >= 0; --i) {
+    ol->strides[i] = acc;
+    acc *= l->dims[i];
+  }
+  *out = static_cast<const float*>(tmp->p);
+  return VH_OK;
+}
+}  // namespace
+
+int vh_matmul(const float* lhs, const vh_layout* ll, const float* rhs, const vh_layout* rl, float* out,
+              void* stream) {
+  VH_TRY(require_init());
+  VH_TRY(check_layout(ll, "vh_matmul lhs"));
+  VH_TRY(check_layout(rl, "vh_matmul rhs"));
+  if (ll->rank < 2 || rl->rank < 2) return fail(VH_ERR_INVALID, "Matmul requires rank >= 2");
+  const int lr = ll->rank, rr = rl->rank;
+  const int64_t M = ll->dims[lr - 2], K = ll->dims[lr - 1], K2 = rl->dims[rr - 2], N = rl->dims[rr - 1];
+  if (K != K2) return fail(VH_ERR_INVALID, "Incompatible dimensions for matmul");
+  const int lb = lr - 2, rb = rr - 2, ob = std::max(lb, rb);
+  int64_t odims[VH_MAX_RANK], as[VH_MAX_RANK], bs[VH_MAX_RANK];
+  for (int i = 0; i < ob; ++i) {
+    const int li = i - (ob - lb), ri = i - (ob - rb);
+    const int64_t a = li >= 0 ? ll->dims[li] : 1, b = ri >= 0 ? rl->dims[ri] : 1;
+    if (a != b && a != 1 && b != 1) return fail(VH_ERR_INVALID, "Batch shapes are not broadcastable");
+    odims[i] = std::max(a, b);
+  }
+  int64_t nout = M * N;
+  for (int i = 0; i < ob; ++i) nout *= odims[i];
+  if (nout == 0) return VH_OK;
+  if (!lhs || !rhs || !out) return fail(VH_ERR_INVALID, "vh_matmul: null pointer");
+  hipStream_t s = S(stream);
+  Contig ta, tb;
+  const float *A, *B;
+  vh_layout al, bl;
+  VH_TRY(matmul_operand(lhs, ll, &ta, &A, &al, s));
+  VH_TRY(matmul_operand(rhs, rl, &tb, &B, &bl, s));
+  for (int i = 0; i < ob; ++i) {
+    const int li = i - (ob - lb), ri = i - (ob - rb);
+    as[i] = (li >= 0 && al.dims[li] != 1) ? al.strides[li] : 0;
+    bs[i] = (ri >= 0 && bl.dims[ri] != 1) ? bl.strides[ri] : 0;
+  }
+  // Output batch strides (contiguous [batch..., M, N]).
+  int64_t cs[VH_MAX_RANK], acc = M * N;
+  for (int i = ob - 1; i >= 0; --i) {
+    cs[i] = acc;
+    acc *= odims[i];
+  }
+  vh_gemm_desc d{};
+  d.M = M;
+  d.N = N;
+  d.K = K;
+  d.a_sm = al.strides[lr - 2];
+  d.a_sk = al.strides[lr - 1];
+  d.b_sk = bl.strides[rr - 2];
+  d.b_sn = bl.strides[rr - 1];
+  d.c_sm = N;
+  d.alpha = 1.0f;
+  // The last two batch dims go to the kernel; any others are looped here.
+  const int inner = std::min(ob, 2), lead = ob - inner;
+  for (int j = 0; j < 2; ++j) {
+    const int i = lead + j - (2 - inner);
+    d.batch[j] = i >= lead ? odims[i] : 1;
+    d.a_sb[j] = i >= lead ? as[i] : 0;
+    d.b_sb[j] = i >= lead ? bs[i] : 0;
+    d.c_sb[j] = i >= lead ? cs[i] : 0;
+  }
+  int64_t nlead = 1;
+  for (int i = 0; i < lead; ++i) nlead *= odims[i];
+  for (int64_t t = 0; t < nlead; ++t) {
+    int64_t rem = t, ao = 0, bo = 0, co = 0;
+    for (int i = lead - 1; i >= 0; --i) {
+      const int64_t c = rem % odims[i];
+      rem /= odims[i];
+      ao += c * as[i];
+      bo += c * bs[i];
+      co += c * cs[i];
+    }
+    d.a = A + ao;
+    d.b = B + bo;
+    d.c = out + co;
+    VH_TRY(vh_gemm(&d, stream));
+  }
+  return VH_OK;
+}
+
+// ------------------------------------------------------- fused attention --
+
+namespace {
+struct AttnShape {
+  int64_t B, H, S, Dk;
+};
+
+int attn_layout(const vh_layout* l, const char* what, AttnShape* sh, bool first) {
+  if (!l || l->rank != 4) return fail(VH_ERR_INVALID, std::string(what) + ": expected a rank-4 [B, H, S, Dk] layout");
+  VH_TRY(check_layout(l, what));
+  if (first) {
+    *sh = AttnShape{l->dims[0], l->dims[1], l->dims[2], l->dims[3]};
+  } else if (l->dims[0] != sh->B || l->dims[1] != sh->H || l->dims[2] != sh->S || l->dims[3] != sh->Dk) {
+    return fail(VH_ERR_INVALID, std::string(what) + ": shape differs from q");
+  }
+  if (l->strides[3] != 1 && l->dims[3] != 1)
+    return fail(VH_ERR_UNSUPPORTED, std::string(what) + ": the last dim must have unit stride");
+  return VH_OK;
+}
+
+// The mask right-aligned to [B, H, S, S] with broadcasting (cpu:2395-2404).
+int attn_mask(const vh_layout* ml, const AttnShape& sh, int64_t st[4]) {
+  if (ml->rank > 4) return fail(VH_ERR_INVALID, "fused attention: mask rank above 4");
+  VH_TRY(check_layout(ml, "fused attention mask"));
+  const int64_t tgt[4] = {sh.B, sh.H, sh.S, sh.S};
+  for (int i = 0; i < 4; ++i) {
+    const int mi = i - (4 - ml->rank);
+    const int64_t dim = mi >= 0 ? ml->dims[mi] : 1;
+    if (dim != 1 && dim != tgt[i]) return fail(VH_ERR_INVALID, "fused attention: mask does not broadcast");
+    st[i] = (mi >= 0 && dim != 1) ? ml->strides[mi] : 0;
+  }
+  return VH_OK;
+}
+
+// scores[b, h] = q k^T * scale (+ mask) into P, then P = softmax(scores) in place.
+int attn_probs(const float* q, const vh_layout* ql, const float* k, const vh_layout* kl, const float* mask,
+               const int64_t* mst, int causal, const AttnShape& sh, float* P, hipStream_t s) {
+  const float scale = 1.0f / std::sqrt((float)sh.Dk);
+  vh_gemm_desc d{};
+  d.M = sh.S;
+  d.N = sh.S;
+  d.K = sh.Dk;
+  d.a = q;
+  d.a_sm = ql->strides[2];
+  d.a_sk = 1;
+  d.b = k;  // B[k=d][n=j] = k[j][d]
+  d.b_sk = 1;
+  d.b_sn = kl->strides[2];
+  d.c = P;
+  d.c_sm = sh.S;
+  d.batch[0] = sh.B;
+  d.batch[1] = sh.H;
+  d.a_sb[0] = ql->strides[0];
+  d.a_sb[1] = ql->strides[1];
+  d.b_sb[0] = kl->strides[0];
+  d.b_sb[1] = kl->strides[1];
+  d.c_sb[0] = sh.H * sh.S * sh.S;
+  d.c_sb[1] = sh.S * sh.S;
+  if (mask) {
+    d.e = mask;
+    d.e_sb[0] = mst[0];
+    d.e_sb[1] = mst[1];
+    d.e_sm = mst[2];
+    d.e_sn = mst[3];
+  }
+  d.alpha = scale;
+  d.causal = causal ? VH_GEMM_SKIP_UPPER : VH_GEMM_DENSE;
+  VH_TRY(vh_gemm(&d, s));
+  return softmax_common("vh_sm_fwd", 16, kSmFwdRpw, P, nullptr, P, sh.B * sh.H * sh.S, sh.S, causal, 0, s, 1);
+}
+}  // namespace
+
+size_t vh_fused_attention_scratch_bytes(int64_t B, int64_t H, int64_t S, int backward) {
+  if (B <= 0 || H <= 0 || S <= 0) return 0;
+  const size_t one = align256((size_t)B * (size_t)H * (size_t)S * (size_t)S * sizeof(float));
+  return backward ? 2 * one : one;
+}
+
+int vh_fused_attention_fwd(const float* q, const vh_layout* ql, const float* k, const vh_layout* kl,
+                           const float* v, const vh_layout* vl, const float* mask, const vh_layout* ml,
+                           int causal, float* out, const vh_layout* ol, void* scratch, size_t scratch_bytes,
+                           void* stream) {
+  VH_TRY(require_init());
+  AttnShape sh;
+  VH_TRY(attn_layout(ql, "fused attention q", &sh, true));
+  VH_TRY(attn_layout(kl, "fused attention k", &sh, false));
+  VH_TRY(attn_layout(vl, "fused attention v", &sh, false));
+  VH_TRY(attn_layout(ol, "fused attention out", &sh, false));
+  int64_t mst[4] = {0, 0, 0, 0};
+  if (mask) VH_TRY(attn_mask(ml, sh, mst));
+  if (sh.B * sh.H * sh.S * sh.Dk == 0) return VH_OK;
+  if (!q || !k || !v || !out) return fail(VH_ERR_INVALID, "vh_fused_attention_fwd: null pointer");
+  if (sh.S > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_fused_attention_fwd: S too large");
+  hipStream_t s = S(stream);
+  Scratch sc;
+  VH_TRY(sc.get(scratch, scratch_bytes, vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 0)));
+  float* P = static_cast<float*>(sc.p);
+  VH_TRY(attn_probs(q, ql, k, kl, mask, mst, causal, sh, P, s));
+  vh_gemm_desc d{};  // out = P v
+  d.M = sh.S;
+  d.N = sh.Dk;
+  d.K = sh.S;
+  d.a = P;
+  d.a_sm = sh.S;
+  d.a_sk = 1;
+  d.b = v;  // B[k=j][n=d] = v[j][d]
+  d.b_sk = vl->strides[2];
+  d.b_sn = 1;
+  d.c = out;
+  d.c_sm = ol->strides[2];
+  d.batch[0] = sh.B;
+  d.batch[1] = sh.H;
+  d.a_sb[0] = sh.H * sh.S * sh.S;
+  d.a_sb[1] = sh.S * sh.S;
+  d.b_sb[0] = vl->strides[0];
+  d.b_sb[1] = vl->strides[1];
+  d.c_sb[0] = ol->strides[0];
+  d.c_sb[1] = ol->strides[1];
+  d.alpha = 1.0f;
+  d.causal = causal ? VH_GEMM_K_LE_M : VH_GEMM_DENSE;
+  return vh_gemm(&d, s);
+}
+
+int vh_fused_attention_bwd(const float* q, const vh_layout* ql, const float* k, const vh_layout* kl,
+                           const float* v, const vh_layout* vl, const float* mask, const vh_layout* ml,
+                           int causal, const float* dout, const vh_layout* dol, float* dq,
+                           const vh_layout* dql, float* dk, const vh_layout* dkl, float* dv,
+                           const vh_layout* dvl, void* scratch, size_t scratch_bytes, void* stream) {
+  VH_TRY(require_init());
+  AttnShape sh;
+  VH_TRY(attn_layout(ql, "fused attention q", &sh, true));
+  VH_TRY(attn_layout(kl, "fused attention k", &sh, false));
+  VH_TRY(attn_layout(vl, "fused attention v", &sh, false));
+  VH_TRY(attn_layout(dol, "fused attention grad_out", &sh, false));
+  VH_TRY(attn_layout(dql, "fused attention dq", &sh, false));
+  VH_TRY(attn_layout(dkl, "fused attention dk", &sh, false));
+  VH_TRY(attn_layout(dvl, "fused attention dv", &sh, false));
+  int64_t mst[4] = {0, 0, 0, 0};
+  if (mask) VH_TRY(attn_mask(ml, sh, mst));
+  if (sh.B * sh.H * sh.S * sh.Dk == 0) return VH_OK;
+  if (!q || !k || !v || !dout || !dq || !dk || !dv)
+    return fail(VH_ERR_INVALID, "vh_fused_attention_bwd: null pointer");
+  if (sh.S > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_fused_attention_bwd: S too large");
+  hipStream_t s = S(stream);
+  Scratch sc;
+  VH_TRY(sc.get(scratch, scratch_bytes, vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 1)));
+  float* P = static_cast<float*>(sc.p);
+  float* G = P + vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 0) / sizeof(float);
+  const float scale = 1.0f / std::sqrt((float)sh.Dk);
+  const int64_t pb0 = sh.H * sh.S * sh.S, pb1 = sh.S * sh.S;
+  // 1. P, recomputed from q and k as the reference does (cpu:2520-2569).
+  VH_TRY(attn_probs(q, ql, k, kl, mask, mst, causal, sh, P, s));
+  // 2. dP = dO v^T into G.
+  vh_gemm_desc d{};
+  d.M = sh.S;
+  d.N = sh.S;
+  d.K = sh.Dk;
+  d.a = dout;
+  d.a_sm = dol->strides[2];
+  d.a_sk = 1;
+  d.b = v;  // B[k=d][n=j] = v[j][d]
+  d.b_sk = 1;
+  d.b_sn = vl->strides[2];
+  d.c = G;
+  d.c_sm = sh.S;
+  d.batch[0] = sh.B;
+  d.batch[1] = sh.H;
+  d.a_sb[0] = dol->strides[0];
+  d.a_sb[1] = dol->strides[1];
+  d.b_sb[0] = vl->strides[0];
+  d.b_sb[1] = vl->strides[1];
+  d.c_sb[0] = pb0;
+  d.c_sb[1] = pb1;
+  d.alpha = 1.0f;
+  d.causal = causal ? VH_GEMM_SKIP_UPPER : VH_GEMM_DENSE;
+  VH_TRY(vh_gemm(&d, s));
+  // 3. dS = P * (dP - sum(dP * P)) in place over G.
+  VH_TRY(softmax_common("vh_sm_bwd", 8, kSmBwdRpw, P, G, G, sh.B * sh.H * sh.S, sh.S, causal, 0, s, 1));
+  // 4. dq = (dS k) * scale.
+  vh_gemm_desc e{};
+  e.M = sh.S;
+  e.N = sh.Dk;
+  e.K = sh.S;
+  e.a = G;
+  e.a_sm = sh.S;
+  e.a_sk = 1;
+  e.b = k;  // B[k=j][n=d] = k[j][d]
+  e.b_sk = kl->strides[2];
+  e.b_sn = 1;
+  e.c = dq;
+  e.c_sm = dql->strides[2];
+  e.batch[0] = sh.B;
+  e.batch[1] = sh.H;
+  e.a_sb[0] = pb0;
+  e.a_sb[1] = pb1;
+  e.b_sb[0] = kl->strides[0];
+  e.b_sb[1] = kl->strides[1];
+  e.c_sb[0] = dql->strides[0];
+  e.c_sb[1] = dql->strides[1];
+  e.alpha = scale;
+  e.causal = causal ? VH_GEMM_K_LE_M : VH_GEMM_DENSE;
+  VH_TRY(vh_gemm(&e, s));
+  // 5. dk = (dS^T q) * scale: A[m=j][k=i] = dS[i][j].
+  e.a_sm = 1;
+  e.a_sk = sh.S;
+  e.b = q;
+  e.b_sk = ql->strides[2];
+  e.b_sb[0] = ql->strides[0];
+  e.b_sb[1] = ql->strides[1];
+  e.c = dk;
+  e.c_sm = dkl->strides[2];
+  e.c_sb[0] = dkl->strides[0];
+  e.c_sb[1] = dkl->strides[1];
+  e.causal = causal ? VH_GEMM_K_GE_M : VH_GEMM_DENSE;
+  VH_TRY(vh_gemm(&e, s));
+  // 6. dv = P^T dO.
+  e.a = P;
+  e.b = dout;
+  e.b_sk = dol->strides[2];
+  e.b_sb[0] = dol->strides[0];
+  e.b_sb[1] = dol->strides[1];
+  e.c = dv;
+  e.c_sm = dvl->strides[2];
+  e.c_sb[0] = dvl->strides[0];
+  e.c_sb[1] = dvl->strides[1];
+  e.alpha = 1.0f;
+  return vh_gemm(&e, s);
+}
+
+// ----------------------------------------------------------------- AdamW --
+
+// f32::powi lowers to compiler-rt's __powisf2: binary exponentiation in f32.
+static float powi_f32(float a, int b) {
+  const bool recip = b < 0;
+  float r = 1.0f;
+  for (;;) {
+    if (b & 1) r *= a;
+    b /= 2;
+    if (b == 0) break;
+    a *= a;
+  }
+  return recip ? 1.0f / r : r;
+}
+
+int vh_adamw_step(float* param, const float* grad, float* m, float* v, int64_t n, int32_t t, float lr,
+                  float beta1, float beta2, float eps, float weight_decay, void* stream) {
+  VH_TRY(require_init());
+  if (n < 0) return fail(VH_ERR_INVALID, "vh_adamw_step: negative size");
+  if (t < 1) return fail(VH_ERR_INVALID, "vh_adamw_step: step count t must be >= 1");
+  if (n == 0) return VH_OK;
+  if (!param || !grad || !m || !v) return fail(VH_ERR_INVALID, "vh_adamw_step: null pointer");
+  AdamArgs a{};
+  a.p = param;
+  a.g = grad;
+  a.m = m;
+  a.v = v;
+  a.n = n;
+  a.beta1 = beta1;
+  a.beta2 = beta2;
+  a.omb1 = 1.0f - beta1;
+  a.omb2 = 1.0f - beta2;
+  a.bc1 = 1.0f - powi_f32(beta1, t);
+  a.bc2 = 1.0f - powi_f32(beta2, t);
+  a.lr = lr;
+  a.lrwd = lr * weight_decay;
+  a.eps = eps;
+  const bool vec = n % 4 == 0 && aligned16(param) && aligned16(grad) && aligned16(m) && aligned16(v);
+  const int64_t blocks = std::min<int64_t>(cdiv(n / (vec ? 4 : 1), 256), 8192);
+  return launch(vec ? "vh_adamw_v4" : "vh_adamw_v1", (unsigned)blocks, 1, 256, 0, S(stream), a);
 }
 
 }  // extern "C"

@@ -51,6 +51,16 @@ struct ColReduceArgs {
   int32_t ncomp;
 };
 
+// Per-workgroup column sums of a [rows, C] block of rows (first stage of a
+// fixed-order row sum; the second stage is the column reduce above).
+struct ColPartialArgs {
+  const float* x;
+  float* part;  // [G][C]
+  int64_t rows;
+  int64_t rpb;  // rows per workgroup
+  int32_t C;
+};
+
 struct SoftmaxArgs {
   const float* x;   // fwd: scores; bwd: y (or x when input_is_x)
   const float* dy;  // bwd only
@@ -59,6 +69,40 @@ struct SoftmaxArgs {
   int32_t T;        // row length
   int32_t causal;   // 1: row r keeps columns [0, r % T], the rest are known masked
   int32_t input_is_x;
+  int32_t attn;     // 1: fused-attention numerics (p = e * (1/(sum + 1e-9)), fma sum of dy*y)
+};
+
+// C tile of one GEMM workgroup (host and device agree on the grid).
+#define VH_GEMM_TILE_M 128
+#define VH_GEMM_TILE_N 128
+
+struct GemmArgs {
+  const float* A;
+  const float* B;
+  float* C;
+  const float* E;  // optional addend E[m, n] (null = none)
+  int64_t M, N, K;
+  int64_t lda;  // A's non-unit stride: along m (k-contiguous A) or along k (m-contiguous A)
+  int64_t ldb;  // B's non-unit stride: along n (k-contiguous B) or along k (n-contiguous B)
+  int64_t ldc;  // C row stride; C's column stride is 1
+  int64_t sa1, sa2, sb1, sb2, sc1, sc2, se1, se2;  // strides of the two batch dims
+  int64_t sem, sen;                                // E strides along m and n
+  int32_t nb2;                                     // size of the inner batch dim
+  int32_t tiles_m, tiles_n;
+  int32_t accumulate;  // 1: C = C + result
+  int32_t causal;      // 0 none; 1 skip tiles above the diagonal; 2 k <= m; 3 k >= m
+  float alpha;
+};
+
+struct AdamArgs {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  int64_t n;
+  float beta1, beta2, omb1, omb2;  // omb = 1 - beta, rounded to f32 as the reference does
+  float bc1, bc2;                  // 1 - beta^t
+  float lr, lrwd, eps;             // lrwd = lr * weight_decay (f32)
 };
 
 struct EltArgs {
