@@ -1,0 +1,79 @@
+/*
+ * vearo_block.h -- C ABI of the config[4] training step: SimpleGPT with one
+ * TransformerBlock (token + position embedding, pre-LN block with fused causal
+ * attention and a GELU MLP, final layernorm, lm_head, cross-entropy), its
+ * autograd backward and one AdamW update, run entirely on one MI355X.
+ *
+ * This replaces, for this model, the reference's host-driven chain
+ *   SimpleGPT::forward        (crates/vearo-nn/src/lib.rs:745-791, 666-675)
+ *   loss.backward()           (crates/vearo-autograd/src/lib.rs:429-760)
+ *   AdamW::step               (crates/vearo-optim/src/lib.rs:105-123,
+ *                              Tensor::adamw_step tensor.rs:931-1023)
+ * issuing the same op sequence -- the forward modules' ops and, in reverse tape
+ * order, the autograd arms' ops -- through libvearo_hip.so. The model lives in
+ * device memory owned by the handle: parameters, gradients, AdamW moments and
+ * every activation the backward needs, allocated once. The causal mask is the
+ * model's -1e9 upper triangle, passed to the attention as its causal flag
+ * (identical results: exp underflows to exactly 0 either way).
+ *
+ * Parameters are numbered in SimpleGPT::parameters() order (nn:797-807):
+ *   0 wte[V,D] 1 wpe[P,D] 2 ln1.w[D] 3 ln1.b[D] 4 q.w[D,D] 5 q.b[D] 6 k.w 7 k.b
+ *   8 v.w 9 v.b 10 out.w 11 out.b 12 ln2.w 13 ln2.b 14 fc1.w[F,D] 15 fc1.b[F]
+ *   16 fc2.w[D,F] 17 fc2.b[D] 18 ln_f.w 19 ln_f.b 20 lm_head.w[V,D]
+ * All entry points return VH_OK (0) or a VH_ERR_* code; vh_last_error() has the
+ * text. vh_init() must have been called.
+ */
+#ifndef VEARO_BLOCK_H
+#define VEARO_BLOCK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VB_GPT_NPARAMS 21
+
+/* B x S tokens, model width D, H heads, MLP width F, vocabulary V,
+ * P = max_seq_len (>= S). D % H == 0. */
+typedef struct {
+  int64_t B, S, D, H, F, V, P;
+} vb_gpt_config;
+
+typedef struct vb_gpt vb_gpt;
+
+/* Allocates the model (parameters zero, LayerNorm weights one, AdamW moments
+ * zero, step count 0). Upload parameters through vb_gpt_param. */
+int vb_gpt_create(const vb_gpt_config* cfg, vb_gpt** out);
+void vb_gpt_destroy(vb_gpt* g);
+
+/* Device pointer and element count of parameter i, of its gradient (valid after
+ * a backward), and of the per-step token ids / targets buffers ([B, S] f32,
+ * the API's f32 ids) that vb_gpt_step reads. */
+int vb_gpt_param(vb_gpt* g, int i, float** ptr, int64_t* numel);
+int vb_gpt_grad(vb_gpt* g, int i, float** ptr, int64_t* numel);
+int vb_gpt_inputs(vb_gpt* g, float** ids, float** targets);
+
+/* One forward (and with backward != 0 the whole autograd backward) on the
+ * current ids/targets. The loss (mean cross-entropy, one float) is written to
+ * device memory at *loss_dev (vb_gpt_loss_ptr). Asynchronous on the library's
+ * stream; vh_sync() waits. */
+int vb_gpt_forward_backward(vb_gpt* g, int backward);
+float* vb_gpt_loss_ptr(vb_gpt* g);
+
+/* AdamW::step: increments the step count and updates every parameter from its
+ * gradient (optim:105-123), lr/betas/eps/weight decay as AdamW::new takes them. */
+int vb_gpt_adamw(vb_gpt* g, float lr, float beta1, float beta2, float eps, float weight_decay);
+
+/* Text of the last error of a vb_* call on this thread (a failing vh_* call's
+ * own text included). */
+const char* vb_last_error(void);
+
+/* The config[4] training step: forward + backward + AdamW. */
+int vb_gpt_train_step(vb_gpt* g, float lr, float beta1, float beta2, float eps, float weight_decay);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VEARO_BLOCK_H */
