@@ -9,7 +9,10 @@ over one synthetic batch at GPT-2-small shape,
 issued in that order on the runtime stream, as a training step meets them
 (forward, then backward in reverse). Other configs of BASELINE.json are
 available with --workload (gelu_bias, embedding_uniform, embedding_zipf,
-cross_entropy, layernorm_cfg0); each prints its own line.
+cross_entropy, layernorm_cfg0, gpt2_block); each prints its own line.
+gpt2_block is config[4]'s training step (token+position embedding, one pre-LN
+transformer block, final layernorm, lm_head, cross-entropy, backward, AdamW);
+its value is milliseconds per step and its roofline is the f32 matrix cores.
 
 Inputs are resident in HBM before timing. Buffers that would otherwise stay in
 the 256 MB MALL between uses alternate between two sets (or are flushed by the
@@ -40,6 +43,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "LayerNorm/softmax fwd+bwd HBM GB/s (% of ~8 TB/s peak); GPT block step ms"
 PEAK_GBPS = 8000.0
+PEAK_F32_MFMA_TFLOPS = 157.3  # MI355X dense f32 matrix peak
 SEED = 0x5EED0000
 
 
@@ -289,9 +293,117 @@ def wl_cross_entropy(vh):
         (L, T, GO, LOSS, DL, SC), None
 
 
-WORKLOADS = {"ln_softmax": wl_ln_softmax, "layernorm_cfg0": wl_layernorm_cfg0, "gelu_bias": wl_gelu_bias,
+def gpt_fwd_flops(B, S, D, H, F, V):
+    R = B * S
+    gemm = 2 * R * D * D * 4 + 2 * R * D * F * 2   # q, k, v, out; fc1, fc2
+    attn = 2 * 2 * B * S * S * D                    # q k^T and p v over all heads (dense)
+    head = 2 * R * D * V                            # lm_head
+    return gemm + attn + head
+
+
+def wl_gpt2_block(vh):
+    """config[4]: SimpleGPT(V=50257, S=1024, D=768, H=12, 1 block, MLP 3072),
+    B=16, one training step = forward + autograd backward + AdamW (lr 0.02,
+    betas 0.9/0.95, eps 1e-8, wd 0.01, verification_harness.rs:203-210)."""
+    from vearo_amd import _block
+    cfg = (16, 1024, 768, 12, 3072, 50257, 1024)
+    B, S, D, H, F, V, P = cfg
+    g = _block.Gpt(_block.GptConfig(*cfg))
+    r = np.random.default_rng(SEED + 4)
+    params = []
+    for name, sh in zip(_block.PARAM_NAMES, g.shapes):
+        if name.startswith("ln") and name.endswith("_w"):
+            params.append(np.ones(sh, np.float32))
+        elif name.startswith("ln"):
+            params.append(np.zeros(sh, np.float32))
+        else:
+            params.append(r.standard_normal(sh, dtype=np.float32) * np.float32(0.02))
+    g.set_params(params)
+    ids = r.integers(0, V, size=(B, S)).astype(np.float32)
+    tg = r.integers(0, V, size=(B, S)).astype(np.float32)
+    g.set_inputs(ids, tg)
+    flops = 3 * gpt_fwd_flops(B, S, D, H, F, V)  # fwd + bwd (2x fwd), the usual accounting
+    ops = [("train_step", flops, lambda i: _block.lib.vb_gpt_train_step(g.h, 0.02, 0.9, 0.95, 1e-8, 0.01))]
+    # The dominant kernel, timed on its own after the timed loop: the lm_head
+    # forward GEMM logits[16384, 50257] = lnf[16384, 768] W^T, through the same
+    # vh_gemm path the step uses, on scratch buffers of the same shapes.
+    A = vh.DeviceBuffer.from_array(r.standard_normal((B * S, D), dtype=np.float32))
+    W = vh.DeviceBuffer.from_array(params[20])
+    C = vh.DeviceBuffer(4 * B * S * V)
+    d = vh.VhGemmDesc()
+    d.M, d.N, d.K = B * S, V, D
+    d.a, d.a_sm, d.a_sk = A.ptr, D, 1
+    d.b, d.b_sk, d.b_sn = W.ptr, 1, D
+    d.c, d.c_sm = C.ptr, V
+    d.batch[0] = d.batch[1] = 1
+    d.alpha = 1.0
+    probe = ("lm_head_gemm", 2 * B * S * D * V, lambda i: vh.lib.vh_gemm(ctypes.byref(d), None))
+
+    def cpu(budget):
+        import oracle
+        ocfg = oracle.GptConfig(1, S, D, H, F, V, P)
+        t0 = time.perf_counter()
+        _, grads = oracle.gpt_step(ocfg, params, ids[:1], tg[:1])
+        t_fb = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        for p, gr in zip(params, grads):
+            oracle.adamw_step(p.copy(), gr, np.zeros_like(p), np.zeros_like(p), 1, 0.02, 0.9, 0.95, 1e-8, 0.01)
+        t_adam = time.perf_counter() - t0
+        ms = (B * t_fb + t_adam) * 1e3
+        threads = int(os.environ.get("VO_THREADS") or os.environ.get("OMP_NUM_THREADS") or os.cpu_count())
+        return ms, threads, (f"oracle SimpleGPT forward+backward for one sequence (B=1, S={S}) took "
+                             f"{t_fb:.1f} s and AdamW over all {sum(p.size for p in params)} parameters "
+                             f"{t_adam:.2f} s; value = 16 x the former + the latter (every op but AdamW "
+                             f"scales with B). Matmuls threaded as the reference's are; attention threaded "
+                             f"over heads (the reference runs it on one thread)")
+
+    info = {"workload": "cfg[4] GPT-2-small block training step: B=16, T=1024, C=768, H=12, MLP 3072, "
+                        "V=50257, one block; fwd + backward + AdamW",
+            "flops_per_step": flops, "_mode": "step_ms", "_probe": probe}
+    return ops, info, cpu, (g, A, W, C, d), None
+
+
+WORKLOADS = {"ln_softmax": wl_ln_softmax, "gpt2_block": wl_gpt2_block, "layernorm_cfg0": wl_layernorm_cfg0, "gelu_bias": wl_gelu_bias,
              "embedding_uniform": wl_embedding_uniform, "embedding_zipf": wl_embedding_zipf,
              "cross_entropy": wl_cross_entropy}
+
+
+def report_step_ms(args, vh, hip, stream, ops, info, cpu, per, wall, K):
+    """The bench line of a training-step workload: value = ms per step."""
+    pname, pflops, pcall = info.pop("_probe")
+    info.pop("_mode")
+    reps = 10
+    vh.check(pcall(0))
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0, stream)
+    for i in range(reps):
+        vh.check(pcall(i))
+    hip.record(e1, stream)
+    hip.sync(stream)
+    p_s = hip.elapsed_ms(e0, e1) / reps / 1e3
+    achieved = pflops / p_s / 1e12
+    name, flops, _ = ops[0]
+    step_s = per[name] / K / 1e3
+    kernels = {name: {"avg_ms": round(step_s * 1e3, 3), "flops": flops,
+                      "tflops": round(flops / step_s / 1e12, 2)},
+               pname: {"avg_us": round(p_s * 1e6, 1), "flops": pflops, "tflops": round(achieved, 2)}}
+    roofline = {"bound": "mfma", "kernel": pname, "achieved": round(achieved, 2), "peak": PEAK_F32_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_F32_MFMA_TFLOPS, 4), "traffic": None}
+    cpu_res = None
+    if not args.no_cpu:
+        ms, threads, sample = cpu(args.cpu_seconds)
+        cpu_res = {"value": round(ms, 1), "unit": "ms per step", "cores": threads, "kind": "port",
+                   "sample": sample}
+    res = {
+        "metric": "GPT block step ms (config[4]: fwd + bwd + AdamW)", "value": round(wall / K * 1e3, 3),
+        "unit": "ms", "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": round(wall / K * 1e3, 3),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random ids/targets, weights ~N(0,0.02))", "config": info,
+        "tflops_per_s": round(info["flops_per_step"] / (wall / K) / 1e12, 2),
+        "frac_of_peak": round(info["flops_per_step"] / (wall / K) / 1e12 / PEAK_F32_MFMA_TFLOPS, 4),
+        "kernels": kernels, "roofline": roofline, "cpu_baseline": cpu_res,
+    }
+    print(json.dumps(res), flush=True)
 
 
 def main():
@@ -363,6 +475,10 @@ def main():
         gbps = nb / avg_s / 1e9
         kernels[n] = {"avg_us": round(avg_s * 1e6, 2), "bytes": nb, "gbps": round(gbps, 1),
                       "frac": round(gbps / PEAK_GBPS, 4)}
+    if info.get("_mode") == "step_ms":
+        report_step_ms(args, vh, hip, stream, ops, info, cpu, per, wall, K)
+        del keep
+        return
     step_bytes = sum(o[1] for o in ops)
     value = step_bytes / (wall / K) / 1e9
     dom = max(names, key=lambda n: per[n])
