@@ -189,6 +189,15 @@ size_t vh_cross_entropy_fwd_scratch_bytes(int64_t B);
 int vh_cross_entropy_bwd(const float* logits, const float* targets,
                          const float* grad_out, float* dlogits, int64_t B, int64_t V,
                          void* stream);
+/* The same with a row stride ld >= V for logits and dlogits (a rank-2 view
+ * with unit column stride, as the reference's CPU path accepts any strides).
+ * The backward writes only the first V columns of each dlogits row. */
+int vh_cross_entropy_fwd_ld(const float* logits, int64_t ld, const float* targets,
+                            float* loss, int64_t B, int64_t V, void* scratch,
+                            size_t scratch_bytes, void* stream);
+int vh_cross_entropy_bwd_ld(const float* logits, int64_t ld, const float* targets,
+                            const float* grad_out, float* dlogits, int64_t B, int64_t V,
+                            void* stream);
 
 /* ------------------------------------- composites the autograd arms drive -- */
 

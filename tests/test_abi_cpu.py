@@ -113,7 +113,7 @@ def launcher_kernel_names():
               "vh_emb_tokens", "vh_emb_alloc", "vh_emb_place", "vh_fill",
               "vh_binary_strided_i32", "vh_binary_strided_i64", "vh_reduce_thread",
               "vh_reduce_wave", "vh_strided_copy_i32", "vh_strided_copy_i64", "vh_col_partial",
-              "vh_adamw_v1", "vh_adamw_v4"}
+              "vh_adamw_v1", "vh_adamw_v4", "vh_gemm_reduce"}
     for a in ("k4", "k1", "m4", "m1"):
         for b in ("k4", "k1", "n4", "n1"):
             names.add(f"vh_gemm_{a}_{b}")

@@ -272,3 +272,53 @@ def test_sum_rows(vh, rows, C):
     X, OUT = dev(vh, x), out(vh, (C,))
     vh.check(vh.lib.vh_sum_rows(X.ptr, rows, C, OUT.ptr, None, 0, None))
     assert_parity(fetch(vh, OUT, (C,)), O.reduce_to(x, (C,)), x.astype(np.float64).sum(axis=0), name="sum_rows")
+
+
+@pytest.mark.parametrize("M,N,K", [(200, 150, 8192), (768, 768, 16384), (3072, 768, 4096)])
+def test_gemm_split_k(vh, M, N, K):
+    """Few C tiles over a long K (the weight gradients) take the split-K path:
+    partials summed in a fixed order, then the epilogue."""
+    print("split-k", M, N, K, flush=True)
+    r = np.random.default_rng(M + N + K)
+    # dW = dy^T x as the block step issues it: A m-contiguous (dy [K, M]), B = x [K, N].
+    dy = (r.standard_normal((K, M)) * 0.02).astype(np.float32)
+    x = r.standard_normal((K, N), dtype=np.float32)
+    bias = (r.standard_normal(N) * 0.02).astype(np.float32)
+    c0 = r.standard_normal((M, N), dtype=np.float32)
+    DY, X, BI = dev(vh, dy), dev(vh, x), dev(vh, bias)
+    ref = O.matmul(np.ascontiguousarray(dy.T), x)
+    ref64 = dy.T.astype(np.float64) @ x.astype(np.float64)
+    C = out(vh, (M, N))
+    d = gemm_desc(vh, M, N, K, DY.ptr, 1, M, X.ptr, N, 1, C.ptr, N)
+    vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+    got = fetch(vh, C, (M, N))
+    assert_parity(got, ref, ref64, name="split-k plain")
+    C2 = dev(vh, c0)
+    d = gemm_desc(vh, M, N, K, DY.ptr, 1, M, X.ptr, N, 1, C2.ptr, N, alpha=0.5, accumulate=1,
+                  e=BI.ptr, e_sm=0, e_sn=1)
+    vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+    assert_parity(fetch(vh, C2, (M, N)), c0 + (ref * np.float32(0.5) + bias),
+                  c0.astype(np.float64) + (ref64 * 0.5 + bias), name="split-k epilogue")
+    # Deterministic: the same call gives the same bits.
+    C3 = out(vh, (M, N))
+    d = gemm_desc(vh, M, N, K, DY.ptr, 1, M, X.ptr, N, 1, C3.ptr, N)
+    vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+    np.testing.assert_array_equal(fetch(vh, C3, (M, N)), got)
+
+
+def test_cross_entropy_row_stride(vh):
+    B, V, ld = 37, 1001, 1004
+    r = np.random.default_rng(12)
+    logits = r.standard_normal((B, V), dtype=np.float32)
+    tg = r.integers(0, V, size=B).astype(np.float32)
+    padded = np.full((B, ld), 7.0, np.float32)
+    padded[:, :V] = logits
+    L, T, GO = dev(vh, padded), dev(vh, tg), dev(vh, np.float32([1.3]))
+    LOSS = out(vh, (1,))
+    DL = dev(vh, np.full((B, ld), -5.0, np.float32))
+    vh.check(vh.lib.vh_cross_entropy_fwd_ld(L.ptr, ld, T.ptr, LOSS.ptr, B, V, None, 0, None))
+    vh.check(vh.lib.vh_cross_entropy_bwd_ld(L.ptr, ld, T.ptr, GO.ptr, DL.ptr, B, V, None))
+    assert_parity(fetch(vh, LOSS, (1,)), O.cross_entropy(logits, tg), name="loss")
+    dl = fetch(vh, DL, (B, ld))
+    assert_parity(dl[:, :V], O.cross_entropy_backward(logits, tg, np.float32([1.3])), name="dlogits")
+    assert np.all(dl[:, V:] == -5.0)  # only the first V columns are written

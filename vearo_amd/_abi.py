@@ -120,6 +120,11 @@ SIGNATURES = {
     ),
     "vh_cross_entropy_fwd_scratch_bytes": (c_size_t, [c_int64]),
     "vh_cross_entropy_bwd": (c_int, [fp, fp, fp, fp, c_int64, c_int64, c_void_p]),
+    "vh_cross_entropy_fwd_ld": (
+        c_int,
+        [fp, c_int64, fp, fp, c_int64, c_int64, c_void_p, c_size_t, c_void_p],
+    ),
+    "vh_cross_entropy_bwd_ld": (c_int, [fp, c_int64, fp, fp, fp, c_int64, c_int64, c_void_p]),
     "vh_binary": (c_int, [c_int, fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, c_void_p]),
     "vh_reduce": (c_int, [c_int, fp, POINTER(VhLayout), c_int, fp, c_void_p]),
     "vh_strided_copy": (c_int, [fp, POINTER(VhLayout), fp, c_void_p]),

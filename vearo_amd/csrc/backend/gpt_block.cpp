@@ -13,6 +13,9 @@
 //     B*S rows (same sum, f32 rounding of a different grouping)
 // The attention's q/k/v/out stay in the Linear layout [B, S, H, Dk]; the
 // reshape/transpose views of nn:585-601 are passed as strides, so no copy runs.
+// The logits and their gradient have rows padded to Vp = V rounded up to 4
+// (zero columns), and lm_head's weight is followed by Vp - V zero rows, so the
+// three lm_head products run on 128-bit loads; the padding adds exact zeros.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -56,7 +59,7 @@ vh_layout contiguous(std::initializer_list<int64_t> dims) {
 
 struct vb_gpt {
   vb_gpt_config c{};
-  int64_t R = 0, Dk = 0;
+  int64_t R = 0, Dk = 0, Vp = 0;
   int64_t off[VB_GPT_NPARAMS] = {}, numel[VB_GPT_NPARAMS] = {};
   size_t block_floats = 0;
   float *P = nullptr, *G = nullptr, *M = nullptr, *Vm = nullptr;  // params, grads, AdamW m and v
@@ -84,7 +87,7 @@ struct vb_gpt {
 
   // out[R, Dout] = x[R, Din] W^T (+ bias) (+ out when accumulate): Linear::forward.
   int linear(const float* x, int64_t Din, const float* W, int64_t Dout, const float* bias, float* out,
-             int accumulate) {
+             int accumulate, int64_t ldc = 0) {
     vh_gemm_desc d{};
     d.M = R;
     d.N = Dout;
@@ -96,7 +99,7 @@ struct vb_gpt {
     d.b_sk = 1;
     d.b_sn = Din;
     d.c = out;
-    d.c_sm = Dout;
+    d.c_sm = ldc ? ldc : Dout;
     d.batch[0] = d.batch[1] = 1;
     d.e = bias;
     d.e_sm = 0;
@@ -184,8 +187,8 @@ struct vb_gpt {
     VB(vh_d2d(h2, h1, (size_t)(R * D) * sizeof(float), nullptr));
     VB(linear(g, F, p(16), D, p(17), h2, 1));  // h2 = h1 + (g W_fc2^T + b_fc2)
     VB(vh_layernorm_fwd(h2, p(18), p(19), lnf, R, D, kEps, nullptr));
-    VB(linear(lnf, D, p(20), V, nullptr, logits, 0));
-    VB(vh_cross_entropy_fwd(logits, tg, loss, R, V, nullptr, 0, nullptr));
+    VB(linear(lnf, D, p(20), V, nullptr, logits, 0, Vp));
+    VB(vh_cross_entropy_fwd_ld(logits, Vp, tg, loss, R, V, nullptr, 0, nullptr));
     return VH_OK;
   }
 
@@ -193,10 +196,11 @@ struct vb_gpt {
     const int64_t D = c.D, F = c.F, V = c.V;
     const vh_layout lrd = contiguous({R, D});
     // cross_entropy arm (autograd:594-599), grad_out = 1 (backward_callback, :795-798).
-    VB(vh_cross_entropy_bwd(logits, tg, one, dlogits, R, V, nullptr));
-    // lm_head (rank-2 input, no bias).
-    VB(linear_dx(dlogits, V, p(20), D, dlnf, 0));
-    VB(linear_dw(dlogits, V, lnf, D, gr(20)));
+    VB(vh_cross_entropy_bwd_ld(logits, Vp, tg, one, dlogits, R, V, nullptr));
+    // lm_head (rank-2 input, no bias), over the padded vocabulary: the zero
+    // columns of dlogits meet the zero rows after the weight.
+    VB(linear_dx(dlogits, Vp, p(20), D, dlnf, 0));
+    VB(linear_dw(dlogits, Vp, lnf, D, gr(20)));
     VB(vh_layernorm_bwd(h2, p(18), dlnf, dh, gr(18), gr(19), R, D, kEps, nullptr, 0, nullptr));
     // h2 = h1 + f2: h1 and f2 both receive dh.
     VB(vh_sum_rows(dh, R, D, gr(17), nullptr, 0, nullptr));
@@ -250,6 +254,7 @@ int vb_gpt_create(const vb_gpt_config* cfg, vb_gpt** out) {
   g->c = c;
   g->R = c.B * c.S;
   g->Dk = c.D / c.H;
+  g->Vp = (c.V + 3) / 4 * 4;
   const int64_t D = c.D, F = c.F;
   const int64_t sizes[VB_GPT_NPARAMS] = {c.V * D, c.P * D, D, D, D * D, D, D * D, D, D * D, D, D * D, D,
                                          D,       D,       F * D, F, D * F, D, D, D, c.V * D};
@@ -259,8 +264,9 @@ int vb_gpt_create(const vb_gpt_config* cfg, vb_gpt** out) {
     g->numel[i] = sizes[i];
     o += ((size_t)sizes[i] + 63) & ~size_t(63);  // 256-byte aligned tensors
   }
+  o += (((size_t)((g->Vp - c.V) * D)) + 63) & ~size_t(63);  // zero rows after lm_head.w
   g->block_floats = o;
-  const int64_t R = g->R, V = c.V;
+  const int64_t R = g->R, Vp = g->Vp;
   int rc = VH_OK;
   auto A = [&](float** p, int64_t n, int zero = 0) {
     if (rc == VH_OK) rc = g->alloc(p, n, zero);
@@ -275,8 +281,8 @@ int vb_gpt_create(const vb_gpt_config* cfg, vb_gpt** out) {
                     &g->dh0})
     A(p, R * D);
   for (float** p : {&g->y1, &g->g, &g->dg, &g->df1}) A(p, R * F);
-  A(&g->logits, R * V);
-  A(&g->dlogits, R * V);
+  A(&g->logits, R * Vp, 1);
+  A(&g->dlogits, R * Vp, 1);
   A(&g->loss, 1, 1);
   A(&g->one, 1);
   if (rc == VH_OK) {

@@ -12,10 +12,13 @@
 // Tiling: a 256-thread workgroup computes a 128 x 128 tile of C; its 4 waves
 // own 64 x 64 quadrants as 2 x 2 matrix-core tiles of 32 x 32. K advances in
 // tiles of 32, double-buffered through LDS: the global loads of tile t+1 are in
-// flight while tile t is multiplied. LDS holds both operands k-contiguous
-// ([row][k], rows padded to 36 floats) whatever their layout in HBM, so each
-// lane reads its fragments as 128-bit LDS loads: lane half h (lanes 32h..32h+31)
-// takes k in [16h, 16h+16) of the tile, step s pairing k = s with k = 16 + s.
+// flight while tile t is multiplied. LDS keeps each operand in the orientation
+// of its HBM layout, so staging is 128-bit and bank-conflict free both ways:
+// a k-contiguous operand as [row][k] (rows padded to 36 floats), read as 128-bit
+// fragments; a row-contiguous one (a transposed view) as [k][row] (132 floats
+// per k), read 32 bits at a time with consecutive lanes on consecutive rows.
+// Lane half h (lanes 32h..32h+31) takes k in [16h, 16h+16) of the tile, step s
+// pairing k = s with k = 16 + s.
 // A operand layouts: k-contiguous (A[m, k] at m*lda + k) or m-contiguous
 // (A[m, k] at k*lda + m, a transposed view); the same for B. Global loads are
 // 128-bit when the layout allows (host-checked alignment), else 32-bit.
@@ -31,7 +34,9 @@
 #define GM_TM VH_GEMM_TILE_M
 #define GM_TN VH_GEMM_TILE_N
 #define GM_TK 32
-#define GM_LS (GM_TK + 4)  // LDS row stride (floats): 16-byte aligned rows, staggered banks
+#define GM_LS (GM_TK + 4)  // [row][k] LDS row stride (floats): 16-byte aligned rows, staggered banks
+#define GM_LT (GM_TM + 4)  // [k][row] LDS stride (floats)
+#define GM_STAGE (GM_TM * GM_LS > GM_TK * GM_LT ? GM_TM * GM_LS : GM_TK * GM_LT)
 #define GM_GROUP 8         // tile rows per group in the launch order (L2 reuse of B)
 
 typedef float vh_f32x16 __attribute__((ext_vector_type(16)));
@@ -92,12 +97,27 @@ VH_DEV void gm_store_lds(float* S, int tid, const float (&st)[16]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int k = (tid >> 5) + 8 * i, r = (tid & 31) * 4;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) S[(r + e) * GM_LS + k] = st[4 * i + e];
+      vh_f4 v = {st[4 * i], st[4 * i + 1], st[4 * i + 2], st[4 * i + 3]};
+      *reinterpret_cast<vh_f4*>(S + k * GM_LT + r) = v;
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) S[(tid & 127) * GM_LS + (tid >> 7) + 2 * i] = st[i];
+    for (int i = 0; i < 16; ++i) S[((tid >> 7) + 2 * i) * GM_LT + (tid & 127)] = st[i];
+  }
+}
+
+// Fragments of rows `row` and `row + 32` for k = k0 .. k0+3 (4 matrix-core steps).
+template <bool KC>
+VH_DEV void gm_frag(const float* S, int row, int k0, vh_f4& f0, vh_f4& f1) {
+  if constexpr (KC) {
+    f0 = *reinterpret_cast<const vh_f4*>(S + row * GM_LS + k0);
+    f1 = *reinterpret_cast<const vh_f4*>(S + (row + 32) * GM_LS + k0);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f0[e] = S[(k0 + e) * GM_LT + row];
+      f1[e] = S[(k0 + e) * GM_LT + row + 32];
+    }
   }
 }
 
@@ -119,15 +139,16 @@ VH_DEV void gm_tile_of(int bid, int nblk, int tiles_m, int tiles_n, int& tm, int
 
 template <bool A_KC, bool A_VEC, bool B_KC, bool B_VEC>
 VH_DEV void gemm_f32_impl(const GemmArgs& a) {
-  __shared__ __attribute__((aligned(16))) float As[2][GM_TM * GM_LS];
-  __shared__ __attribute__((aligned(16))) float Bs[2][GM_TN * GM_LS];
+  __shared__ __attribute__((aligned(16))) float As[2][GM_STAGE];
+  __shared__ __attribute__((aligned(16))) float Bs[2][GM_STAGE];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   int tm, tn;
   gm_tile_of(blockIdx.x, gridDim.x, a.tiles_m, a.tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * GM_TM, n0 = (int64_t)tn * GM_TN;
   if (a.causal == 1 && n0 > m0 + GM_TM - 1) return;  // the whole tile is masked
 
-  const int64_t b1 = blockIdx.y / a.nb2, b2 = blockIdx.y % a.nb2;
+  const bool split = a.ksplit > 1;
+  const int64_t b1 = split ? 0 : blockIdx.y / a.nb2, b2 = split ? 0 : blockIdx.y % a.nb2;
   const float* A = a.A + b1 * a.sa1 + b2 * a.sa2;
   const float* B = a.B + b1 * a.sb1 + b2 * a.sb2;
   float* C = a.C + b1 * a.sc1 + b2 * a.sc2;
@@ -135,6 +156,10 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
   int64_t kb = 0, ke = a.K;
   if (a.causal == 2) ke = m0 + GM_TM < a.K ? m0 + GM_TM : a.K;
   if (a.causal == 3) kb = (m0 / GM_TK) * GM_TK;
+  if (split) {
+    kb = (int64_t)blockIdx.y * a.kchunk;
+    ke = kb + a.kchunk < a.K ? kb + a.kchunk : a.K;
+  }
 
   vh_f32x16 acc[2][2];
 #pragma unroll
@@ -158,14 +183,11 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
       gm_load<A_KC, A_VEC>(A, a.lda, m0, a.M, k0 + GM_TK, a.K, tid, sa);
       gm_load<B_KC, B_VEC>(B, a.ldb, n0, a.N, k0 + GM_TK, a.K, tid, sb);
     }
-    const float* as = As[s] + (wm * 64 + li) * GM_LS + h * 16;
-    const float* bs = Bs[s] + (wn * 64 + li) * GM_LS + h * 16;
 #pragma unroll
     for (int kc = 0; kc < 16; kc += 4) {
-      const vh_f4 a0 = *reinterpret_cast<const vh_f4*>(as + kc);
-      const vh_f4 a1 = *reinterpret_cast<const vh_f4*>(as + 32 * GM_LS + kc);
-      const vh_f4 b0 = *reinterpret_cast<const vh_f4*>(bs + kc);
-      const vh_f4 bv1 = *reinterpret_cast<const vh_f4*>(bs + 32 * GM_LS + kc);
+      vh_f4 a0, a1, b0, bv1;
+      gm_frag<A_KC>(As[s], wm * 64 + li, h * 16 + kc, a0, a1);
+      gm_frag<B_KC>(Bs[s], wn * 64 + li, h * 16 + kc, b0, bv1);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], b0[e], acc[0][0], 0, 0, 0);
@@ -184,6 +206,21 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
 
   // Epilogue. Accumulator register r of a 32 x 32 tile holds row
   // 8*(r/4) + 4*h + r%4, column li.
+  if (split) {  // raw partial sums; the reduce applies the epilogue
+    float* W = a.ws + (int64_t)blockIdx.y * a.M * a.N;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int64_t n = n0 + wn * 64 + nt * 32 + li;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (m < a.M && n < a.N) W[m * a.N + n] = acc[mt][nt][r];
+        }
+      }
+    return;
+  }
   const float* E = a.E ? a.E + b1 * a.se1 + b2 * a.se2 : nullptr;
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
@@ -202,5 +239,22 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
         }
       }
     }
+  }
+}
+
+// C[m, n] = epilogue(sum over y of ws[y][m][n], y ascending): the split-K
+// partials in a fixed order, so the result does not depend on timing.
+VH_DEV void gemm_reduce_impl(const GemmReduceArgs& a) {
+  const int64_t total = a.M * a.N;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t m = i / a.N, n = i % a.N;
+    float s = a.ws[i];
+    for (int y = 1; y < a.ksplit; ++y) s += a.ws[(int64_t)y * total + i];
+    float v = s * a.alpha;
+    if (a.E) v = v + a.E[m * a.sem + n * a.sen];
+    float* cp = a.C + m * a.ldc + n;
+    if (a.accumulate) v = *cp + v;
+    *cp = v;
   }
 }

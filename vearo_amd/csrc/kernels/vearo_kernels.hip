@@ -166,6 +166,8 @@ K_GEMM(false, false, true, false, vh_gemm_m1_k1)
 K_GEMM(false, false, false, true, vh_gemm_m1_n4)
 K_GEMM(false, false, false, false, vh_gemm_m1_n1)
 
+extern "C" __global__ void __launch_bounds__(256) vh_gemm_reduce(GemmReduceArgs a) { gemm_reduce_impl(a); }
+
 // AdamW
 extern "C" __global__ void __launch_bounds__(256) vh_adamw_v1(AdamArgs a) { adamw_impl<1>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_adamw_v4(AdamArgs a) { adamw_impl<4>(a); }

@@ -6,7 +6,7 @@
 // cross_entropy_backward (lib.rs:1053-1127): dl = go * (p - 1[c == t]) / B with
 // p = exp(l - max) / sum. Targets are f32 class ids, rounded like Rust's round().
 //
-// Layout: logits / dlogits [B, V] row-major, targets [B], one 1024-thread
+// Layout: logits / dlogits [B, V] with row stride ld (>= V), targets [B], one 1024-thread
 // workgroup (16 waves) per row. When V <= 1024*NV the row is held in VGPRs and
 // read from HBM once (fwd 4 B/elem read; bwd 4 B read + 4 B write). Longer rows
 // take the streaming variant: one online max/sum pass, plus a write pass in bwd.
@@ -35,7 +35,7 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
   __shared__ float red[16];
   const int64_t row = blockIdx.x;
   const int V = a.V;
-  const float* lr = a.logits + row * V;
+  const float* lr = a.logits + row * a.ld;
   // One buffer resource per row: base and bound live in SGPRs, the unit offset
   // k*4096 goes in the scalar offset field, so the cached row costs one VGPR
   // per float and no per-load address registers.
@@ -69,7 +69,7 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
     const float go = *a.grad_out;
     const float Bf = (float)a.B;
     const __amdgpu_buffer_rsrc_t rout =
-        __builtin_amdgcn_make_buffer_rsrc(a.out + row * V, 0, V * 4, VH_BUF_WORD3);
+        __builtin_amdgcn_make_buffer_rsrc(a.out + row * a.ld, 0, V * 4, VH_BUF_WORD3);
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int c = threadIdx.x + k * 1024;
@@ -88,7 +88,7 @@ VH_DEV void xent_stream_impl(const XentArgs& a) {
   __shared__ float red[16];
   const int64_t row = blockIdx.x;
   const int V = a.V;
-  const float* lr = a.logits + row * V;
+  const float* lr = a.logits + row * a.ld;
   float m = -INFINITY, s = 0.0f;
   for (int c = threadIdx.x; c < V; c += 1024) {
     const float x = lr[c];
@@ -108,7 +108,7 @@ VH_DEV void xent_stream_impl(const XentArgs& a) {
   } else {
     const float go = *a.grad_out;
     const float Bf = (float)a.B;
-    float* o = a.out + row * V;
+    float* o = a.out + row * a.ld;
     for (int c = threadIdx.x; c < V; c += 1024) {
       const float p = expf(lr[c] - M) / s;
       const float ind = c == t ? 1.0f : 0.0f;

@@ -791,32 +791,44 @@ size_t vh_cross_entropy_fwd_scratch_bytes(int64_t B) {
   return B <= 0 ? 0 : align256((size_t)B * sizeof(float));
 }
 
-int vh_cross_entropy_fwd(const float* logits, const float* targets, float* loss, int64_t B,
-                         int64_t V, void* scratch, size_t scratch_bytes, void* stream) {
+int vh_cross_entropy_fwd_ld(const float* logits, int64_t ld, const float* targets, float* loss, int64_t B,
+                            int64_t V, void* scratch, size_t scratch_bytes, void* stream) {
   VH_TRY(require_init());
   if (B <= 0) return fail(VH_ERR_INVALID, "Batch size must be greater than 0");
   if (V <= 0) return fail(VH_ERR_INVALID, "vh_cross_entropy_fwd: vocabulary must be > 0");
+  if (ld < V) return fail(VH_ERR_INVALID, "vh_cross_entropy_fwd: row stride below V");
   if (!logits || !targets || !loss) return fail(VH_ERR_INVALID, "vh_cross_entropy_fwd: null pointer");
   if (V > INT32_MAX || B > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_cross_entropy_fwd: size exceeds int32");
   hipStream_t s = S(stream);
   Scratch sc;
   VH_TRY(sc.get(scratch, scratch_bytes, vh_cross_entropy_fwd_scratch_bytes(B)));
-  XentArgs a{logits, targets, nullptr, static_cast<float*>(sc.p), g_rt.err, B, (int32_t)V};
+  XentArgs a{logits, targets, nullptr, static_cast<float*>(sc.p), g_rt.err, B, ld, (int32_t)V};
   VH_TRY(launch(xent_kernel("fwd", V), (unsigned)B, 1, 1024, 0, s, a));
   XentReduceArgs r{static_cast<float*>(sc.p), loss, B};
   return launch("vh_xent_reduce", 1, 1, 1024, 0, s, r);
 }
 
-int vh_cross_entropy_bwd(const float* logits, const float* targets, const float* grad_out,
-                         float* dlogits, int64_t B, int64_t V, void* stream) {
+int vh_cross_entropy_fwd(const float* logits, const float* targets, float* loss, int64_t B,
+                         int64_t V, void* scratch, size_t scratch_bytes, void* stream) {
+  return vh_cross_entropy_fwd_ld(logits, V, targets, loss, B, V, scratch, scratch_bytes, stream);
+}
+
+int vh_cross_entropy_bwd_ld(const float* logits, int64_t ld, const float* targets, const float* grad_out,
+                            float* dlogits, int64_t B, int64_t V, void* stream) {
   VH_TRY(require_init());
   if (B <= 0) return fail(VH_ERR_INVALID, "Batch size must be greater than 0");
   if (V <= 0) return fail(VH_ERR_INVALID, "vh_cross_entropy_bwd: vocabulary must be > 0");
+  if (ld < V) return fail(VH_ERR_INVALID, "vh_cross_entropy_bwd: row stride below V");
   if (!logits || !targets || !grad_out || !dlogits)
     return fail(VH_ERR_INVALID, "vh_cross_entropy_bwd: null pointer");
   if (V > INT32_MAX || B > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_cross_entropy_bwd: size exceeds int32");
-  XentArgs a{logits, targets, grad_out, dlogits, g_rt.err, B, (int32_t)V};
+  XentArgs a{logits, targets, grad_out, dlogits, g_rt.err, B, ld, (int32_t)V};
   return launch(xent_kernel("bwd", V), (unsigned)B, 1, 1024, 0, S(stream), a);
+}
+
+int vh_cross_entropy_bwd(const float* logits, const float* targets, const float* grad_out,
+                         float* dlogits, int64_t B, int64_t V, void* stream) {
+  return vh_cross_entropy_bwd_ld(logits, V, targets, grad_out, dlogits, B, V, stream);
 }
 
 // ------------------------------------------------------------ composites --
@@ -974,6 +986,47 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
   const std::string name = std::string("vh_gemm_") + (akc ? "k" : "m") + (avec ? "4" : "1") + "_" +
                            (bkc ? "k" : "n") + (bvec ? "4" : "1");
   hipStream_t s = S(stream);
+  // Split K when one unbatched product has too few C tiles to fill the chip
+  // (the weight gradients: 768 x 768 outputs over K = 16384 rows): each split
+  // writes its raw partial, a fixed-order reduce sums them and applies the
+  // epilogue.
+  const int64_t tiles = tiles_m * tiles_n;
+  const int64_t slots = 2 * std::max(g_rt.cu_count, 1);
+  if (d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE && tiles < slots && K >= 4096) {
+    int64_t ks = std::min<int64_t>({16, cdiv(slots, tiles), K / 1024});
+    const int64_t kchunk = cdiv(cdiv(K, ks), 32) * 32;
+    ks = cdiv(K, kchunk);
+    if (ks > 1) {
+      void* ws = nullptr;
+      VH_TRY(g_arena.alloc((size_t)(ks * M * N) * sizeof(float), &ws));
+      GemmArgs g{};
+      g.A = d->a;
+      g.B = d->b;
+      g.C = d->c;
+      g.M = M;
+      g.N = N;
+      g.K = K;
+      g.lda = lda;
+      g.ldb = ldb;
+      g.ldc = d->c_sm;
+      g.nb2 = 1;
+      g.tiles_m = (int32_t)tiles_m;
+      g.tiles_n = (int32_t)tiles_n;
+      g.alpha = d->alpha;
+      g.ksplit = (int32_t)ks;
+      g.kchunk = kchunk;
+      g.ws = static_cast<float*>(ws);
+      int rc = launch(name, (unsigned)tiles, (unsigned)ks, 256, 0, s, g);
+      if (rc == VH_OK) {
+        GemmReduceArgs r{g.ws, d->c, d->e, M, N, d->c_sm, d->e_sm, d->e_sn, (int32_t)ks,
+                         d->accumulate ? 1 : 0, d->alpha};
+        const int64_t blocks = std::min<int64_t>(cdiv(M * N, 256), 8192);
+        rc = launch("vh_gemm_reduce", (unsigned)blocks, 1, 256, 0, s, r);
+      }
+      g_arena.free(ws);  // stream-ordered reuse
+      return rc;
+    }
+  }
   // Grid y covers both batch dims; runs of the outer one keep it under 65535.
   const int64_t outer_chunk = std::max<int64_t>(1, 65535 / d->batch[1]);
   if (d->batch[1] > 65535) return fail(VH_ERR_UNSUPPORTED, "vh_gemm: inner batch too large");

@@ -92,6 +92,22 @@ struct GemmArgs {
   int32_t accumulate;  // 1: C = C + result
   int32_t causal;      // 0 none; 1 skip tiles above the diagonal; 2 k <= m; 3 k >= m
   float alpha;
+  // Split K (unbatched only): workgroup row y takes k in [y*kchunk, (y+1)*kchunk)
+  // and stores its raw partial to ws[y][M][N]; vh_gemm_reduce finishes.
+  int32_t ksplit;
+  int64_t kchunk;
+  float* ws;
+};
+
+// Fixed-order sum of the split-K partials plus the GEMM epilogue.
+struct GemmReduceArgs {
+  const float* ws;  // [ksplit][M][N]
+  float* C;
+  const float* E;
+  int64_t M, N, ldc, sem, sen;
+  int32_t ksplit;
+  int32_t accumulate;
+  float alpha;
 };
 
 struct AdamArgs {
@@ -197,6 +213,7 @@ struct XentArgs {
   float* out;             // fwd: per-row losses [B]; bwd: dlogits [B, V]
   VhErrRecord* err;
   int64_t B;
+  int64_t ld;             // row stride of logits and dlogits (>= V)
   int32_t V;
 };
 
