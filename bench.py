@@ -341,21 +341,18 @@ def wl_gpt2_block(vh):
 
     def cpu(budget):
         import oracle
-        ocfg = oracle.GptConfig(1, S, D, H, F, V, P)
         t0 = time.perf_counter()
-        _, grads = oracle.gpt_step(ocfg, params, ids[:1], tg[:1])
+        _, grads = oracle.gpt_step(oracle.GptConfig(*cfg), params, ids, tg)
         t_fb = time.perf_counter() - t0
         t0 = time.perf_counter()
         for p, gr in zip(params, grads):
             oracle.adamw_step(p.copy(), gr, np.zeros_like(p), np.zeros_like(p), 1, 0.02, 0.9, 0.95, 1e-8, 0.01)
         t_adam = time.perf_counter() - t0
-        ms = (B * t_fb + t_adam) * 1e3
         threads = int(os.environ.get("VO_THREADS") or os.environ.get("OMP_NUM_THREADS") or os.cpu_count())
-        return ms, threads, (f"oracle SimpleGPT forward+backward for one sequence (B=1, S={S}) took "
-                             f"{t_fb:.1f} s and AdamW over all {sum(p.size for p in params)} parameters "
-                             f"{t_adam:.2f} s; value = 16 x the former + the latter (every op but AdamW "
-                             f"scales with B). Matmuls threaded as the reference's are; attention threaded "
-                             f"over heads (the reference runs it on one thread)")
+        return (t_fb + t_adam) * 1e3, threads, (
+            f"one whole config[4] step of the oracle (forward+backward {t_fb:.1f} s, AdamW over "
+            f"{sum(p.size for p in params)} parameters {t_adam:.2f} s); matmuls threaded as the "
+            f"reference's are, attention threaded over heads (the reference runs it on one thread)")
 
     info = {"workload": "cfg[4] GPT-2-small block training step: B=16, T=1024, C=768, H=12, MLP 3072, "
                         "V=50257, one block; fwd + backward + AdamW",

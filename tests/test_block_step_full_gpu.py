@@ -1,0 +1,68 @@
+"""Config[4] at its real size (B=16, T=1024, C=768, H=12, MLP 3072, V=50257):
+the device step against the CPU oracle's SimpleGPT step on identical inputs --
+the step-0 loss, every parameter gradient, and the loss after one AdamW step
+(north_star: "the full config[4] block step runs end to end with loss matching
+the CPU backend"; loss within 1e-4 relative).
+
+The oracle needs about 6 TFLOP here; it runs threaded (its results do not
+depend on the thread count), a few tens of seconds on the GPU box's cores.
+"""
+import time
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+CFG = (16, 1024, 768, 12, 3072, 50257, 1024)
+ADAM = (0.02, 0.9, 0.95, 1e-8, 0.01)  # verification_harness.rs:203-210
+
+
+def test_block_step_full_size_matches_oracle(vh):
+    from vearo_amd import _block
+    B, S, D, H, F, V, P = CFG
+    r = np.random.default_rng(0x5EED0000 + 4)
+    params = []
+    for name, sh in zip(O.GPT_PARAM_NAMES, O.gpt_param_shapes(O.GptConfig(*CFG))):
+        if name.startswith("ln") and name.endswith("_w"):
+            params.append(np.ones(sh, np.float32))
+        elif name.startswith("ln"):
+            params.append(np.zeros(sh, np.float32))
+        else:
+            params.append(r.standard_normal(sh, dtype=np.float32) * np.float32(0.02))
+    ids = r.integers(0, V, size=(B, S)).astype(np.float32)
+    tg = r.integers(0, V, size=(B, S)).astype(np.float32)
+
+    g = _block.Gpt(_block.GptConfig(*CFG))
+    g.set_params(params)
+    g.set_inputs(ids, tg)
+    g.forward_backward(True)
+    loss0 = g.loss()
+    grads = g.grads()
+    g.adamw(*ADAM)
+    g.forward_backward(False)
+    loss1 = g.loss()
+    g.close()
+    print(f"device: loss0 {loss0:.7f} loss1 {loss1:.7f}", flush=True)
+    assert np.isfinite(loss0) and np.isfinite(loss1)
+
+    t0 = time.perf_counter()
+    oloss0, ograds = O.gpt_step(O.GptConfig(*CFG), params, ids, tg)
+    print(f"oracle forward+backward {time.perf_counter() - t0:.1f} s: loss0 {oloss0:.7f}", flush=True)
+    assert abs(loss0 - oloss0) <= 1e-4 * abs(oloss0), (loss0, oloss0)
+    for i, name in enumerate(O.GPT_PARAM_NAMES):
+        if name == "k_b":  # exact gradient 0 (softmax ignores a per-row shift)
+            assert np.abs(grads[i]).max() < 1e-6 and np.abs(ograds[i]).max() < 1e-6
+            continue
+        scale = np.abs(ograds[i]).max()
+        err = np.abs(grads[i] - ograds[i]).max()
+        print(f"  grad {name:6s} max|cpu| {scale:.3e} max|gpu-cpu| {err:.3e}", flush=True)
+        assert err <= 1e-4 * scale, (name, err, scale)
+    for p, gr in zip(params, ograds):
+        O.adamw_step(p, gr, np.zeros_like(p), np.zeros_like(p), 1, *ADAM)
+    t0 = time.perf_counter()
+    oloss1, _ = O.gpt_step(O.GptConfig(*CFG), params, ids, tg, grads=False)
+    print(f"oracle forward after AdamW {time.perf_counter() - t0:.1f} s: loss1 {oloss1:.7f}", flush=True)
+    assert abs(loss1 - oloss1) <= 1e-4 * abs(oloss1), (loss1, oloss1)
