@@ -288,8 +288,81 @@ int main() {
                  "Weight dimension must match norm_dim");
     expect_panic([&] { Tensor::from_f32({1}, Shape{1}).embedding_backward(W, Tensor::zeros(Shape{1, 2})); },
                  "grad_out shape must be x.shape() + [embedding_dim]");
-    expect_panic([&] { get_backend_ops(Device::hip())->matmul(logits, logits); },
-                 "matmul is not part of this backend");
+    expect_panic([&] { get_backend_ops(Device::hip())->relu(logits); }, "relu is not part of this backend");
+    expect_panic([&] { logits.matmul(logits); }, "Incompatible dimensions for matmul");
+    expect_panic([&] { Tensor::zeros(Shape{3}).matmul(logits); }, "Matmul requires rank >= 2");
+    expect_panic([&] { Tensor::zeros(Shape{2, 2, 3}).matmul(Tensor::zeros(Shape{3, 3, 2})); },
+                 "Batch shapes are not broadcastable");
+  });
+
+  // crates/vearo-backend-cuda/src/lib.rs:1676-1699: matmul with a transposed,
+  // non-contiguous rhs -- exactly what backward feeds it -- equals the CPU.
+  run("test_hip_matmul_transposed", [] {
+    Tensor a = Tensor::from_f32({1, 2, 3, 4, 5, 6}, Shape{2, 3});
+    Tensor b = Tensor::from_f32({7, 8, 9, 10, 11, 12}, Shape{2, 3});
+    const std::vector<float> c = a.matmul(b.transpose(0, 1)).to_vec_f32();
+    const std::vector<float> bt = b.transpose(0, 1).to_vec_f32();
+    std::vector<float> ref(4);
+    char err[256];
+    vo_layout al = contig({2, 3}), bl = contig({3, 2});
+    CHECK(vo_matmul(std::vector<float>{1, 2, 3, 4, 5, 6}.data(), &al, bt.data(), &bl, ref.data(), err, sizeof err) == 0,
+          "oracle matmul");
+    CHECK(c == ref, "transposed rhs matches the CPU exactly");
+    CHECK((c == std::vector<float>{50, 68, 122, 167}), "known values");
+  });
+
+  // Linear::forward at GPT-2 width: x [256, 768] @ W^T with W [512, 768] ~ N(0, 0.02).
+  run("matmul_linear_vs_oracle", [] {
+    const auto xv = randn(256 * 768, 21), wv = randn(512 * 768, 22, 0.02f);
+    Tensor X = Tensor::from_f32(xv, Shape{256, 768}), W = Tensor::from_f32(wv, Shape{512, 768});
+    const std::vector<float> y = X.matmul(W.transpose(0, 1)).to_vec_f32();
+    std::vector<float> wt(768 * 512), ref(256 * 512);
+    for (int o = 0; o < 512; ++o)
+      for (int i = 0; i < 768; ++i) wt[(size_t)i * 512 + o] = wv[(size_t)o * 768 + i];
+    char err[256];
+    vo_layout xl = contig({256, 768}), tl = contig({768, 512});
+    CHECK(vo_matmul(xv.data(), &xl, wt.data(), &tl, ref.data(), err, sizeof err) == 0, "oracle matmul");
+    expect_close(y, ref, "linear");
+  });
+
+  // crates/vearo/tests/fused_attention_parity.rs: the fused op against the
+  // unfused chain of backend ops, same inputs and bounds; and its backward
+  // against the CPU fused backward.
+  run("fused_attention_matches_unfused_reference", [] {
+    const int B = 2, H = 2, S = 4, DK = 8, n = B * H * S * DK;
+    auto fill = [&](float phase) {
+      std::vector<float> v(n);
+      for (int i = 0; i < n; ++i) {
+        const float x = (float)i;
+        v[i] = std::sin(x * 0.37f + phase) * 0.5f + std::cos(x * 0.11f + phase) * 0.25f;
+      }
+      return v;
+    };
+    const auto qv = fill(0.0f), kv = fill(1.3f), vv = fill(2.7f);
+    std::vector<float> mv(S * S, 0.0f), cv(n);
+    for (int r = 0; r < S; ++r)
+      for (int c = 0; c < S; ++c)
+        if (c > r) mv[r * S + c] = -1e9f;
+    for (int i = 0; i < n; ++i) cv[i] = std::sin((float)i * 0.19f) + 1.5f;
+    const Shape sh{B, H, S, DK};
+    Tensor q = Tensor::from_f32(qv, sh), k = Tensor::from_f32(kv, sh), v = Tensor::from_f32(vv, sh);
+    Tensor mask = Tensor::from_f32(mv, Shape{S, S});
+    Tensor scale = Tensor::from_f32({1.0f / std::sqrt((float)DK)}, Shape{1});
+    const auto out_ref = q.matmul(k.transpose(2, 3)).mul(scale).add(mask).softmax(3).matmul(v).to_vec_f32();
+    const auto out = q.fused_attention(k, v, &mask).to_vec_f32();
+    double maxabs = 0;
+    for (float x : out_ref) maxabs = std::max(maxabs, (double)std::fabs(x));
+    CHECK(maxabs > 1e-4, "reference output is not degenerate");
+    CHECK(maxdiff(out_ref, out) < 1e-5, "fused output within 1e-5 of the unfused chain");
+    Tensor go = Tensor::from_f32(cv, sh);
+    auto [dq, dk, dv] = q.fused_attention_backward(k, v, &mask, go);
+    std::vector<float> rq(n), rk(n), rv(n);
+    vo_layout ml = contig({S, S});
+    vo_fused_attention_backward(qv.data(), kv.data(), vv.data(), B, H, S, DK, mv.data(), &ml, cv.data(), rq.data(),
+                                rk.data(), rv.data());
+    CHECK(maxdiff(dq.to_vec_f32(), rq) < 1e-4, "dq");
+    CHECK(maxdiff(dk.to_vec_f32(), rk) < 1e-4, "dk");
+    CHECK(maxdiff(dv.to_vec_f32(), rv) < 1e-4, "dv");
   });
 
   run("empty_tensors", [] {

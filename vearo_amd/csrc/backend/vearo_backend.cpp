@@ -212,6 +212,18 @@ Tensor Tensor::cross_entropy(const Tensor& t) const { return ops_for(device_).cr
 Tensor Tensor::cross_entropy_backward(const Tensor& t, const Tensor& g) const {
   return ops_for(device_).cross_entropy_backward(*this, t, g);
 }
+Tensor Tensor::matmul(const Tensor& o) const {
+  panic_if(!(o.device() == device_), "Tensors must reside on the same device");
+  return ops_for(device_).matmul(*this, o);
+}
+Tensor Tensor::fused_attention(const Tensor& k, const Tensor& v, const Tensor* mask) const {
+  return ops_for(device_).fused_attention(*this, k, v, mask);
+}
+std::tuple<Tensor, Tensor, Tensor> Tensor::fused_attention_backward(const Tensor& k, const Tensor& v,
+                                                                    const Tensor* mask,
+                                                                    const Tensor& g) const {
+  return ops_for(device_).fused_attention_backward(*this, k, v, mask, g);
+}
 
 // ------------------------------------------------------------- registry --
 
@@ -387,7 +399,30 @@ Tensor cross_entropy_backward(const Tensor& logits, const Tensor& targets, const
   throw Panic(std::string("vearo-backend-hip: ") + op +
               " is not part of this backend (fused layer kernels only)");
 }
-Tensor matmul(const Tensor&, const Tensor&) { out_of_scope("matmul"); }
+// cpu:266-417: batched matmul with broadcast batch dims; a fresh contiguous
+// output (zeros when it is empty).
+Tensor matmul(const Tensor& l, const Tensor& r) {
+  const int lr = l.shape().rank, rr = r.shape().rank;
+  panic_if(lr < 2 || rr < 2, "Matmul requires rank >= 2");
+  const int64_t M = l.shape()[lr - 2], K = l.shape()[lr - 1], K2 = r.shape()[rr - 2], N = r.shape()[rr - 1];
+  panic_if(K != K2, "Incompatible dimensions for matmul");
+  const int lb = lr - 2, rb = rr - 2, ob = std::max(lb, rb);
+  std::vector<int64_t> od(ob);
+  for (int i = 0; i < ob; ++i) {
+    const int li = i - (ob - lb), ri = i - (ob - rb);
+    const int64_t a = li >= 0 ? l.shape()[li] : 1, b = ri >= 0 ? r.shape()[ri] : 1;
+    panic_if(!(a == b || a == 1 || b == 1), "Batch shapes are not broadcastable");
+    od[i] = std::max(a, b);
+  }
+  od.push_back(M);
+  od.push_back(N);
+  Tensor out = Tensor::zeros(Shape(od), l.device());
+  if (out.shape().numel() == 0) return out;
+  const vh_layout ll = layout_of(l), rl = layout_of(r);
+  check(vh_matmul(l.data(), &ll, r.data(), &rl, out.data(), nullptr));
+  return out;
+}
+
 Tensor relu(const Tensor&) { out_of_scope("relu"); }
 Tensor conv2d(const Tensor&, const Tensor&, const Tensor&, size_t, size_t) { out_of_scope("conv2d"); }
 std::tuple<Tensor, Tensor, Tensor> conv2d_backward(const Tensor&, const Tensor&, const Tensor&, size_t,
@@ -411,12 +446,53 @@ std::tuple<Tensor, Tensor, Tensor> batchnorm_backward(const Tensor&, const Tenso
                                                       float) {
   out_of_scope("batchnorm_backward");
 }
-Tensor fused_attention(const Tensor&, const Tensor&, const Tensor&, const Tensor*) {
-  out_of_scope("fused_attention");
+// Operands of the attention kernels need a unit stride on the last dim.
+static Tensor unit_last(const Tensor& t) {
+  const int r = t.shape().rank;
+  return (r > 0 && t.strides()[r - 1] != 1 && t.shape()[r - 1] != 1) ? t.contiguous() : t;
 }
-std::tuple<Tensor, Tensor, Tensor> fused_attention_backward(const Tensor&, const Tensor&, const Tensor&,
-                                                            const Tensor*, const Tensor&) {
-  out_of_scope("fused_attention_backward");
+
+static void attention_checks(const Tensor& q, const Tensor& k, const Tensor& v) {
+  // cpu:2376-2383: [B, H, S, Dk] and k, v of q's shape.
+  panic_if(q.shape().rank != 4, "fused attention expects [B, H, S, Dk]");
+  panic_if(k.shape() != q.shape(), "assertion `left == right` failed: k shape " + k.shape().str() +
+                                       " != q shape " + q.shape().str());
+  panic_if(v.shape() != q.shape(), "assertion `left == right` failed: v shape " + v.shape().str() +
+                                       " != q shape " + q.shape().str());
+}
+
+// cpu:2366-2464: softmax(q k^T / sqrt(Dk) + mask) v, mask broadcast from the right.
+Tensor fused_attention(const Tensor& q0, const Tensor& k0, const Tensor& v0, const Tensor* mask) {
+  attention_checks(q0, k0, v0);
+  const Tensor q = unit_last(q0), k = unit_last(k0), v = unit_last(v0);
+  Tensor out = Tensor::zeros(q.shape(), q.device());
+  if (q.shape().numel() == 0) return out;
+  const vh_layout ql = layout_of(q), kl = layout_of(k), vl = layout_of(v), ol = layout_of(out);
+  vh_layout ml{};
+  if (mask) ml = layout_of(*mask);
+  check(vh_fused_attention_fwd(q.data(), &ql, k.data(), &kl, v.data(), &vl, mask ? mask->data() : nullptr,
+                               mask ? &ml : nullptr, 0, out.data(), &ol, nullptr, 0, nullptr));
+  return out;
+}
+
+// cpu:2467-2630: (dq, dk, dv), recomputing the probabilities from q and k.
+std::tuple<Tensor, Tensor, Tensor> fused_attention_backward(const Tensor& q0, const Tensor& k0,
+                                                            const Tensor& v0, const Tensor* mask,
+                                                            const Tensor& g0) {
+  attention_checks(q0, k0, v0);
+  panic_if(g0.shape() != q0.shape(), "grad_out must have the attention output's shape");
+  const Tensor q = unit_last(q0), k = unit_last(k0), v = unit_last(v0), g = unit_last(g0);
+  Tensor dq = Tensor::zeros(q.shape(), q.device()), dk = Tensor::zeros(q.shape(), q.device()),
+         dv = Tensor::zeros(q.shape(), q.device());
+  if (q.shape().numel() == 0) return {dq, dk, dv};
+  const vh_layout ql = layout_of(q), kl = layout_of(k), vl = layout_of(v), gl = layout_of(g),
+                  dl = layout_of(dq);
+  vh_layout ml{};
+  if (mask) ml = layout_of(*mask);
+  check(vh_fused_attention_bwd(q.data(), &ql, k.data(), &kl, v.data(), &vl, mask ? mask->data() : nullptr,
+                               mask ? &ml : nullptr, 0, g.data(), &gl, dq.data(), &dl, dk.data(), &dl,
+                               dv.data(), &dl, nullptr, 0, nullptr));
+  return {dq, dk, dv};
 }
 
 }  // namespace ops

@@ -104,6 +104,11 @@ class Tensor {
   Tensor embedding_backward(const Tensor& weight, const Tensor& grad_out) const;
   Tensor cross_entropy(const Tensor& targets) const;
   Tensor cross_entropy_backward(const Tensor& targets, const Tensor& grad_out) const;
+  Tensor matmul(const Tensor& o) const;
+  Tensor fused_attention(const Tensor& k, const Tensor& v, const Tensor* mask) const;
+  std::tuple<Tensor, Tensor, Tensor> fused_attention_backward(const Tensor& k, const Tensor& v,
+                                                              const Tensor* mask,
+                                                              const Tensor& grad_out) const;
 
  private:
   std::shared_ptr<Storage> storage_;
