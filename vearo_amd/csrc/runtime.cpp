@@ -986,14 +986,28 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
   const std::string name = std::string("vh_gemm_") + (akc ? "k" : "m") + (avec ? "4" : "1") + "_" +
                            (bkc ? "k" : "n") + (bvec ? "4" : "1");
   hipStream_t s = S(stream);
-  // Split K when one unbatched product has too few C tiles to fill the chip
-  // (the weight gradients: 768 x 768 outputs over K = 16384 rows): each split
-  // writes its raw partial, a fixed-order reduce sums them and applies the
-  // epilogue.
+  // Split K for an unbatched product over a long K when its C tiles would
+  // leave the chip idle: too few tiles to fill it (the weight gradients, 768 x
+  // 768 outputs over K = 16384 rows), or a last wave of workgroups mostly empty
+  // (768 tiles on 512 resident workgroups). Each split writes its raw partial;
+  // a fixed-order reduce sums them and applies the epilogue.
   const int64_t tiles = tiles_m * tiles_n;
-  const int64_t slots = 2 * std::max(g_rt.cu_count, 1);
-  if (d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE && tiles < slots && K >= 4096) {
-    int64_t ks = std::min<int64_t>({16, cdiv(slots, tiles), K / 1024});
+  const int64_t slots = 2 * std::max(g_rt.cu_count, 1);  // 2 resident workgroups per CU (LDS)
+  int64_t ks = 1;
+  if (d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE && K >= 4096) {
+    if (tiles < slots) {
+      ks = std::min<int64_t>({16, cdiv(slots, tiles), K / 1024});
+    } else {
+      for (int64_t c = 1; c <= 4 && K / c >= 1024; ++c) {
+        const int64_t n = tiles * c;
+        if ((double)n / (double)(cdiv(n, slots) * slots) >= 0.95) {
+          ks = c;
+          break;
+        }
+      }
+    }
+  }
+  if (ks > 1) {
     const int64_t kchunk = cdiv(cdiv(K, ks), 32) * 32;
     ks = cdiv(K, kchunk);
     if (ks > 1) {
