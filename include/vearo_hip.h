@@ -198,6 +198,14 @@ int vh_cross_entropy_fwd_ld(const float* logits, int64_t ld, const float* target
 int vh_cross_entropy_bwd_ld(const float* logits, int64_t ld, const float* targets,
                             const float* grad_out, float* dlogits, int64_t B, int64_t V,
                             void* stream);
+/* Forward and backward in one read of the logits, for a caller that knows
+ * grad_out before running the forward (the training step: the seed gradient of
+ * loss.backward() is 1, autograd:795-798). Same loss and dlogits as
+ * vh_cross_entropy_fwd_ld followed by vh_cross_entropy_bwd_ld.
+ * scratch: NULL or vh_cross_entropy_fwd_scratch_bytes(B) bytes. */
+int vh_cross_entropy_fwd_bwd_ld(const float* logits, int64_t ld, const float* targets,
+                                const float* grad_out, float* loss, float* dlogits, int64_t B,
+                                int64_t V, void* scratch, size_t scratch_bytes, void* stream);
 
 /* ------------------------------------- composites the autograd arms drive -- */
 
@@ -293,6 +301,18 @@ int vh_fused_attention_bwd(const float* q, const vh_layout* ql, const float* k,
                            const vh_layout* dvl, void* scratch, size_t scratch_bytes,
                            void* stream);
 size_t vh_fused_attention_scratch_bytes(int64_t B, int64_t H, int64_t S, int backward);
+/* The backward from the probabilities the forward computed: a caller-supplied
+ * forward scratch holds P [B, H, S, S] on return, and passing it here as P skips
+ * recomputing it (same results as vh_fused_attention_bwd; P already carries the
+ * mask). No counterpart in the reference, whose backward always recomputes;
+ * for a training step that keeps the forward's scratch alive.
+ * scratch: NULL or vh_fused_attention_scratch_bytes(B, H, S, 0) bytes. */
+int vh_fused_attention_bwd_probs(const float* P, const float* q, const vh_layout* ql,
+                                 const float* k, const vh_layout* kl, const float* v,
+                                 const vh_layout* vl, int causal, const float* dout,
+                                 const vh_layout* dol, float* dq, const vh_layout* dql, float* dk,
+                                 const vh_layout* dkl, float* dv, const vh_layout* dvl,
+                                 void* scratch, size_t scratch_bytes, void* stream);
 
 /* AdamW update of one parameter tensor in place, moments m and v in device
  * memory, step count t >= 1. Replaces Tensor::adamw_step (tensor.rs:931-1023,

@@ -215,6 +215,32 @@ def attention_gpu(vh, q, k, v, mask, causal, go=None, layout="bhsd"):
     return res
 
 
+def test_attention_backward_from_saved_probs(vh):
+    """vh_fused_attention_bwd_probs on the probabilities left in the forward's
+    scratch gives the same bits as the recomputing backward."""
+    B, H, S, Dk = 2, 3, 200, 32
+    r = np.random.default_rng(13)
+    q, k, v, go = (r.standard_normal((B, H, S, Dk), dtype=np.float32) for _ in range(4))
+    Q, K, V, G = (dev(vh, a) for a in (q, k, v, go))
+    l = vh.layout((B, H, S, Dk))
+    nsc = vh.lib.vh_fused_attention_scratch_bytes(B, H, S, 0)
+    SC, WS = vh.DeviceBuffer(nsc), vh.DeviceBuffer(nsc)
+    O_ = out(vh, q.shape)
+    vh.check(vh.lib.vh_fused_attention_fwd(Q.ptr, ctypes.byref(l), K.ptr, ctypes.byref(l), V.ptr, ctypes.byref(l),
+                                           None, None, 1, O_.ptr, ctypes.byref(l), SC.ptr, nsc, None))
+    r1 = [out(vh, q.shape) for _ in range(3)]
+    r2 = [out(vh, q.shape) for _ in range(3)]
+    vh.check(vh.lib.vh_fused_attention_bwd(Q.ptr, ctypes.byref(l), K.ptr, ctypes.byref(l), V.ptr, ctypes.byref(l),
+                                           None, None, 1, G.ptr, ctypes.byref(l), r1[0].ptr, ctypes.byref(l),
+                                           r1[1].ptr, ctypes.byref(l), r1[2].ptr, ctypes.byref(l), None, 0, None))
+    vh.check(vh.lib.vh_fused_attention_bwd_probs(SC.ptr, Q.ptr, ctypes.byref(l), K.ptr, ctypes.byref(l), V.ptr,
+                                                 ctypes.byref(l), 1, G.ptr, ctypes.byref(l), r2[0].ptr,
+                                                 ctypes.byref(l), r2[1].ptr, ctypes.byref(l), r2[2].ptr,
+                                                 ctypes.byref(l), WS.ptr, nsc, None))
+    for a, b in zip(r1, r2):
+        np.testing.assert_array_equal(fetch(vh, a, q.shape), fetch(vh, b, q.shape))
+
+
 @pytest.mark.parametrize("tag", ["attkat", "attc", "attm", "attn"])
 def test_attention_golden(vh, tag):
     print("attention", tag, flush=True)
@@ -322,3 +348,8 @@ def test_cross_entropy_row_stride(vh):
     dl = fetch(vh, DL, (B, ld))
     assert_parity(dl[:, :V], O.cross_entropy_backward(logits, tg, np.float32([1.3])), name="dlogits")
     assert np.all(dl[:, V:] == -5.0)  # only the first V columns are written
+    # Forward and backward in one pass: the same bits as the two passes.
+    LOSS2, DL2 = out(vh, (1,)), dev(vh, np.full((B, ld), -5.0, np.float32))
+    vh.check(vh.lib.vh_cross_entropy_fwd_bwd_ld(L.ptr, ld, T.ptr, GO.ptr, LOSS2.ptr, DL2.ptr, B, V, None, 0, None))
+    np.testing.assert_array_equal(fetch(vh, LOSS2, (1,)), fetch(vh, LOSS, (1,)))
+    np.testing.assert_array_equal(fetch(vh, DL2, (B, ld)), dl)

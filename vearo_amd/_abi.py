@@ -125,6 +125,10 @@ SIGNATURES = {
         [fp, c_int64, fp, fp, c_int64, c_int64, c_void_p, c_size_t, c_void_p],
     ),
     "vh_cross_entropy_bwd_ld": (c_int, [fp, c_int64, fp, fp, fp, c_int64, c_int64, c_void_p]),
+    "vh_cross_entropy_fwd_bwd_ld": (
+        c_int,
+        [fp, c_int64, fp, fp, fp, fp, c_int64, c_int64, c_void_p, c_size_t, c_void_p],
+    ),
     "vh_binary": (c_int, [c_int, fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, c_void_p]),
     "vh_reduce": (c_int, [c_int, fp, POINTER(VhLayout), c_int, fp, c_void_p]),
     "vh_strided_copy": (c_int, [fp, POINTER(VhLayout), fp, c_void_p]),
@@ -144,6 +148,12 @@ SIGNATURES = {
          POINTER(VhLayout), c_void_p, c_size_t, c_void_p],
     ),
     "vh_fused_attention_scratch_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int]),
+    "vh_fused_attention_bwd_probs": (
+        c_int,
+        [fp, fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, POINTER(VhLayout), c_int, fp,
+         POINTER(VhLayout), fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, POINTER(VhLayout),
+         c_void_p, c_size_t, c_void_p],
+    ),
     "vh_adamw_step": (
         c_int,
         [fp, fp, fp, fp, c_int64, c_int32, c_float, c_float, c_float, c_float, c_float, c_void_p],

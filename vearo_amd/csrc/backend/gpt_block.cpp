@@ -69,6 +69,8 @@ struct vb_gpt {
   float *loss, *one;
   // backward buffers
   float *dlogits, *dlnf, *dh, *dg, *df1, *lnx, *dh1, *datt, *dq, *dk, *dv, *dln1, *dh0;
+  float *attP = nullptr, *attG = nullptr;  // attention probabilities (kept for the backward), workspace
+  size_t att_bytes = 0;
   std::vector<void*> allocs;
 
   float* p(int i) { return P + off[i]; }
@@ -167,7 +169,10 @@ struct vb_gpt {
     return l;
   }
 
-  int forward() {
+  // with_grad: the cross-entropy arm of the backward (autograd:594-599, seed
+  // gradient 1, autograd:795-798) runs together with the forward loss, in one
+  // read of the logits.
+  int forward(bool with_grad) {
     const int64_t D = c.D, F = c.F, V = c.V;
     const vh_layout lrd = contiguous({R, D});
     VB(vh_embedding_fwd(ids, p(0), tok, R, V, D, nullptr));
@@ -178,7 +183,7 @@ struct vb_gpt {
     VB(linear(ln1, D, p(6), D, p(7), k, 0));
     VB(linear(ln1, D, p(8), D, p(9), v, 0));
     const vh_layout hl = heads();
-    VB(vh_fused_attention_fwd(q, &hl, k, &hl, v, &hl, nullptr, nullptr, 1, att, &hl, nullptr, 0, nullptr));
+    VB(vh_fused_attention_fwd(q, &hl, k, &hl, v, &hl, nullptr, nullptr, 1, att, &hl, attP, att_bytes, nullptr));
     VB(vh_d2d(h1, h0, (size_t)(R * D) * sizeof(float), nullptr));
     VB(linear(att, D, p(10), D, p(11), h1, 1));  // h1 = h0 + (att W_o^T + b_o)
     VB(vh_layernorm_fwd(h1, p(12), p(13), ln2, R, D, kEps, nullptr));
@@ -188,16 +193,17 @@ struct vb_gpt {
     VB(linear(g, F, p(16), D, p(17), h2, 1));  // h2 = h1 + (g W_fc2^T + b_fc2)
     VB(vh_layernorm_fwd(h2, p(18), p(19), lnf, R, D, kEps, nullptr));
     VB(linear(lnf, D, p(20), V, nullptr, logits, 0, Vp));
-    VB(vh_cross_entropy_fwd_ld(logits, Vp, tg, loss, R, V, nullptr, 0, nullptr));
+    if (with_grad)
+      VB(vh_cross_entropy_fwd_bwd_ld(logits, Vp, tg, one, loss, dlogits, R, V, nullptr, 0, nullptr));
+    else
+      VB(vh_cross_entropy_fwd_ld(logits, Vp, tg, loss, R, V, nullptr, 0, nullptr));
     return VH_OK;
   }
 
   int backward() {
     const int64_t D = c.D, F = c.F, V = c.V;
     const vh_layout lrd = contiguous({R, D});
-    // cross_entropy arm (autograd:594-599), grad_out = 1 (backward_callback, :795-798).
-    VB(vh_cross_entropy_bwd_ld(logits, Vp, tg, one, dlogits, R, V, nullptr));
-    // lm_head (rank-2 input, no bias), over the padded vocabulary: the zero
+    // dlogits came with the forward (forward(true)). lm_head (rank-2 input, no bias), over the padded vocabulary: the zero
     // columns of dlogits meet the zero rows after the weight.
     VB(linear_dx(dlogits, Vp, p(20), D, dlnf, 0));
     VB(linear_dw(dlogits, Vp, lnf, D, gr(20)));
@@ -217,8 +223,9 @@ struct vb_gpt {
     VB(linear_dx(dh1, D, p(10), D, datt, 0));
     VB(linear_dw(dh1, D, att, D, gr(10)));
     const vh_layout hl = heads();
-    VB(vh_fused_attention_bwd(q, &hl, k, &hl, v, &hl, nullptr, nullptr, 1, datt, &hl, dq, &hl, dk, &hl, dv,
-                              &hl, nullptr, 0, nullptr));
+    // The Fused attention arm (autograd:600-612) from the forward's probabilities.
+    VB(vh_fused_attention_bwd_probs(attP, q, &hl, k, &hl, v, &hl, 1, datt, &hl, dq, &hl, dk, &hl, dv, &hl, attG,
+                                    att_bytes, nullptr));
     // v, k, q projections in reverse tape order; ln1's gradient accumulates.
     VB(vh_sum_rows(dv, R, D, gr(9), nullptr, 0, nullptr));
     VB(linear_dx(dv, D, p(8), D, dln1, 0));
@@ -283,6 +290,9 @@ int vb_gpt_create(const vb_gpt_config* cfg, vb_gpt** out) {
   for (float** p : {&g->y1, &g->g, &g->dg, &g->df1}) A(p, R * F);
   A(&g->logits, R * Vp, 1);
   A(&g->dlogits, R * Vp, 1);
+  g->att_bytes = vh_fused_attention_scratch_bytes(c.B, c.H, c.S, 0);
+  A(&g->attP, (int64_t)(g->att_bytes / sizeof(float)));
+  A(&g->attG, (int64_t)(g->att_bytes / sizeof(float)));
   A(&g->loss, 1, 1);
   A(&g->one, 1);
   if (rc == VH_OK) {
@@ -332,7 +342,7 @@ float* vb_gpt_loss_ptr(vb_gpt* g) { return g ? g->loss : nullptr; }
 
 int vb_gpt_forward_backward(vb_gpt* g, int backward) {
   if (!g) return vb_fail(VH_ERR_INVALID, "vb_gpt_forward_backward: null handle");
-  int rc = g->forward();
+  int rc = g->forward(backward != 0);
   if (rc == VH_OK && backward) rc = g->backward();
   return rc;
 }

@@ -122,10 +122,13 @@ extern "C" __global__ void __launch_bounds__(256) vh_emb_rows_v4(EmbSegArgs a) {
 #define XE_CFG(M) M(1) M(2) M(4) M(8) M(16) M(24) M(32) M(40) M(48) M(50) M(56) M(64)
 #define K_XE(N)                                                                   \
   extern "C" __global__ void __launch_bounds__(1024) vh_xent_fwd_n##N(XentArgs a) { \
-    xent_cached_impl<N, false>(a);                                                \
+    xent_cached_impl<N, 0>(a);                                                \
   }                                                                               \
   extern "C" __global__ void __launch_bounds__(1024) vh_xent_bwd_n##N(XentArgs a) { \
-    xent_cached_impl<N, true>(a);                                                 \
+    xent_cached_impl<N, 1>(a);                                                    \
+  }                                                                               \
+  extern "C" __global__ void __launch_bounds__(1024) vh_xent_fb_n##N(XentArgs a) { \
+    xent_cached_impl<N, 2>(a);                                                 \
   }
 XE_CFG(K_XE)
 extern "C" __global__ void __launch_bounds__(1024) vh_xent_fwd_stream(XentArgs a) { xent_stream_impl<false>(a); }

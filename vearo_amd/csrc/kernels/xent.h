@@ -11,7 +11,10 @@
 // read from HBM once (fwd 4 B/elem read; bwd 4 B read + 4 B write). Longer rows
 // take the streaming variant: one online max/sum pass, plus a write pass in bwd.
 // The scalar per-row log_softmax values are reduced by xent_reduce in a fixed
-// order, so the loss is deterministic.
+// order, so the loss is deterministic. MODE 2 does forward and backward in one
+// read of the row (for a caller that knows grad_out before the forward, as the
+// training step does: the seed gradient of backward() is 1): the same row
+// loss and the same dlogits as MODE 0 and MODE 1.
 #pragma once
 #include "common.h"
 
@@ -30,7 +33,7 @@ VH_DEV int32_t xent_target(const XentArgs& a, int64_t row) {
 // out-of-range stores are dropped.
 #define VH_BUF_WORD3 0x00020000
 
-template <int NV, bool BWD>
+template <int NV, int MODE>  // 0 forward, 1 backward, 2 both
 VH_DEV void xent_cached_impl(const XentArgs& a) {
   __shared__ float red[16];
   const int64_t row = blockIdx.x;
@@ -63,9 +66,10 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
   }
   s = team_sum<1024>(s, red);
   const int32_t t = xent_target(a, row);
-  if constexpr (!BWD) {
-    if (threadIdx.x == 0) a.out[row] = t >= 0 ? lr[t] - m - logf(s) : 0.0f;
-  } else {
+  if constexpr (MODE != 1) {
+    if (threadIdx.x == 0) (MODE == 0 ? a.out : a.row_loss)[row] = t >= 0 ? lr[t] - m - logf(s) : 0.0f;
+  }
+  if constexpr (MODE != 0) {
     const float go = *a.grad_out;
     const float Bf = (float)a.B;
     const __amdgpu_buffer_rsrc_t rout =

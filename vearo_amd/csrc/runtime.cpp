@@ -802,7 +802,7 @@ int vh_cross_entropy_fwd_ld(const float* logits, int64_t ld, const float* target
   hipStream_t s = S(stream);
   Scratch sc;
   VH_TRY(sc.get(scratch, scratch_bytes, vh_cross_entropy_fwd_scratch_bytes(B)));
-  XentArgs a{logits, targets, nullptr, static_cast<float*>(sc.p), g_rt.err, B, ld, (int32_t)V};
+  XentArgs a{logits, targets, nullptr, static_cast<float*>(sc.p), nullptr, g_rt.err, B, ld, (int32_t)V};
   VH_TRY(launch(xent_kernel("fwd", V), (unsigned)B, 1, 1024, 0, s, a));
   XentReduceArgs r{static_cast<float*>(sc.p), loss, B};
   return launch("vh_xent_reduce", 1, 1, 1024, 0, s, r);
@@ -822,8 +822,34 @@ int vh_cross_entropy_bwd_ld(const float* logits, int64_t ld, const float* target
   if (!logits || !targets || !grad_out || !dlogits)
     return fail(VH_ERR_INVALID, "vh_cross_entropy_bwd: null pointer");
   if (V > INT32_MAX || B > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_cross_entropy_bwd: size exceeds int32");
-  XentArgs a{logits, targets, grad_out, dlogits, g_rt.err, B, ld, (int32_t)V};
+  XentArgs a{logits, targets, grad_out, dlogits, nullptr, g_rt.err, B, ld, (int32_t)V};
   return launch(xent_kernel("bwd", V), (unsigned)B, 1, 1024, 0, S(stream), a);
+}
+
+int vh_cross_entropy_fwd_bwd_ld(const float* logits, int64_t ld, const float* targets, const float* grad_out,
+                                float* loss, float* dlogits, int64_t B, int64_t V, void* scratch,
+                                size_t scratch_bytes, void* stream) {
+  VH_TRY(require_init());
+  if (B <= 0) return fail(VH_ERR_INVALID, "Batch size must be greater than 0");
+  if (V <= 0) return fail(VH_ERR_INVALID, "vh_cross_entropy_fwd_bwd: vocabulary must be > 0");
+  if (ld < V) return fail(VH_ERR_INVALID, "vh_cross_entropy_fwd_bwd: row stride below V");
+  if (!logits || !targets || !grad_out || !loss || !dlogits)
+    return fail(VH_ERR_INVALID, "vh_cross_entropy_fwd_bwd: null pointer");
+  if (V > INT32_MAX || B > INT32_MAX)
+    return fail(VH_ERR_UNSUPPORTED, "vh_cross_entropy_fwd_bwd: size exceeds int32");
+  const std::string fk = xent_kernel("fwd", V);
+  if (fk.find("_stream") != std::string::npos) {  // rows too long to cache: two passes
+    VH_TRY(vh_cross_entropy_fwd_ld(logits, ld, targets, loss, B, V, scratch, scratch_bytes, stream));
+    return vh_cross_entropy_bwd_ld(logits, ld, targets, grad_out, dlogits, B, V, stream);
+  }
+  hipStream_t s = S(stream);
+  Scratch sc;
+  VH_TRY(sc.get(scratch, scratch_bytes, vh_cross_entropy_fwd_scratch_bytes(B)));
+  float* rows = static_cast<float*>(sc.p);
+  XentArgs a{logits, targets, grad_out, dlogits, rows, g_rt.err, B, ld, (int32_t)V};
+  VH_TRY(launch(xent_kernel("fb", V), (unsigned)B, 1, 1024, 0, s, a));
+  XentReduceArgs r{rows, loss, B};
+  return launch("vh_xent_reduce", 1, 1, 1024, 0, s, r);
 }
 
 int vh_cross_entropy_bwd(const float* logits, const float* targets, const float* grad_out,
@@ -1257,6 +1283,93 @@ int attn_probs(const float* q, const vh_layout* ql, const float* k, const vh_lay
 }
 }  // namespace
 
+namespace {
+// The backward from the probabilities P [B, H, S, S] (contiguous): G is a
+// score-sized workspace.
+int attn_bwd_from_probs(const float* P, float* G, const float* q, const vh_layout* ql, const float* k,
+                        const vh_layout* kl, const float* v, const vh_layout* vl, int causal, const float* dout,
+                        const vh_layout* dol, float* dq, const vh_layout* dql, float* dk, const vh_layout* dkl,
+                        float* dv, const vh_layout* dvl, const AttnShape& sh, hipStream_t s) {
+  const float scale = 1.0f / std::sqrt((float)sh.Dk);
+  const int64_t pb0 = sh.H * sh.S * sh.S, pb1 = sh.S * sh.S;
+  // 2. dP = dO v^T into G.
+  vh_gemm_desc d{};
+  d.M = sh.S;
+  d.N = sh.S;
+  d.K = sh.Dk;
+  d.a = dout;
+  d.a_sm = dol->strides[2];
+  d.a_sk = 1;
+  d.b = v;  // B[k=d][n=j] = v[j][d]
+  d.b_sk = 1;
+  d.b_sn = vl->strides[2];
+  d.c = G;
+  d.c_sm = sh.S;
+  d.batch[0] = sh.B;
+  d.batch[1] = sh.H;
+  d.a_sb[0] = dol->strides[0];
+  d.a_sb[1] = dol->strides[1];
+  d.b_sb[0] = vl->strides[0];
+  d.b_sb[1] = vl->strides[1];
+  d.c_sb[0] = pb0;
+  d.c_sb[1] = pb1;
+  d.alpha = 1.0f;
+  d.causal = causal ? VH_GEMM_SKIP_UPPER : VH_GEMM_DENSE;
+  VH_TRY(vh_gemm(&d, s));
+  // 3. dS = P * (dP - sum(dP * P)) in place over G.
+  VH_TRY(softmax_common("vh_sm_bwd", 8, kSmBwdRpw, P, G, G, sh.B * sh.H * sh.S, sh.S, causal, 0, s, 1));
+  // 4. dq = (dS k) * scale.
+  vh_gemm_desc e{};
+  e.M = sh.S;
+  e.N = sh.Dk;
+  e.K = sh.S;
+  e.a = G;
+  e.a_sm = sh.S;
+  e.a_sk = 1;
+  e.b = k;  // B[k=j][n=d] = k[j][d]
+  e.b_sk = kl->strides[2];
+  e.b_sn = 1;
+  e.c = dq;
+  e.c_sm = dql->strides[2];
+  e.batch[0] = sh.B;
+  e.batch[1] = sh.H;
+  e.a_sb[0] = pb0;
+  e.a_sb[1] = pb1;
+  e.b_sb[0] = kl->strides[0];
+  e.b_sb[1] = kl->strides[1];
+  e.c_sb[0] = dql->strides[0];
+  e.c_sb[1] = dql->strides[1];
+  e.alpha = scale;
+  e.causal = causal ? VH_GEMM_K_LE_M : VH_GEMM_DENSE;
+  VH_TRY(vh_gemm(&e, s));
+  // 5. dk = (dS^T q) * scale: A[m=j][k=i] = dS[i][j].
+  e.a_sm = 1;
+  e.a_sk = sh.S;
+  e.b = q;
+  e.b_sk = ql->strides[2];
+  e.b_sb[0] = ql->strides[0];
+  e.b_sb[1] = ql->strides[1];
+  e.c = dk;
+  e.c_sm = dkl->strides[2];
+  e.c_sb[0] = dkl->strides[0];
+  e.c_sb[1] = dkl->strides[1];
+  e.causal = causal ? VH_GEMM_K_GE_M : VH_GEMM_DENSE;
+  VH_TRY(vh_gemm(&e, s));
+  // 6. dv = P^T dO.
+  e.a = P;
+  e.b = dout;
+  e.b_sk = dol->strides[2];
+  e.b_sb[0] = dol->strides[0];
+  e.b_sb[1] = dol->strides[1];
+  e.c = dv;
+  e.c_sm = dvl->strides[2];
+  e.c_sb[0] = dvl->strides[0];
+  e.c_sb[1] = dvl->strides[1];
+  e.alpha = 1.0f;
+  return vh_gemm(&e, s);
+}
+}  // namespace
+
 size_t vh_fused_attention_scratch_bytes(int64_t B, int64_t H, int64_t S, int backward) {
   if (B <= 0 || H <= 0 || S <= 0) return 0;
   const size_t one = align256((size_t)B * (size_t)H * (size_t)S * (size_t)S * sizeof(float));
@@ -1333,85 +1446,34 @@ int vh_fused_attention_bwd(const float* q, const vh_layout* ql, const float* k, 
   VH_TRY(sc.get(scratch, scratch_bytes, vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 1)));
   float* P = static_cast<float*>(sc.p);
   float* G = P + vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 0) / sizeof(float);
-  const float scale = 1.0f / std::sqrt((float)sh.Dk);
-  const int64_t pb0 = sh.H * sh.S * sh.S, pb1 = sh.S * sh.S;
-  // 1. P, recomputed from q and k as the reference does (cpu:2520-2569).
+  // P, recomputed from q and k as the reference does (cpu:2520-2569).
   VH_TRY(attn_probs(q, ql, k, kl, mask, mst, causal, sh, P, s));
-  // 2. dP = dO v^T into G.
-  vh_gemm_desc d{};
-  d.M = sh.S;
-  d.N = sh.S;
-  d.K = sh.Dk;
-  d.a = dout;
-  d.a_sm = dol->strides[2];
-  d.a_sk = 1;
-  d.b = v;  // B[k=d][n=j] = v[j][d]
-  d.b_sk = 1;
-  d.b_sn = vl->strides[2];
-  d.c = G;
-  d.c_sm = sh.S;
-  d.batch[0] = sh.B;
-  d.batch[1] = sh.H;
-  d.a_sb[0] = dol->strides[0];
-  d.a_sb[1] = dol->strides[1];
-  d.b_sb[0] = vl->strides[0];
-  d.b_sb[1] = vl->strides[1];
-  d.c_sb[0] = pb0;
-  d.c_sb[1] = pb1;
-  d.alpha = 1.0f;
-  d.causal = causal ? VH_GEMM_SKIP_UPPER : VH_GEMM_DENSE;
-  VH_TRY(vh_gemm(&d, s));
-  // 3. dS = P * (dP - sum(dP * P)) in place over G.
-  VH_TRY(softmax_common("vh_sm_bwd", 8, kSmBwdRpw, P, G, G, sh.B * sh.H * sh.S, sh.S, causal, 0, s, 1));
-  // 4. dq = (dS k) * scale.
-  vh_gemm_desc e{};
-  e.M = sh.S;
-  e.N = sh.Dk;
-  e.K = sh.S;
-  e.a = G;
-  e.a_sm = sh.S;
-  e.a_sk = 1;
-  e.b = k;  // B[k=j][n=d] = k[j][d]
-  e.b_sk = kl->strides[2];
-  e.b_sn = 1;
-  e.c = dq;
-  e.c_sm = dql->strides[2];
-  e.batch[0] = sh.B;
-  e.batch[1] = sh.H;
-  e.a_sb[0] = pb0;
-  e.a_sb[1] = pb1;
-  e.b_sb[0] = kl->strides[0];
-  e.b_sb[1] = kl->strides[1];
-  e.c_sb[0] = dql->strides[0];
-  e.c_sb[1] = dql->strides[1];
-  e.alpha = scale;
-  e.causal = causal ? VH_GEMM_K_LE_M : VH_GEMM_DENSE;
-  VH_TRY(vh_gemm(&e, s));
-  // 5. dk = (dS^T q) * scale: A[m=j][k=i] = dS[i][j].
-  e.a_sm = 1;
-  e.a_sk = sh.S;
-  e.b = q;
-  e.b_sk = ql->strides[2];
-  e.b_sb[0] = ql->strides[0];
-  e.b_sb[1] = ql->strides[1];
-  e.c = dk;
-  e.c_sm = dkl->strides[2];
-  e.c_sb[0] = dkl->strides[0];
-  e.c_sb[1] = dkl->strides[1];
-  e.causal = causal ? VH_GEMM_K_GE_M : VH_GEMM_DENSE;
-  VH_TRY(vh_gemm(&e, s));
-  // 6. dv = P^T dO.
-  e.a = P;
-  e.b = dout;
-  e.b_sk = dol->strides[2];
-  e.b_sb[0] = dol->strides[0];
-  e.b_sb[1] = dol->strides[1];
-  e.c = dv;
-  e.c_sm = dvl->strides[2];
-  e.c_sb[0] = dvl->strides[0];
-  e.c_sb[1] = dvl->strides[1];
-  e.alpha = 1.0f;
-  return vh_gemm(&e, s);
+  return attn_bwd_from_probs(P, G, q, ql, k, kl, v, vl, causal, dout, dol, dq, dql, dk, dkl, dv, dvl, sh, s);
+}
+
+int vh_fused_attention_bwd_probs(const float* P, const float* q, const vh_layout* ql, const float* k,
+                                 const vh_layout* kl, const float* v, const vh_layout* vl, int causal,
+                                 const float* dout, const vh_layout* dol, float* dq, const vh_layout* dql,
+                                 float* dk, const vh_layout* dkl, float* dv, const vh_layout* dvl, void* scratch,
+                                 size_t scratch_bytes, void* stream) {
+  VH_TRY(require_init());
+  AttnShape sh;
+  VH_TRY(attn_layout(ql, "fused attention q", &sh, true));
+  VH_TRY(attn_layout(kl, "fused attention k", &sh, false));
+  VH_TRY(attn_layout(vl, "fused attention v", &sh, false));
+  VH_TRY(attn_layout(dol, "fused attention grad_out", &sh, false));
+  VH_TRY(attn_layout(dql, "fused attention dq", &sh, false));
+  VH_TRY(attn_layout(dkl, "fused attention dk", &sh, false));
+  VH_TRY(attn_layout(dvl, "fused attention dv", &sh, false));
+  if (sh.B * sh.H * sh.S * sh.Dk == 0) return VH_OK;
+  if (!P || !q || !k || !v || !dout || !dq || !dk || !dv)
+    return fail(VH_ERR_INVALID, "vh_fused_attention_bwd_probs: null pointer");
+  if (sh.S > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_fused_attention_bwd_probs: S too large");
+  hipStream_t s = S(stream);
+  Scratch sc;
+  VH_TRY(sc.get(scratch, scratch_bytes, vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 0)));
+  return attn_bwd_from_probs(P, static_cast<float*>(sc.p), q, ql, k, kl, v, vl, causal, dout, dol, dq, dql, dk,
+                             dkl, dv, dvl, sh, s);
 }
 
 // ----------------------------------------------------------------- AdamW --

@@ -210,7 +210,8 @@ struct XentArgs {
   const float* logits;
   const float* targets;
   const float* grad_out;  // bwd: device scalar
-  float* out;             // fwd: per-row losses [B]; bwd: dlogits [B, V]
+  float* out;             // fwd: per-row losses [B]; bwd and fused: dlogits [B, V]
+  float* row_loss;        // fused forward+backward: per-row losses [B]
   VhErrRecord* err;
   int64_t B;
   int64_t ld;             // row stride of logits and dlogits (>= V)
