@@ -11,8 +11,14 @@
 //   reduce_to(grad, [C]) for a bias   -> vh_sum_rows (fixed grouping)
 //   x^T.matmul(dy) per batch + reduce_to over the batch -> one GEMM over all
 //     B*S rows (same sum, f32 rounding of a different grouping)
-// The attention's q/k/v/out stay in the Linear layout [B, S, H, Dk]; the
-// reshape/transpose views of nn:585-601 are passed as strides, so no copy runs.
+//   the q, k and v Linears (same input) -> one GEMM against the three weights
+//     stacked [3D, D] (the parameter block stores q.w, k.w, v.w back to back,
+//     and their biases); its backward is one GEMM for ln1's gradient (the sum
+//     dq Wq + dk Wk + dv Wv in one chain instead of three added in tape order),
+//     one for the stacked weight gradient, one row sum for the three biases
+// The attention's q/k/v/out stay in the Linear layout [B, S, H, Dk] (q, k, v as
+// column blocks of one [B*S, 3D] buffer); the reshape/transpose views of
+// nn:585-601 are passed as strides, so no copy runs.
 // The logits and their gradient have rows padded to Vp = V rounded up to 4
 // (zero columns), and lm_head's weight is followed by Vp - V zero rows, so the
 // three lm_head products run on 128-bit loads; the padding adds exact zeros.
@@ -65,10 +71,10 @@ struct vb_gpt {
   float *P = nullptr, *G = nullptr, *M = nullptr, *Vm = nullptr;  // params, grads, AdamW m and v
   int t = 0;
   // forward activations
-  float *ids, *tg, *pos, *tok, *pe, *h0, *ln1, *q, *k, *v, *att, *h1, *ln2, *y1, *g, *h2, *lnf, *logits;
+  float *ids, *tg, *pos, *tok, *pe, *h0, *ln1, *qkv, *att, *h1, *ln2, *y1, *g, *h2, *lnf, *logits;
   float *loss, *one;
   // backward buffers
-  float *dlogits, *dlnf, *dh, *dg, *df1, *lnx, *dh1, *datt, *dq, *dk, *dv, *dln1, *dh0;
+  float *dlogits, *dlnf, *dh, *dg, *df1, *lnx, *dh1, *datt, *dqkv, *dln1, *dh0;
   float *attP = nullptr, *attG = nullptr;  // attention probabilities (kept for the backward), workspace
   size_t att_bytes = 0;
   std::vector<void*> allocs;
@@ -154,17 +160,18 @@ struct vb_gpt {
     return VH_OK;
   }
 
-  // [B, H, S, Dk] view of a [B, S, D] tensor (reshape + transpose(1, 2)).
-  vh_layout heads() const {
+  // [B, H, S, Dk] view of a [B, S, D] tensor stored with row stride ld
+  // (reshape + transpose(1, 2)).
+  vh_layout heads(int64_t ld) const {
     vh_layout l{};
     l.rank = 4;
     l.dims[0] = c.B;
     l.dims[1] = c.H;
     l.dims[2] = c.S;
     l.dims[3] = Dk;
-    l.strides[0] = c.S * c.D;
+    l.strides[0] = c.S * ld;
     l.strides[1] = Dk;
-    l.strides[2] = c.D;
+    l.strides[2] = ld;
     l.strides[3] = 1;
     return l;
   }
@@ -179,11 +186,10 @@ struct vb_gpt {
     VB(vh_embedding_fwd(pos, p(1), pe, R, c.P, D, nullptr));
     VB(vh_binary(VH_OP_ADD, tok, &lrd, pe, &lrd, h0, nullptr));
     VB(vh_layernorm_fwd(h0, p(2), p(3), ln1, R, D, kEps, nullptr));
-    VB(linear(ln1, D, p(4), D, p(5), q, 0));
-    VB(linear(ln1, D, p(6), D, p(7), k, 0));
-    VB(linear(ln1, D, p(8), D, p(9), v, 0));
-    const vh_layout hl = heads();
-    VB(vh_fused_attention_fwd(q, &hl, k, &hl, v, &hl, nullptr, nullptr, 1, att, &hl, attP, att_bytes, nullptr));
+    VB(linear(ln1, D, p(4), 3 * D, p(5), qkv, 0));  // [q | k | v] = ln1 [Wq; Wk; Wv]^T + [bq | bk | bv]
+    const vh_layout hq = heads(3 * D), ha = heads(D);
+    VB(vh_fused_attention_fwd(qkv, &hq, qkv + D, &hq, qkv + 2 * D, &hq, nullptr, nullptr, 1, att, &ha, attP,
+                              att_bytes, nullptr));
     VB(vh_d2d(h1, h0, (size_t)(R * D) * sizeof(float), nullptr));
     VB(linear(att, D, p(10), D, p(11), h1, 1));  // h1 = h0 + (att W_o^T + b_o)
     VB(vh_layernorm_fwd(h1, p(12), p(13), ln2, R, D, kEps, nullptr));
@@ -222,20 +228,14 @@ struct vb_gpt {
     VB(vh_sum_rows(dh1, R, D, gr(11), nullptr, 0, nullptr));
     VB(linear_dx(dh1, D, p(10), D, datt, 0));
     VB(linear_dw(dh1, D, att, D, gr(10)));
-    const vh_layout hl = heads();
+    const vh_layout hq = heads(3 * D), ha = heads(D);
     // The Fused attention arm (autograd:600-612) from the forward's probabilities.
-    VB(vh_fused_attention_bwd_probs(attP, q, &hl, k, &hl, v, &hl, 1, datt, &hl, dq, &hl, dk, &hl, dv, &hl, attG,
-                                    att_bytes, nullptr));
-    // v, k, q projections in reverse tape order; ln1's gradient accumulates.
-    VB(vh_sum_rows(dv, R, D, gr(9), nullptr, 0, nullptr));
-    VB(linear_dx(dv, D, p(8), D, dln1, 0));
-    VB(linear_dw(dv, D, ln1, D, gr(8)));
-    VB(vh_sum_rows(dk, R, D, gr(7), nullptr, 0, nullptr));
-    VB(linear_dx(dk, D, p(6), D, dln1, 1));
-    VB(linear_dw(dk, D, ln1, D, gr(6)));
-    VB(vh_sum_rows(dq, R, D, gr(5), nullptr, 0, nullptr));
-    VB(linear_dx(dq, D, p(4), D, dln1, 1));
-    VB(linear_dw(dq, D, ln1, D, gr(4)));
+    VB(vh_fused_attention_bwd_probs(attP, qkv, &hq, qkv + D, &hq, qkv + 2 * D, &hq, 1, datt, &ha, dqkv, &hq,
+                                    dqkv + D, &hq, dqkv + 2 * D, &hq, attG, att_bytes, nullptr));
+    // The q, k, v Linears at once: bias sums, ln1's gradient, stacked weight gradient.
+    VB(vh_sum_rows(dqkv, R, 3 * D, gr(5), nullptr, 0, nullptr));
+    VB(linear_dx(dqkv, 3 * D, p(4), D, dln1, 0));
+    VB(linear_dw(dqkv, 3 * D, ln1, D, gr(4)));
     VB(vh_layernorm_bwd(h0, p(2), dln1, lnx, gr(2), gr(3), R, D, kEps, nullptr, 0, nullptr));
     VB(vh_binary(VH_OP_ADD, dh1, &lrd, lnx, &lrd, dh0, nullptr));
     // h0 = tok + pe; the embeddings' arms (position recorded last, runs first).
@@ -265,11 +265,16 @@ int vb_gpt_create(const vb_gpt_config* cfg, vb_gpt** out) {
   const int64_t D = c.D, F = c.F;
   const int64_t sizes[VB_GPT_NPARAMS] = {c.V * D, c.P * D, D, D, D * D, D, D * D, D, D * D, D, D * D, D,
                                          D,       D,       F * D, F, D * F, D, D, D, c.V * D};
+  // Memory order: q.w, k.w, v.w back to back (a [3D, D] stack), then q.b, k.b,
+  // v.b (a [3D] vector); every other tensor starts 256-byte aligned.
+  const int order[VB_GPT_NPARAMS] = {0, 1, 2, 3, 4, 6, 8, 5, 7, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20};
   size_t o = 0;
-  for (int i = 0; i < VB_GPT_NPARAMS; ++i) {
+  for (int j = 0; j < VB_GPT_NPARAMS; ++j) {
+    const int i = order[j];
     g->off[i] = (int64_t)o;
     g->numel[i] = sizes[i];
-    o += ((size_t)sizes[i] + 63) & ~size_t(63);  // 256-byte aligned tensors
+    const bool packed = i == 4 || i == 6 || i == 5 || i == 7;  // followed by the next of its stack
+    o += packed ? (size_t)sizes[i] : (((size_t)sizes[i] + 63) & ~size_t(63));
   }
   o += (((size_t)((g->Vp - c.V) * D)) + 63) & ~size_t(63);  // zero rows after lm_head.w
   g->block_floats = o;
@@ -283,10 +288,11 @@ int vb_gpt_create(const vb_gpt_config* cfg, vb_gpt** out) {
   A(&g->M, (int64_t)o, 1);
   A(&g->Vm, (int64_t)o, 1);
   for (float** p : {&g->ids, &g->tg, &g->pos}) A(p, R, 1);
-  for (float** p : {&g->tok, &g->pe, &g->h0, &g->ln1, &g->q, &g->k, &g->v, &g->att, &g->h1, &g->ln2, &g->h2,
-                    &g->lnf, &g->dlnf, &g->dh, &g->lnx, &g->dh1, &g->datt, &g->dq, &g->dk, &g->dv, &g->dln1,
-                    &g->dh0})
+  for (float** p : {&g->tok, &g->pe, &g->h0, &g->ln1, &g->att, &g->h1, &g->ln2, &g->h2, &g->lnf, &g->dlnf,
+                    &g->dh, &g->lnx, &g->dh1, &g->datt, &g->dln1, &g->dh0})
     A(p, R * D);
+  A(&g->qkv, 3 * R * D);
+  A(&g->dqkv, 3 * R * D);
   for (float** p : {&g->y1, &g->g, &g->dg, &g->df1}) A(p, R * F);
   A(&g->logits, R * Vp, 1);
   A(&g->dlogits, R * Vp, 1);
