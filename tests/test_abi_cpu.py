@@ -117,6 +117,7 @@ def launcher_kernel_names():
     for a in ("k4", "k1", "m4", "m1"):
         for b in ("k4", "k1", "n4", "n1"):
             names.add(f"vh_gemm_{a}_{b}")
+            names.add(f"vh_gemm_{a}_{b}_t64")
     return names
 
 

@@ -64,7 +64,8 @@ def test_matmul_reference_kats(vh):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 1, 1), (5, 7, 3), (128, 32, 128), (129, 33, 131),
-                                   (300, 768, 200), (64, 1000, 96), (257, 64, 513)])
+                                   (300, 768, 200), (64, 1000, 96), (257, 64, 513),
+                                   (300, 200, 64), (257, 96, 33), (1024, 1024, 64)])
 def test_matmul_shapes(vh, M, K, N):
     """Parity at the block step's scale (activations ~N(0,1), weights
     ~N(0,0.02)); and, with both operands ~N(0,1), the error bound every f32
@@ -300,7 +301,7 @@ def test_sum_rows(vh, rows, C):
     assert_parity(fetch(vh, OUT, (C,)), O.reduce_to(x, (C,)), x.astype(np.float64).sum(axis=0), name="sum_rows")
 
 
-@pytest.mark.parametrize("M,N,K", [(200, 150, 8192), (768, 768, 16384), (3072, 768, 4096)])
+@pytest.mark.parametrize("M,N,K", [(200, 150, 8192), (768, 768, 16384), (3072, 768, 4096), (200, 64, 8192)])
 def test_gemm_split_k(vh, M, N, K):
     """Few C tiles over a long K (the weight gradients) take the split-K path:
     partials summed in a fixed order, then the epilogue."""

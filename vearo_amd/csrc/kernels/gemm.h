@@ -9,8 +9,9 @@
 // `* scale` and `+ mask` in attention (cpu:2431-2449), `+ bias` in Linear
 // (nn:120-128), and gradient accumulation `existing.add(g)` (autograd:733-742).
 //
-// Tiling: a 256-thread workgroup computes a 128 x 128 tile of C; its 4 waves
-// own 64 x 64 quadrants as 2 x 2 matrix-core tiles of 32 x 32. K advances in
+// Tiling: a 256-thread workgroup computes a 128 x TN tile of C (TN = 128, or
+// 64 for the attention products with N = Dk = 64); its 4 waves own 64 x TN/2
+// quadrants as 2 x TN/64 matrix-core tiles of 32 x 32. K advances in
 // tiles of 32, double-buffered through LDS: the global loads of tile t+1 are in
 // flight while tile t is multiplied. LDS keeps each operand in the orientation
 // of its HBM layout, so staging is 128-bit and bank-conflict free both ways:
@@ -32,25 +33,24 @@
 #include "common.h"
 
 #define GM_TM VH_GEMM_TILE_M
-#define GM_TN VH_GEMM_TILE_N
 #define GM_TK 32
 #define GM_LS (GM_TK + 4)  // [row][k] LDS row stride (floats): 16-byte aligned rows, staggered banks
 #define GM_LT (GM_TM + 4)  // [k][row] LDS stride (floats)
-#define GM_STAGE (GM_TM * GM_LS > GM_TK * GM_LT ? GM_TM * GM_LS : GM_TK * GM_LT)
+#define GM_STAGE (GM_TM * GM_LS > GM_TK * GM_LT ? GM_TM * GM_LS : GM_TK * GM_LT)  // one 128-row operand tile
 #define GM_GROUP 8         // tile rows per group in the launch order (L2 reuse of B)
 
 typedef float vh_f32x16 __attribute__((ext_vector_type(16)));
 
-// The [128 rows x 32 k] tile whose element (r, k) is at
+// The [NR rows x 32 k] tile (NR = 128 or 64) whose element (r, k) is at
 //   KC:  base[(r0 + r) * ld + k0 + k]      !KC: base[(k0 + k) * ld + r0 + r]
-// into 16 staging registers per thread; rows >= R or k >= K read as 0.
+// into NR/8 staging registers per thread; rows >= R or k >= K read as 0.
 // VEC requires 16-byte aligned base and ld, and K (KC) or R (!KC) % 4 == 0.
-template <bool KC, bool VEC>
+template <bool KC, bool VEC, int NR>
 VH_DEV void gm_load(const float* base, int64_t ld, int64_t r0, int64_t R, int64_t k0, int64_t K, int tid,
-                    float (&st)[16]) {
+                    float (&st)[NR / 8]) {
   if constexpr (KC && VEC) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NR / 32; ++i) {
       const int r = (tid >> 3) + 32 * i, k = (tid & 7) * 4;
       vh_f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
       if (r0 + r < R && k0 + k < K) v = *reinterpret_cast<const vh_f4*>(base + (r0 + r) * ld + k0 + k);
@@ -59,14 +59,15 @@ VH_DEV void gm_load(const float* base, int64_t ld, int64_t r0, int64_t R, int64_
     }
   } else if constexpr (KC) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < NR / 8; ++i) {
       const int r = (tid >> 5) + 8 * i, k = tid & 31;
       st[i] = (r0 + r < R && k0 + k < K) ? base[(r0 + r) * ld + k0 + k] : 0.0f;
     }
   } else if constexpr (VEC) {
+    constexpr int TPR = NR / 4;  // threads per k row
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int k = (tid >> 5) + 8 * i, r = (tid & 31) * 4;
+    for (int i = 0; i < NR / 32; ++i) {
+      const int k = tid / TPR + (256 / TPR) * i, r = (tid % TPR) * 4;
       vh_f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
       if (k0 + k < K && r0 + r < R) v = *reinterpret_cast<const vh_f4*>(base + (k0 + k) * ld + r0 + r);
 #pragma unroll
@@ -74,50 +75,49 @@ VH_DEV void gm_load(const float* base, int64_t ld, int64_t r0, int64_t R, int64_
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int k = (tid >> 7) + 2 * i, r = tid & 127;
+    for (int i = 0; i < NR / 8; ++i) {
+      const int k = tid / NR + (256 / NR) * i, r = tid % NR;
       st[i] = (k0 + k < K && r0 + r < R) ? base[(k0 + k) * ld + r0 + r] : 0.0f;
     }
   }
 }
 
-template <bool KC, bool VEC>
-VH_DEV void gm_store_lds(float* S, int tid, const float (&st)[16]) {
+template <bool KC, bool VEC, int NR>
+VH_DEV void gm_store_lds(float* S, int tid, const float (&st)[NR / 8]) {
   if constexpr (KC && VEC) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NR / 32; ++i) {
       const int r = (tid >> 3) + 32 * i, k = (tid & 7) * 4;
       vh_f4 v = {st[4 * i], st[4 * i + 1], st[4 * i + 2], st[4 * i + 3]};
       *reinterpret_cast<vh_f4*>(S + r * GM_LS + k) = v;
     }
   } else if constexpr (KC) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) S[((tid >> 5) + 8 * i) * GM_LS + (tid & 31)] = st[i];
+    for (int i = 0; i < NR / 8; ++i) S[((tid >> 5) + 8 * i) * GM_LS + (tid & 31)] = st[i];
   } else if constexpr (VEC) {
+    constexpr int TPR = NR / 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int k = (tid >> 5) + 8 * i, r = (tid & 31) * 4;
+    for (int i = 0; i < NR / 32; ++i) {
+      const int k = tid / TPR + (256 / TPR) * i, r = (tid % TPR) * 4;
       vh_f4 v = {st[4 * i], st[4 * i + 1], st[4 * i + 2], st[4 * i + 3]};
       *reinterpret_cast<vh_f4*>(S + k * GM_LT + r) = v;
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) S[((tid >> 7) + 2 * i) * GM_LT + (tid & 127)] = st[i];
+    for (int i = 0; i < NR / 8; ++i) S[(tid / NR + (256 / NR) * i) * GM_LT + tid % NR] = st[i];
   }
 }
 
-// Fragments of rows `row` and `row + 32` for k = k0 .. k0+3 (4 matrix-core steps).
+// Fragment of row `row` for k = k0 .. k0+3 (4 matrix-core steps).
 template <bool KC>
-VH_DEV void gm_frag(const float* S, int row, int k0, vh_f4& f0, vh_f4& f1) {
+VH_DEV vh_f4 gm_frag(const float* S, int row, int k0) {
   if constexpr (KC) {
-    f0 = *reinterpret_cast<const vh_f4*>(S + row * GM_LS + k0);
-    f1 = *reinterpret_cast<const vh_f4*>(S + (row + 32) * GM_LS + k0);
+    return *reinterpret_cast<const vh_f4*>(S + row * GM_LS + k0);
   } else {
+    vh_f4 f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      f0[e] = S[(k0 + e) * GM_LT + row];
-      f1[e] = S[(k0 + e) * GM_LT + row + 32];
-    }
+    for (int e = 0; e < 4; ++e) f[e] = S[(k0 + e) * GM_LT + row];
+    return f;
   }
 }
 
@@ -137,14 +137,16 @@ VH_DEV void gm_tile_of(int bid, int nblk, int tiles_m, int tiles_n, int& tm, int
   tn = in / gsize;
 }
 
-template <bool A_KC, bool A_VEC, bool B_KC, bool B_VEC>
+template <bool A_KC, bool A_VEC, bool B_KC, bool B_VEC, int TN>
 VH_DEV void gemm_f32_impl(const GemmArgs& a) {
+  static_assert(TN == 128 || TN == 64, "C tile width");
+  constexpr int NTW = TN / 64;  // 32-wide n tiles per wave
   __shared__ __attribute__((aligned(16))) float As[2][GM_STAGE];
   __shared__ __attribute__((aligned(16))) float Bs[2][GM_STAGE];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   int tm, tn;
   gm_tile_of(blockIdx.x, gridDim.x, a.tiles_m, a.tiles_n, tm, tn);
-  const int64_t m0 = (int64_t)tm * GM_TM, n0 = (int64_t)tn * GM_TN;
+  const int64_t m0 = (int64_t)tm * GM_TM, n0 = (int64_t)tn * TN;
   if (a.causal == 1 && n0 > m0 + GM_TM - 1) return;  // the whole tile is masked
 
   const bool split = a.ksplit > 1;
@@ -161,44 +163,47 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
     ke = kb + a.kchunk < a.K ? kb + a.kchunk : a.K;
   }
 
-  vh_f32x16 acc[2][2];
+  vh_f32x16 acc[2][NTW];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = vh_f32x16{};
+    for (int j = 0; j < NTW; ++j) acc[i][j] = vh_f32x16{};
 
   const int wm = w >> 1, wn = w & 1, li = lane & 31, h = lane >> 5;
-  float sa[16], sb[16];
+  float sa[GM_TM / 8], sb[TN / 8];
   int s = 0;
   if (kb < ke) {
-    gm_load<A_KC, A_VEC>(A, a.lda, m0, a.M, kb, a.K, tid, sa);
-    gm_load<B_KC, B_VEC>(B, a.ldb, n0, a.N, kb, a.K, tid, sb);
-    gm_store_lds<A_KC, A_VEC>(As[0], tid, sa);
-    gm_store_lds<B_KC, B_VEC>(Bs[0], tid, sb);
+    gm_load<A_KC, A_VEC, GM_TM>(A, a.lda, m0, a.M, kb, a.K, tid, sa);
+    gm_load<B_KC, B_VEC, TN>(B, a.ldb, n0, a.N, kb, a.K, tid, sb);
+    gm_store_lds<A_KC, A_VEC, GM_TM>(As[0], tid, sa);
+    gm_store_lds<B_KC, B_VEC, TN>(Bs[0], tid, sb);
     __syncthreads();
   }
   for (int64_t k0 = kb; k0 < ke; k0 += GM_TK) {
     const bool more = k0 + GM_TK < ke;
     if (more) {
-      gm_load<A_KC, A_VEC>(A, a.lda, m0, a.M, k0 + GM_TK, a.K, tid, sa);
-      gm_load<B_KC, B_VEC>(B, a.ldb, n0, a.N, k0 + GM_TK, a.K, tid, sb);
+      gm_load<A_KC, A_VEC, GM_TM>(A, a.lda, m0, a.M, k0 + GM_TK, a.K, tid, sa);
+      gm_load<B_KC, B_VEC, TN>(B, a.ldb, n0, a.N, k0 + GM_TK, a.K, tid, sb);
     }
 #pragma unroll
     for (int kc = 0; kc < 16; kc += 4) {
-      vh_f4 a0, a1, b0, bv1;
-      gm_frag<A_KC>(As[s], wm * 64 + li, h * 16 + kc, a0, a1);
-      gm_frag<B_KC>(Bs[s], wn * 64 + li, h * 16 + kc, b0, bv1);
+      const vh_f4 a0 = gm_frag<A_KC>(As[s], wm * 64 + li, h * 16 + kc);
+      const vh_f4 a1 = gm_frag<A_KC>(As[s], wm * 64 + 32 + li, h * 16 + kc);
+      vh_f4 bf[NTW];
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) bf[nt] = gm_frag<B_KC>(Bs[s], wn * (TN / 2) + nt * 32 + li, h * 16 + kc);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], b0[e], acc[0][0], 0, 0, 0);
-        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], bv1[e], acc[0][1], 0, 0, 0);
-        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], b0[e], acc[1][0], 0, 0, 0);
-        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], bv1[e], acc[1][1], 0, 0, 0);
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) {
+          acc[0][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], bf[nt][e], acc[0][nt], 0, 0, 0);
+          acc[1][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], bf[nt][e], acc[1][nt], 0, 0, 0);
+        }
       }
     }
     if (more) {
-      gm_store_lds<A_KC, A_VEC>(As[s ^ 1], tid, sa);
-      gm_store_lds<B_KC, B_VEC>(Bs[s ^ 1], tid, sb);
+      gm_store_lds<A_KC, A_VEC, GM_TM>(As[s ^ 1], tid, sa);
+      gm_store_lds<B_KC, B_VEC, TN>(Bs[s ^ 1], tid, sb);
     }
     __syncthreads();
     s ^= 1;
@@ -211,8 +216,8 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int64_t n = n0 + wn * 64 + nt * 32 + li;
+      for (int nt = 0; nt < NTW; ++nt) {
+        const int64_t n = n0 + wn * (TN / 2) + nt * 32 + li;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int64_t m = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -225,8 +230,8 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int64_t n = n0 + wn * 64 + nt * 32 + li;
+    for (int nt = 0; nt < NTW; ++nt) {
+      const int64_t n = n0 + wn * (TN / 2) + nt * 32 + li;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t m = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);

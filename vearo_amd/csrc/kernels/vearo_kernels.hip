@@ -150,7 +150,10 @@ extern "C" __global__ void __launch_bounds__(256) vh_fill(FillArgs a) { fill_imp
 // m/n-contiguous ("m"/"n"), with 128-bit ("4") or 32-bit ("1") global loads.
 #define K_GEMM(AK, AV, BK, BV, NAME)                                                            \
   extern "C" __global__ void __launch_bounds__(256, 2) NAME(GemmArgs a) {                      \
-    gemm_f32_impl<AK, AV, BK, BV>(a);                                                           \
+    gemm_f32_impl<AK, AV, BK, BV, 128>(a);                                                      \
+  }                                                                                             \
+  extern "C" __global__ void __launch_bounds__(256, 2) NAME##_t64(GemmArgs a) {                \
+    gemm_f32_impl<AK, AV, BK, BV, 64>(a);                                                       \
   }
 K_GEMM(true, true, true, true, vh_gemm_k4_k4)
 K_GEMM(true, true, true, false, vh_gemm_k4_k1)

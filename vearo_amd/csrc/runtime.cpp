@@ -980,6 +980,52 @@ static bool gemm_vec_ok(const float* p, int64_t ld, int64_t ext, const int64_t* 
   return aligned16(p) && ld % 4 == 0 && ext % 4 == 0 && sb[0] % 4 == 0 && sb[1] % 4 == 0;
 }
 
+namespace {
+struct GemmPlan {
+  bool narrow;     // 128 x 64 C tiles instead of 128 x 128
+  int64_t ksplit;  // K ranges, each its own workgroups; 1 = no split
+  int64_t kchunk;  // k per range, a multiple of the 32-wide k tile
+};
+
+// Tile width and split-K for a product: the shape whose estimated time is
+// least. A split or a narrow tile pays where the C tiles leave the chip's
+// resident workgroups (2 per CU) idle -- a last wave mostly empty (768 tiles on
+// 512 slots) or too few tiles to fill it (the weight gradients, 768 x 768
+// outputs over K = 16384 rows). Time is counted in k steps of one 128-wide
+// tile: waves x tile width x (k per range + a fixed cost for the prologue and
+// epilogue), a narrow tile at 0.88 of the wide one's matrix-core rate (its B
+// fragments feed half as many products), plus the fixed-order reduce of the
+// split partials ((ks + 1) M N floats through HBM). Batched and causal
+// products do not split. N <= 64 (attention's P v and its gradients,
+// N = Dk = 64) always takes the narrow tile.
+GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool may_split) {
+  const int64_t slots = 2 * std::max(g_rt.cu_count, 1);
+  GemmPlan best{N <= VH_GEMM_TILE_N / 2, 1, K};
+  if (!may_split || K == 0) return best;
+  double best_t = -1.0;
+  for (int tn : {VH_GEMM_TILE_N, VH_GEMM_TILE_N / 2}) {
+    if (N <= VH_GEMM_TILE_N / 2 && tn != VH_GEMM_TILE_N / 2) continue;
+    const int64_t tiles = cdiv(M, VH_GEMM_TILE_M) * cdiv(N, tn);
+    for (int64_t want = 1; want <= 32; ++want) {
+      if (want > 1 && K / want < 256) break;
+      const int64_t kchunk = cdiv(cdiv(K, want), 32) * 32;
+      const int64_t ks = cdiv(K, kchunk);
+      if (ks != want) continue;
+      const int64_t n = tiles * ks;
+      const double waves = (double)cdiv(n, slots);  // a part-filled last wave costs a whole one
+      double t = waves * ((double)tn / VH_GEMM_TILE_N) * ((double)kchunk + 48.0) /
+                 (tn == VH_GEMM_TILE_N ? 1.0 : 0.88);
+      if (ks > 1) t += (double)(ks + 1) * (double)M * (double)N * 4.0 / 536e3;
+      if (best_t < 0.0 || t < best_t) {
+        best_t = t;
+        best = GemmPlan{tn != VH_GEMM_TILE_N, ks, kchunk};
+      }
+    }
+  }
+  return best;
+}
+}  // namespace
+
 int vh_gemm(const vh_gemm_desc* d, void* stream) {
   VH_TRY(require_init());
   if (!d) return fail(VH_ERR_INVALID, "vh_gemm: null descriptor");
@@ -1007,35 +1053,15 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
   const int64_t ldb = bkc ? (N == 1 ? 0 : d->b_sn) : d->b_sk;
   const bool avec = K > 0 && gemm_vec_ok(d->a, lda, akc ? K : M, d->a_sb);
   const bool bvec = K > 0 && gemm_vec_ok(d->b, ldb, bkc ? K : N, d->b_sb);
-  const int64_t tiles_m = cdiv(M, VH_GEMM_TILE_M), tiles_n = cdiv(N, VH_GEMM_TILE_N);
+  const GemmPlan plan = gemm_plan(M, N, K, d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE);
+  const int64_t tiles_m = cdiv(M, VH_GEMM_TILE_M), tiles_n = cdiv(N, plan.narrow ? 64 : VH_GEMM_TILE_N);
   if (tiles_m * tiles_n > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_gemm: too many tiles");
   const std::string name = std::string("vh_gemm_") + (akc ? "k" : "m") + (avec ? "4" : "1") + "_" +
-                           (bkc ? "k" : "n") + (bvec ? "4" : "1");
+                           (bkc ? "k" : "n") + (bvec ? "4" : "1") + (plan.narrow ? "_t64" : "");
   hipStream_t s = S(stream);
-  // Split K for an unbatched product over a long K when its C tiles would
-  // leave the chip idle: too few tiles to fill it (the weight gradients, 768 x
-  // 768 outputs over K = 16384 rows), or a last wave of workgroups mostly empty
-  // (768 tiles on 512 resident workgroups). Each split writes its raw partial;
-  // a fixed-order reduce sums them and applies the epilogue.
   const int64_t tiles = tiles_m * tiles_n;
-  const int64_t slots = 2 * std::max(g_rt.cu_count, 1);  // 2 resident workgroups per CU (LDS)
-  int64_t ks = 1;
-  if (d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE && K >= 4096) {
-    if (tiles < slots) {
-      ks = std::min<int64_t>({16, cdiv(slots, tiles), K / 1024});
-    } else {
-      for (int64_t c = 1; c <= 4 && K / c >= 1024; ++c) {
-        const int64_t n = tiles * c;
-        if ((double)n / (double)(cdiv(n, slots) * slots) >= 0.95) {
-          ks = c;
-          break;
-        }
-      }
-    }
-  }
-  if (ks > 1) {
-    const int64_t kchunk = cdiv(cdiv(K, ks), 32) * 32;
-    ks = cdiv(K, kchunk);
+  {
+    const int64_t ks = plan.ksplit, kchunk = plan.kchunk;
     if (ks > 1) {
       void* ws = nullptr;
       VH_TRY(g_arena.alloc((size_t)(ks * M * N) * sizeof(float), &ws));
