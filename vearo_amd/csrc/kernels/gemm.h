@@ -179,31 +179,49 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
     gm_store_lds<B_KC, B_VEC, TN>(Bs[0], tid, sb);
     __syncthreads();
   }
+  // Per k tile: the next tile's global loads go out first; then all of this
+  // tile's fragments are read from LDS at once (the products wait only on the
+  // reads they use, which return in order); the next tile is written to the
+  // other LDS buffer (free since the last barrier) between the last group's
+  // products. On the last tile that write goes to a buffer nothing reads again
+  // (it keeps the loop body one block, so the order below holds).
+  constexpr int RD = 4 * ((A_KC ? 2 : 8) + NTW * (B_KC ? 1 : 4));              // LDS reads per tile
+  constexpr int WR = (A_VEC ? GM_TM / 32 : GM_TM / 8) + (B_VEC ? TN / 32 : TN / 8);  // LDS writes per tile
+  constexpr int MF = 8 * NTW;                                                   // products per 4-k group
   for (int64_t k0 = kb; k0 < ke; k0 += GM_TK) {
     const bool more = k0 + GM_TK < ke;
     if (more) {
       gm_load<A_KC, A_VEC, GM_TM>(A, a.lda, m0, a.M, k0 + GM_TK, a.K, tid, sa);
       gm_load<B_KC, B_VEC, TN>(B, a.ldb, n0, a.N, k0 + GM_TK, a.K, tid, sb);
     }
+    vh_f4 fa[4][2], fb[4][NTW];
 #pragma unroll
-    for (int kc = 0; kc < 16; kc += 4) {
-      const vh_f4 a0 = gm_frag<A_KC>(As[s], wm * 64 + li, h * 16 + kc);
-      const vh_f4 a1 = gm_frag<A_KC>(As[s], wm * 64 + 32 + li, h * 16 + kc);
-      vh_f4 bf[NTW];
+    for (int q = 0; q < 4; ++q) {
+      const int kc = h * 16 + 4 * q;
+      fa[q][0] = gm_frag<A_KC>(As[s], wm * 64 + li, kc);
+      fa[q][1] = gm_frag<A_KC>(As[s], wm * 64 + 32 + li, kc);
 #pragma unroll
-      for (int nt = 0; nt < NTW; ++nt) bf[nt] = gm_frag<B_KC>(Bs[s], wn * (TN / 2) + nt * 32 + li, h * 16 + kc);
+      for (int nt = 0; nt < NTW; ++nt) fb[q][nt] = gm_frag<B_KC>(Bs[s], wn * (TN / 2) + nt * 32 + li, kc);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt) {
-          acc[0][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], bf[nt][e], acc[0][nt], 0, 0, 0);
-          acc[1][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], bf[nt][e], acc[1][nt], 0, 0, 0);
+          acc[0][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][0][e], fb[q][nt][e], acc[0][nt], 0, 0, 0);
+          acc[1][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][1][e], fb[q][nt][e], acc[1][nt], 0, 0, 0);
         }
       }
     }
-    if (more) {
-      gm_store_lds<A_KC, A_VEC, GM_TM>(As[s ^ 1], tid, sa);
-      gm_store_lds<B_KC, B_VEC, TN>(Bs[s ^ 1], tid, sb);
+    gm_store_lds<A_KC, A_VEC, GM_TM>(As[s ^ 1], tid, sa);
+    gm_store_lds<B_KC, B_VEC, TN>(Bs[s ^ 1], tid, sb);
+    __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);      // all fragment reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 3 * MF, 0);  // groups 0-2
+#pragma unroll
+    for (int i = 0; i < MF; ++i) {                            // group 3 with the writes
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x200, (WR + MF - 1) / MF, 0);
     }
     __syncthreads();
     s ^= 1;
