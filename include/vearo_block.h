@@ -70,6 +70,14 @@ int vb_gpt_adamw(vb_gpt* g, float lr, float beta1, float beta2, float eps, float
  * own text included). */
 const char* vb_last_error(void);
 
+/* The parameters as a `.ve` checkpoint, SimpleGPT::parameters() order and
+ * shapes (crates/vearo/src/checkpoint.rs:9-33 on model.parameters()), and back
+ * (checkpoint.rs:40-91; the reference's count/shape checks and texts). The
+ * file is the one the reference's save_checkpoint writes for the same model.
+ * Waits for queued work on the library's stream. */
+int vb_gpt_save(vb_gpt* g, const char* path);
+int vb_gpt_load(vb_gpt* g, const char* path);
+
 /* The config[4] training step: forward + backward + AdamW. */
 int vb_gpt_train_step(vb_gpt* g, float lr, float beta1, float beta2, float eps, float weight_decay);
 

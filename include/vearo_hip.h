@@ -42,6 +42,7 @@ extern "C" {
 #define VH_ERR_DEVICE_PANIC 4  /* a kernel met data the CPU backend panics on */
 #define VH_ERR_UNSUPPORTED 5   /* size outside the implemented range          */
 #define VH_ERR_OOM 6           /* device allocation failed                    */
+#define VH_ERR_IO 7            /* a file could not be opened, read or written */
 
 #define VH_MAX_RANK 8
 
@@ -321,6 +322,36 @@ int vh_fused_attention_bwd_probs(const float* P, const float* q, const vh_layout
 int vh_adamw_step(float* param, const float* grad, float* m, float* v, int64_t n, int32_t t,
                   float lr, float beta1, float beta2, float eps, float weight_decay,
                   void* stream);
+
+/* --------------------------------------------- .ve checkpoints of device tensors -- */
+
+/* The `.ve` weight checkpoint (crates/vearo/src/checkpoint.rs:9-33): u32 tensor
+ * count, then per tensor u32 rank, u32 dims, u32 element count and the f32
+ * data, all little-endian. tensors[i] is a device pointer with layout
+ * layouts[i]; each must be contiguous (the reference's to_vec_f32 asserts it,
+ * tensor.rs:751-755), and every dim and element count must fit a u32 (the
+ * reference truncates silently; this returns VH_ERR_UNSUPPORTED). Data leaves
+ * the device through two pinned staging buffers, so the file writes overlap
+ * the copies. Queued work on `stream` that writes the tensors is waited for;
+ * returns after the file is complete and closed. Replaces save_checkpoint. */
+int vh_checkpoint_save(const char* path, int32_t n, const float* const* tensors,
+                       const vh_layout* layouts, void* stream);
+
+/* Reads a `.ve` checkpoint into n device tensors in order (checkpoint.rs:40-91),
+ * with the reference's checks and texts, which vh_last_error() reports:
+ *   count differs   -> VH_ERR_INVALID "Checkpoint tensor count does not match
+ *                      model parameter count";
+ *   dims differ     -> VH_ERR_INVALID "Checkpoint shape does not match parameter
+ *                      shape";
+ *   not contiguous  -> VH_ERR_INVALID "copy_from_slice requires contiguous tensor";
+ *   element count   -> VH_ERR_INVALID "Source slice length must match tensor numel"
+ *   differs            (tensor.rs:816-826);
+ *   short file, open or read failure -> VH_ERR_IO.
+ * Tensors before the failing one keep their loaded values, as in the reference.
+ * The copies run on `stream`; returns once they are done. Replaces
+ * load_checkpoint. */
+int vh_checkpoint_load(const char* path, int32_t n, float* const* tensors,
+                       const vh_layout* layouts, void* stream);
 
 #ifdef __cplusplus
 }

@@ -78,6 +78,8 @@ def _load():
                           c_float],
         "vo_gpt_param_numel": [POINTER(GptConfig), POINTER(c_int64)],
         "vo_gpt_step": [POINTER(GptConfig), POINTER(c_void_p), f, f, f, POINTER(c_void_p)] + err,
+        "vo_checkpoint_save": [c_char_p, c_int, POINTER(c_void_p), L] + err,
+        "vo_checkpoint_load": [c_char_p, c_int, POINTER(c_void_p), L] + err,
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -371,3 +373,45 @@ def gpt_step(cfg: GptConfig, params, ids, targets, grads: bool = True):
         gp = (c_void_p * len(gs))(*[g.ctypes.data for g in gs])
     _call(lib.vo_gpt_step, ctypes.byref(cfg), pp, _ptr(ids), _ptr(targets), _ptr(loss), gp)
     return float(loss[0]), gs
+
+
+class CheckpointIOError(OSError):
+    """The reference's save/load_checkpoint would return this io::Error."""
+
+
+def _ckpt_args(arrays):
+    n = len(arrays)
+    ptrs = (c_void_p * max(n, 1))()
+    lays = (Layout * max(n, 1))()
+    keep = []
+    for i, a in enumerate(arrays):
+        if a.dtype != np.float32:
+            raise TypeError("checkpoint tensors are float32")
+        keep.append(a)
+        ptrs[i] = a.ctypes.data if a.size else None
+        if a.flags["C_CONTIGUOUS"]:
+            lays[i] = layout(a.shape)
+        else:
+            lays[i] = layout(a.shape, [st // 4 for st in a.strides])
+    return n, ptrs, lays, keep
+
+
+def _ckpt_call(fn, path, arrays):
+    n, ptrs, lays, keep = _ckpt_args(arrays)
+    buf = ctypes.create_string_buffer(512)
+    rc = fn(os.fsencode(path), n, ptrs, lays, buf, 512)
+    del keep
+    if rc == 1:
+        raise Panic(buf.value.decode())
+    if rc == 2:
+        raise CheckpointIOError(buf.value.decode())
+
+
+def checkpoint_save(path, arrays) -> None:
+    """save_checkpoint (crates/vearo/src/checkpoint.rs:9-33) of float32 arrays."""
+    _ckpt_call(lib.vo_checkpoint_save, path, [np.asarray(a) for a in arrays])
+
+
+def checkpoint_load(path, arrays) -> None:
+    """load_checkpoint (checkpoint.rs:40-91) into float32 arrays, in place."""
+    _ckpt_call(lib.vo_checkpoint_load, path, arrays)

@@ -39,6 +39,7 @@ typedef struct {
 /* Return codes: 0 = ok, 1 = the reference would panic (message in err). */
 #define VO_OK 0
 #define VO_PANIC 1
+#define VO_IOERR 2 /* the reference returns an io::Error (message in err) */
 
 /* Binary broadcast ops (cpu:160-238). op: 0 add, 1 sub, 2 mul, 3 div.
  * out_shape must be the broadcast of the two shapes; out is contiguous. */
@@ -153,6 +154,12 @@ void vo_gpt_param_numel(const vo_gpt_config* c, int64_t* numel);
  * model's own [S, S] tensor with -1e9 above the diagonal (nn:763-771). */
 int vo_gpt_step(const vo_gpt_config* c, const float* const* params, const float* ids,
                 const float* targets, float* loss, float* const* grads, char* err, size_t errlen);
+
+/* `.ve` weight checkpoint (crates/vearo/src/checkpoint.rs:9-91), host tensors. */
+int vo_checkpoint_save(const char* path, int n, const float* const* data, const vo_layout* layouts, char* err,
+                       size_t errlen);
+int vo_checkpoint_load(const char* path, int n, float* const* data, const vo_layout* layouts, char* err,
+                       size_t errlen);
 
 #ifdef __cplusplus
 }

@@ -96,6 +96,39 @@ static std::vector<float> randn(size_t n, unsigned seed, float scale = 1.0f) {
   return v;
 }
 
+static void vh_ok(int rc) {
+  if (rc != VH_OK) throw std::runtime_error(std::string("vh call failed: ") + vh_last_error());
+}
+
+static std::vector<unsigned char> file_bytes(const std::string& path) {
+  std::vector<unsigned char> out;
+  if (std::FILE* f = std::fopen(path.c_str(), "rb")) {
+    unsigned char buf[4096];
+    size_t n;
+    while ((n = std::fread(buf, 1, sizeof buf, f)) > 0) out.insert(out.end(), buf, buf + n);
+    std::fclose(f);
+  }
+  return out;
+}
+
+// The device-written file is byte for byte the oracle's save of the same values.
+static void check_file_is_oracle_save(const std::string& path, const std::vector<std::vector<float>>& data,
+                                      const std::vector<std::vector<int64_t>>& dims) {
+  std::vector<const float*> ptrs;
+  std::vector<vo_layout> lays;
+  for (size_t i = 0; i < data.size(); ++i) {
+    ptrs.push_back(data[i].data());
+    lays.push_back(contig(dims[i]));
+  }
+  const std::string opath = path + ".oracle";
+  char err[256];
+  CHECK(vo_checkpoint_save(opath.c_str(), (int)data.size(), ptrs.data(), lays.data(), err, sizeof err) == VO_OK,
+        "oracle save");
+  const std::vector<unsigned char> a = file_bytes(path), b = file_bytes(opath);
+  std::remove(opath.c_str());
+  CHECK(!a.empty() && a == b, "device checkpoint file equals the oracle's");
+}
+
 int main() {
   init(0);
 
@@ -374,6 +407,37 @@ int main() {
     CHECK(z.shape() == (Shape{0, 6}) && z.to_vec_f32().empty(), "empty add");
     auto [gx, gw, gb] = x.layernorm_backward(Tensor::from_f32({1, 1, 1, 1}, Shape{4}), Tensor::zeros(Shape{4}), x, 1e-5f);
     CHECK(gw.to_vec_f32() == std::vector<float>(4, 0.0f), "empty layernorm backward gives zero dgamma");
+  });
+
+  run("checkpoint_save_load", [] {
+    // crates/vearo/src/checkpoint.rs:97-120 on device tensors.
+    Tensor t1 = Tensor::from_f32({1.0f, 2.0f, 3.0f, 4.0f}, Shape{2, 2});
+    Tensor t2 = Tensor::from_f32({-0.5f, 0.5f}, Shape{2});
+    const std::vector<Tensor> params{t1, t2};
+    const std::string path = "/tmp/vearo_hip_model_checkpoint.ve";
+    save_checkpoint(params, path);
+    check_file_is_oracle_save(path, {{1.0f, 2.0f, 3.0f, 4.0f}, {-0.5f, 0.5f}}, {{2, 2}, {2}});
+    vh_ok(vh_h2d(t1.data(), std::vector<float>(4, 0.0f).data(), 16));
+    vh_ok(vh_h2d(t2.data(), std::vector<float>(2, 0.0f).data(), 8));
+    load_checkpoint(params, path);
+    CHECK(t1.to_vec_f32() == (std::vector<float>{1.0f, 2.0f, 3.0f, 4.0f}), "t1 restored");
+    CHECK(t2.to_vec_f32() == (std::vector<float>{-0.5f, 0.5f}), "t2 restored");
+    // The reference's asserts (checkpoint.rs:50-54, 64-68; tensor.rs:817-820).
+    expect_panic([&] { load_checkpoint({t1}, path); },
+                 "Checkpoint tensor count does not match model parameter count");
+    expect_panic([&] { load_checkpoint({t2, t1}, path); }, "Checkpoint shape does not match parameter shape");
+    expect_panic([&] { load_checkpoint({t1.transpose(0, 1), t2}, path); },
+                 "copy_from_slice requires contiguous tensor");
+    Tensor sq = Tensor::from_f32({1.0f, 2.0f, 3.0f, 4.0f}, Shape{2, 2});
+    expect_panic([&] { save_checkpoint({sq.transpose(0, 1)}, path + ".t"); }, "to_vec_f32 requires contiguous tensor");
+    bool io = false;
+    try {
+      load_checkpoint(params, "/tmp/vearo_hip_no_such_dir/none.ve");
+    } catch (const IoError&) {
+      io = true;
+    }
+    CHECK(io, "a missing file is an io error, not a panic");
+    std::remove(path.c_str());
   });
 
   run("memory_regression", [] {

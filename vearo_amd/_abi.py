@@ -21,6 +21,7 @@ VH_ERR_NOT_INIT = 3
 VH_ERR_DEVICE_PANIC = 4
 VH_ERR_UNSUPPORTED = 5
 VH_ERR_OOM = 6
+VH_ERR_IO = 7
 MAX_RANK = 8
 
 OP_ADD, OP_SUB, OP_MUL, OP_DIV = 0, 1, 2, 3
@@ -158,6 +159,8 @@ SIGNATURES = {
         c_int,
         [fp, fp, fp, fp, c_int64, c_int32, c_float, c_float, c_float, c_float, c_float, c_void_p],
     ),
+    "vh_checkpoint_save": (c_int, [ctypes.c_char_p, c_int32, POINTER(c_void_p), POINTER(VhLayout), c_void_p]),
+    "vh_checkpoint_load": (c_int, [ctypes.c_char_p, c_int32, POINTER(c_void_p), POINTER(VhLayout), c_void_p]),
 }
 
 

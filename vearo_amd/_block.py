@@ -43,6 +43,8 @@ def _load():
         "vb_gpt_adamw": (c_int, [H, c_float, c_float, c_float, c_float, c_float]),
         "vb_gpt_train_step": (c_int, [H, c_float, c_float, c_float, c_float, c_float]),
         "vb_last_error": (ctypes.c_char_p, []),
+        "vb_gpt_save": (c_int, [H, ctypes.c_char_p]),
+        "vb_gpt_load": (c_int, [H, ctypes.c_char_p]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -117,6 +119,14 @@ class Gpt:
 
     def train_step(self, lr=0.02, beta1=0.9, beta2=0.95, eps=1e-8, wd=0.01) -> None:
         check(lib.vb_gpt_train_step(self.h, lr, beta1, beta2, eps, wd))
+
+    def save(self, path) -> None:
+        """The parameters as a `.ve` checkpoint (checkpoint.rs:9-33)."""
+        check(lib.vb_gpt_save(self.h, os.fsencode(path)))
+
+    def load(self, path) -> None:
+        """Parameters from a `.ve` checkpoint (checkpoint.rs:40-91)."""
+        check(lib.vb_gpt_load(self.h, os.fsencode(path)))
 
     def close(self) -> None:
         if self.h is not None:

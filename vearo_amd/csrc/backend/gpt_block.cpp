@@ -363,6 +363,56 @@ int vb_gpt_adamw(vb_gpt* g, float lr, float beta1, float beta2, float eps, float
   return VH_OK;
 }
 
+namespace {
+// Parameter i's layout in SimpleGPT::parameters() order (nn:797-807).
+vh_layout param_layout(const vb_gpt_config& c, int i) {
+  const int64_t D = c.D;
+  int64_t r = D, k = 0;  // [r, k]; k == 0: rank 1 [r]
+  switch (i) {
+    case 0: case 20: r = c.V; k = D; break;
+    case 1: r = c.P; k = D; break;
+    case 4: case 6: case 8: case 10: k = D; break;
+    case 14: r = c.F; k = D; break;
+    case 15: r = c.F; break;
+    case 16: k = c.F; break;
+    default: break;
+  }
+  vh_layout l{};
+  l.rank = k ? 2 : 1;
+  l.dims[0] = r;
+  l.strides[0] = k ? k : 1;
+  if (k) {
+    l.dims[1] = k;
+    l.strides[1] = 1;
+  }
+  return l;
+}
+}  // namespace
+
+int vb_gpt_save(vb_gpt* g, const char* path) {
+  if (!g) return vb_fail(VH_ERR_INVALID, "vb_gpt_save: null handle");
+  const float* ptrs[VB_GPT_NPARAMS];
+  vh_layout lays[VB_GPT_NPARAMS];
+  for (int i = 0; i < VB_GPT_NPARAMS; ++i) {
+    ptrs[i] = g->p(i);
+    lays[i] = param_layout(g->c, i);
+  }
+  VB(vh_checkpoint_save(path, VB_GPT_NPARAMS, ptrs, lays, nullptr));
+  return VH_OK;
+}
+
+int vb_gpt_load(vb_gpt* g, const char* path) {
+  if (!g) return vb_fail(VH_ERR_INVALID, "vb_gpt_load: null handle");
+  float* ptrs[VB_GPT_NPARAMS];
+  vh_layout lays[VB_GPT_NPARAMS];
+  for (int i = 0; i < VB_GPT_NPARAMS; ++i) {
+    ptrs[i] = g->p(i);
+    lays[i] = param_layout(g->c, i);
+  }
+  VB(vh_checkpoint_load(path, VB_GPT_NPARAMS, ptrs, lays, nullptr));
+  return VH_OK;
+}
+
 int vb_gpt_train_step(vb_gpt* g, float lr, float beta1, float beta2, float eps, float weight_decay) {
   int rc = vb_gpt_forward_backward(g, 1);
   if (rc != VH_OK) return rc;

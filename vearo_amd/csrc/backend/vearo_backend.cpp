@@ -551,6 +551,38 @@ Tensor softmax_backward_fused(const Tensor& x, const Tensor& grad_out) {
   return out;
 }
 
+namespace {
+// The checkpoint entries report the reference's panics as VH_ERR_INVALID with
+// the panic text, and its io::Errors as VH_ERR_IO.
+void check_checkpoint(int rc) {
+  if (rc == VH_OK) return;
+  const std::string msg = vh_last_error();
+  if (rc == VH_ERR_IO) throw IoError(msg);
+  if (rc == VH_ERR_INVALID) throw Panic(msg);
+  check(rc);
+}
+}  // namespace
+
+void save_checkpoint(const std::vector<Tensor>& params, const std::string& path) {
+  std::vector<const float*> ptrs;
+  std::vector<vh_layout> lays;
+  for (const Tensor& t : params) {
+    ptrs.push_back(t.data());
+    lays.push_back(layout_of(t));
+  }
+  check_checkpoint(vh_checkpoint_save(path.c_str(), (int32_t)params.size(), ptrs.data(), lays.data(), nullptr));
+}
+
+void load_checkpoint(const std::vector<Tensor>& params, const std::string& path) {
+  std::vector<float*> ptrs;
+  std::vector<vh_layout> lays;
+  for (Tensor t : params) {  // a handle copy shares the storage it writes
+    ptrs.push_back(t.data());
+    lays.push_back(layout_of(t));
+  }
+  check_checkpoint(vh_checkpoint_load(path.c_str(), (int32_t)params.size(), ptrs.data(), lays.data(), nullptr));
+}
+
 Tensor gelu_backward_fused(const Tensor& x, const Tensor& grad_out) {
   panic_if(x.shape() != grad_out.shape(), "Shapes are not broadcastable");
   Tensor out = Tensor::empty(x.shape(), x.device());

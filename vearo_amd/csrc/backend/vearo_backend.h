@@ -28,6 +28,12 @@ struct Panic : std::runtime_error {
   using std::runtime_error::runtime_error;
 };
 
+// An std::io::Error the reference would return (a file that cannot be
+// created, opened, read or written, or ends early).
+struct IoError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
 // Device with the backend slot the reference reserves for a third backend
 // (device.rs:1-5: 0 = CPU, 1 = CUDA, 2/3 reserved).
 struct Device {
@@ -171,5 +177,11 @@ Tensor softmax_backward_arm(const Tensor& x, const Tensor& grad_out, size_t dim)
 Tensor softmax_backward_fused(const Tensor& x, const Tensor& grad_out);
 // Gelu arm with the mask built on the device: grad_out * gelu'(x).
 Tensor gelu_backward_fused(const Tensor& x, const Tensor& grad_out);
+
+// vearo::checkpoint (crates/vearo/src/checkpoint.rs:9-91) for device tensors:
+// the same `.ve` file, the same panics (Panic) and io errors (IoError).
+// load_checkpoint writes into the tensors' storage, as copy_from_slice does.
+void save_checkpoint(const std::vector<Tensor>& params, const std::string& path);
+void load_checkpoint(const std::vector<Tensor>& params, const std::string& path);
 
 }  // namespace vearo_hip

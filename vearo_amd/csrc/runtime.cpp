@@ -20,6 +20,7 @@
 
 #include "../../include/vearo_hip.h"
 #include "vh_kargs.h"
+#include "rt_internal.h"
 
 extern "C" const unsigned char vh_code_object_start[];
 extern "C" const unsigned char vh_code_object_end[];
@@ -359,6 +360,12 @@ bool is_contig(const vh_layout* l) {
 }
 
 }  // namespace
+
+namespace vh_rt {
+int fail(int code, const std::string& msg) { return ::fail(code, msg); }
+int require_init() { return ::require_init(); }
+hipStream_t stream_of(void* s) { return S(s); }
+}  // namespace vh_rt
 
 // ===================================================================== ABI ==
 extern "C" {
