@@ -360,9 +360,84 @@ def wl_gpt2_block(vh):
     return ops, info, cpu, (g, A, W, C, d), None
 
 
+PEAK_PCIE_GBPS = 64.0  # MI355X host link, PCIe 5.0 x16, one direction
+
+
+def run_checkpoint(args, vh):
+    """`.ve` checkpoint save + load (crates/vearo/src/checkpoint.rs:9-91) of
+    the cfg[4] parameter set (SimpleGPT, 21 tensors, 85,070,592 floats) from
+    and to device memory, through vb_gpt_save / vb_gpt_load. Both directions
+    are synchronous calls: wall-clock time, file written to TMPDIR, then read.
+    The oracle's save/load of the same host arrays is the CPU baseline."""
+    import tempfile
+    from vearo_amd import _block
+    cfg = (16, 1024, 768, 12, 3072, 50257, 1024)
+    g = _block.Gpt(_block.GptConfig(*cfg))
+    r = np.random.default_rng(SEED + 4)
+    params = [r.standard_normal(sh, dtype=np.float32) * np.float32(0.02) for sh in g.shapes]
+    g.set_params(params)
+    vh.sync()
+    d = tempfile.mkdtemp(prefix="vearo_ckpt_")
+    path = os.path.join(d, "gpt.ve")
+    try:
+        for _ in range(max(args.warmup, 1)):
+            g.save(path)
+            g.load(path)
+        nbytes = os.path.getsize(path)
+        ts, tl = [], []
+        for _ in range(args.steps):
+            t0 = time.perf_counter()
+            g.save(path)
+            t1 = time.perf_counter()
+            g.load(path)
+            t2 = time.perf_counter()
+            ts.append(t1 - t0)
+            tl.append(t2 - t1)
+        back = g.params()
+        assert all(a.tobytes() == b.tobytes() for a, b in zip(back, params)), "checkpoint round trip changed bits"
+        cpu_res = None
+        if not args.no_cpu:
+            import oracle
+            cpath = os.path.join(d, "oracle.ve")
+            arrays = [p.copy() for p in params]
+            t0 = time.perf_counter()
+            oracle.checkpoint_save(cpath, params)
+            t1 = time.perf_counter()
+            oracle.checkpoint_load(cpath, arrays)
+            t2 = time.perf_counter()
+            os.remove(cpath)
+            cpu_res = {"value": round(2 * nbytes / (t2 - t0) / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                       "sample": f"one save ({t1 - t0:.2f} s) and one load ({t2 - t1:.2f} s) of the same "
+                                 f"{nbytes} B file from host arrays, one value per stdio call as the reference's "
+                                 f"BufWriter/BufReader loop does"}
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+        os.rmdir(d)
+        g.close()
+    save_s, load_s = sum(ts) / len(ts), sum(tl) / len(tl)
+    value = 2 * nbytes / (save_s + load_s) / 1e9
+    kernels = {"save": {"avg_ms": round(save_s * 1e3, 2), "bytes": nbytes, "gbps": round(nbytes / save_s / 1e9, 2)},
+               "load": {"avg_ms": round(load_s * 1e3, 2), "bytes": nbytes, "gbps": round(nbytes / load_s / 1e9, 2)}}
+    dom = max(kernels, key=lambda k: kernels[k]["avg_ms"])
+    res = {
+        "metric": "checkpoint save+load GB/s (cfg[4] parameters as a .ve file)", "value": round(value, 2),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round((save_s + load_s) * 1e3, 2), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (weights ~N(0,0.02))",
+        "config": {"workload": "vb_gpt_save + vb_gpt_load of SimpleGPT cfg[4] (85,070,592 floats, "
+                               f"{nbytes} B file in TMPDIR)", "bytes_per_step": 2 * nbytes},
+        "kernels": kernels,
+        "roofline": {"bound": "pcie", "kernel": dom, "achieved": kernels[dom]["gbps"], "peak": PEAK_PCIE_GBPS,
+                     "unit": "GB/s", "frac": round(kernels[dom]["gbps"] / PEAK_PCIE_GBPS, 4), "traffic": None},
+        "cpu_baseline": cpu_res,
+    }
+    print(json.dumps(res), flush=True)
+
+
 WORKLOADS = {"ln_softmax": wl_ln_softmax, "gpt2_block": wl_gpt2_block, "layernorm_cfg0": wl_layernorm_cfg0, "gelu_bias": wl_gelu_bias,
              "embedding_uniform": wl_embedding_uniform, "embedding_zipf": wl_embedding_zipf,
-             "cross_entropy": wl_cross_entropy}
+             "cross_entropy": wl_cross_entropy, "checkpoint": run_checkpoint}
 
 
 def report_step_ms(args, vh, hip, stream, ops, info, cpu, per, wall, K):
@@ -440,6 +515,9 @@ def main():
                           "copy_gbps": round(4 * 2 * nb / (ms / 1e3) / 1e9, 1)}), flush=True)
         return
 
+    if args.workload == "checkpoint":
+        run_checkpoint(args, vh)
+        return
     ops, info, cpu, keep, traffic_file = WORKLOADS[args.workload](vh)
     vh.sync()
     names = [o[0] for o in ops]
