@@ -119,16 +119,20 @@ extern "C" __global__ void __launch_bounds__(256) vh_emb_rows_v1(EmbSegArgs a) {
 extern "C" __global__ void __launch_bounds__(256) vh_emb_rows_v4(EmbSegArgs a) { emb_rows_impl<4>(a); }
 
 // Cross-entropy
-#define XE_CFG(M) M(1) M(2) M(4) M(8) M(16) M(24) M(32) M(40) M(48) M(50) M(56) M(64)
-#define K_XE(N)                                                                   \
-  extern "C" __global__ void __launch_bounds__(1024) vh_xent_fwd_n##N(XentArgs a) { \
-    xent_cached_impl<N, 0>(a);                                                \
-  }                                                                               \
-  extern "C" __global__ void __launch_bounds__(1024) vh_xent_bwd_n##N(XentArgs a) { \
-    xent_cached_impl<N, 1>(a);                                                    \
-  }                                                                               \
-  extern "C" __global__ void __launch_bounds__(1024) vh_xent_fb_n##N(XentArgs a) { \
-    xent_cached_impl<N, 2>(a);                                                 \
+// Up to NV = 104 (V <= 53,248, the GPT-2 vocabulary among them) the kernels
+// are held to 128 VGPRs: 4 waves per SIMD, two 512-thread rows per CU, one's
+// HBM traffic overlapping the other's reductions.
+#define XE_CFG(M) M(8, 4) M(16, 4) M(24, 4) M(32, 4) M(40, 4) M(48, 4) M(56, 4) M(64, 4) M(72, 4) M(80, 4) \
+  M(88, 4) M(96, 4) M(104, 4) M(112, 1) M(120, 1) M(128, 1)
+#define K_XE(N, W)                                                                       \
+  extern "C" __global__ void __launch_bounds__(XE_TEAM, W) vh_xent_fwd_n##N(XentArgs a) { \
+    xent_cached_impl<N, 0>(a);                                                           \
+  }                                                                                      \
+  extern "C" __global__ void __launch_bounds__(XE_TEAM, W) vh_xent_bwd_n##N(XentArgs a) { \
+    xent_cached_impl<N, 1>(a);                                                           \
+  }                                                                                      \
+  extern "C" __global__ void __launch_bounds__(XE_TEAM, W) vh_xent_fb_n##N(XentArgs a) {  \
+    xent_cached_impl<N, 2>(a);                                                           \
   }
 XE_CFG(K_XE)
 extern "C" __global__ void __launch_bounds__(1024) vh_xent_fwd_stream(XentArgs a) { xent_stream_impl<false>(a); }

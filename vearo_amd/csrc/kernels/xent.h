@@ -6,9 +6,9 @@
 // cross_entropy_backward (lib.rs:1053-1127): dl = go * (p - 1[c == t]) / B with
 // p = exp(l - max) / sum. Targets are f32 class ids, rounded like Rust's round().
 //
-// Layout: logits / dlogits [B, V] with row stride ld (>= V), targets [B], one 1024-thread
-// workgroup (16 waves) per row. When V <= 1024*NV the row is held in VGPRs and
-// read from HBM once (fwd 4 B/elem read; bwd 4 B read + 4 B write). Longer rows
+// Layout: logits / dlogits [B, V] with row stride ld (>= V), targets [B], one
+// 512-thread workgroup (8 waves) per row. When V <= 512*128 the row is held in
+// VGPRs and read from HBM once (fwd 4 B/elem read; bwd 4 B read + 4 B write). Longer rows
 // take the streaming variant: one online max/sum pass, plus a write pass in bwd.
 // The scalar per-row log_softmax values are reduced by xent_reduce in a fixed
 // order, so the loss is deterministic. MODE 2 does forward and backward in one
@@ -33,6 +33,13 @@ VH_DEV int32_t xent_target(const XentArgs& a, int64_t row) {
 // out-of-range stores are dropped.
 #define VH_BUF_WORD3 0x00020000
 
+// Row-cached kernels: a team of XE_TEAM threads per row, each holding NV
+// values in VGPRs (two rows in flight per CU at the GPT-2 vocabulary). Units
+// 0 .. NV - XE_MASK - 1 lie inside the row for every thread (the host picks NV
+// with NV - XE_MASK < ceil(V / XE_TEAM) <= NV); only the last XE_MASK are
+// masked (-inf, so exp gives 0).
+#define XE_TEAM 512
+#define XE_MASK 8
 template <int NV, int MODE>  // 0 forward, 1 backward, 2 both
 VH_DEV void xent_cached_impl(const XentArgs& a) {
   __shared__ float red[16];
@@ -40,8 +47,8 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
   const int V = a.V;
   const float* lr = a.logits + row * a.ld;
   // One buffer resource per row: base and bound live in SGPRs, the unit offset
-  // k*4096 goes in the scalar offset field, so the cached row costs one VGPR
-  // per float and no per-load address registers.
+  // k * XE_TEAM * 4 goes in the scalar offset field, so the cached row costs
+  // one VGPR per float and no per-load address registers.
   const __amdgpu_buffer_rsrc_t rin =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(lr), 0, V * 4, VH_BUF_WORD3);
   const int voff = threadIdx.x * 4;
@@ -49,22 +56,21 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
   float m = -INFINITY;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
-    const int c = threadIdx.x + k * 1024;
     // The builtin returns the raw 32 bits: reinterpret, do not convert.
-    const float x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rin, voff, k * 4096, 0));
-    v[k] = c < V ? x : -INFINITY;
+    const float x =
+        __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rin, voff, k * XE_TEAM * 4, 0));
+    v[k] = (k < NV - XE_MASK || (int)threadIdx.x + k * XE_TEAM < V) ? x : -INFINITY;
     if (v[k] > m) m = v[k];
   }
-  m = team_max<1024>(m, red);
+  m = team_max<XE_TEAM>(m, red);
   float s = 0.0f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
-    const int c = threadIdx.x + k * 1024;
-    const float e = c < V ? expf(v[k] - m) : 0.0f;
+    const float e = expf(v[k] - m);
     v[k] = e;
     s += e;
   }
-  s = team_sum<1024>(s, red);
+  s = team_sum<XE_TEAM>(s, red);
   const int32_t t = xent_target(a, row);
   if constexpr (MODE != 1) {
     if (threadIdx.x == 0) (MODE == 0 ? a.out : a.row_loss)[row] = t >= 0 ? lr[t] - m - logf(s) : 0.0f;
@@ -76,12 +82,12 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
         __builtin_amdgcn_make_buffer_rsrc(a.out + row * a.ld, 0, V * 4, VH_BUF_WORD3);
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const int c = threadIdx.x + k * 1024;
+      const int c = threadIdx.x + k * XE_TEAM;
       const float p = v[k] / s;
       const float ind = c == t ? 1.0f : 0.0f;
       // Units past the row end fall outside the resource and are dropped.
       const float g = go * (p - ind) / Bf;
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, g), rout, voff, k * 4096, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, g), rout, voff, k * XE_TEAM * 4, 0);
     }
   }
 }

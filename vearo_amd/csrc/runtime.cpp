@@ -785,13 +785,21 @@ int vh_embedding_bwd(const float* ids, const float* dy, float* dW, int64_t n, in
 
 // --------------------------------------------------------- cross-entropy --
 
-static const int kXE[] = {1, 2, 4, 8, 16, 24, 32, 40, 48, 50, 56, 64};
+static const int kXE[] = {8, 16, 24, 32, 40, 48, 56, 64, 72, 80, 88, 96, 104, 112, 120, 128};
+constexpr int kXeTeam = 512;  // threads per row of the row-cached kernels
+constexpr int kXeMask = 8;    // trailing units they mask
 
+// The row-cached kernels hold NV values per thread of a 512-thread team and
+// mask only their last 8 units, so NV - 8 < ceil(V / 512) <= NV; longer rows
+// take the streaming kernel (1024 threads).
 static std::string xent_kernel(const char* dir, int64_t V) {
-  const int64_t need = cdiv(V, 1024);
+  const int64_t need = cdiv(V, kXeTeam);
   for (int v : kXE)
-    if (v >= need) return std::string("vh_xent_") + dir + "_n" + std::to_string(v);
+    if (v >= need && v - kXeMask < need) return std::string("vh_xent_") + dir + "_n" + std::to_string(v);
   return std::string("vh_xent_") + dir + "_stream";
+}
+static unsigned xent_threads(const std::string& kernel) {
+  return kernel.compare(kernel.size() - 7, 7, "_stream") == 0 ? 1024u : (unsigned)kXeTeam;
 }
 
 size_t vh_cross_entropy_fwd_scratch_bytes(int64_t B) {
@@ -810,7 +818,7 @@ int vh_cross_entropy_fwd_ld(const float* logits, int64_t ld, const float* target
   Scratch sc;
   VH_TRY(sc.get(scratch, scratch_bytes, vh_cross_entropy_fwd_scratch_bytes(B)));
   XentArgs a{logits, targets, nullptr, static_cast<float*>(sc.p), nullptr, g_rt.err, B, ld, (int32_t)V};
-  VH_TRY(launch(xent_kernel("fwd", V), (unsigned)B, 1, 1024, 0, s, a));
+  VH_TRY(launch(xent_kernel("fwd", V), (unsigned)B, 1, xent_threads(xent_kernel("fwd", V)), 0, s, a));
   XentReduceArgs r{static_cast<float*>(sc.p), loss, B};
   return launch("vh_xent_reduce", 1, 1, 1024, 0, s, r);
 }
@@ -830,7 +838,7 @@ int vh_cross_entropy_bwd_ld(const float* logits, int64_t ld, const float* target
     return fail(VH_ERR_INVALID, "vh_cross_entropy_bwd: null pointer");
   if (V > INT32_MAX || B > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_cross_entropy_bwd: size exceeds int32");
   XentArgs a{logits, targets, grad_out, dlogits, nullptr, g_rt.err, B, ld, (int32_t)V};
-  return launch(xent_kernel("bwd", V), (unsigned)B, 1, 1024, 0, S(stream), a);
+  return launch(xent_kernel("bwd", V), (unsigned)B, 1, xent_threads(xent_kernel("bwd", V)), 0, S(stream), a);
 }
 
 int vh_cross_entropy_fwd_bwd_ld(const float* logits, int64_t ld, const float* targets, const float* grad_out,
@@ -854,7 +862,7 @@ int vh_cross_entropy_fwd_bwd_ld(const float* logits, int64_t ld, const float* ta
   VH_TRY(sc.get(scratch, scratch_bytes, vh_cross_entropy_fwd_scratch_bytes(B)));
   float* rows = static_cast<float*>(sc.p);
   XentArgs a{logits, targets, grad_out, dlogits, rows, g_rt.err, B, ld, (int32_t)V};
-  VH_TRY(launch(xent_kernel("fb", V), (unsigned)B, 1, 1024, 0, s, a));
+  VH_TRY(launch(xent_kernel("fb", V), (unsigned)B, 1, xent_threads(xent_kernel("fb", V)), 0, s, a));
   XentReduceArgs r{rows, loss, B};
   return launch("vh_xent_reduce", 1, 1, 1024, 0, s, r);
 }
