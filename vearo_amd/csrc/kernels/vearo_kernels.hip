@@ -119,11 +119,11 @@ extern "C" __global__ void __launch_bounds__(256) vh_emb_rows_v1(EmbSegArgs a) {
 extern "C" __global__ void __launch_bounds__(256) vh_emb_rows_v4(EmbSegArgs a) { emb_rows_impl<4>(a); }
 
 // Cross-entropy
-// Up to NV = 104 (V <= 53,248, the GPT-2 vocabulary among them) the kernels
-// are held to 128 VGPRs: 4 waves per SIMD, two 512-thread rows per CU, one's
-// HBM traffic overlapping the other's reductions.
+// Up to NV = 104 (V <= 53,248) the kernels are held to 128 VGPRs: 4 waves per
+// SIMD, two 512-thread rows per CU, one's HBM traffic overlapping the other's
+// reductions. NV = 99 is the GPT-2 vocabulary (V = 50,257) exactly.
 #define XE_CFG(M) M(8, 4) M(16, 4) M(24, 4) M(32, 4) M(40, 4) M(48, 4) M(56, 4) M(64, 4) M(72, 4) M(80, 4) \
-  M(88, 4) M(96, 4) M(104, 4) M(112, 1) M(120, 1) M(128, 1)
+  M(88, 4) M(96, 4) M(99, 4) M(104, 4) M(112, 1) M(120, 1) M(128, 1)
 #define K_XE(N, W)                                                                       \
   extern "C" __global__ void __launch_bounds__(XE_TEAM, W) vh_xent_fwd_n##N(XentArgs a) { \
     xent_cached_impl<N, 0>(a);                                                           \

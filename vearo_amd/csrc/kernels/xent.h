@@ -57,11 +57,19 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     // The builtin returns the raw 32 bits: reinterpret, do not convert.
-    const float x =
-        __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rin, voff, k * XE_TEAM * 4, 0));
-    v[k] = (k < NV - XE_MASK || (int)threadIdx.x + k * XE_TEAM < V) ? x : -INFINITY;
-    if (v[k] > m) m = v[k];
+    // Unit offset k * 2048 B as (k / 2) * 4096 in the scalar offset plus
+    // (k % 2) * 2048 folded into the instruction's immediate: half as many
+    // scalar constants live across the burst of loads.
+    const float x = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(rin, voff + (k & 1) * XE_TEAM * 4, (k >> 1) * XE_TEAM * 8, 0));
+    // tid < V - k * XE_TEAM: the bound is a scalar, no per-unit index register.
+    v[k] = (k < NV - XE_MASK || (int)threadIdx.x < V - k * XE_TEAM) ? x : -INFINITY;
   }
+  // Every load issued before the max chain starts consuming them.
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+    if (v[k] > m) m = v[k];
   m = team_max<XE_TEAM>(m, red);
   float s = 0.0f;
 #pragma unroll
@@ -72,23 +80,30 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
   }
   s = team_sum<XE_TEAM>(s, red);
   const int32_t t = xent_target(a, row);
-  if constexpr (MODE != 1) {
-    if (threadIdx.x == 0) (MODE == 0 ? a.out : a.row_loss)[row] = t >= 0 ? lr[t] - m - logf(s) : 0.0f;
+  if constexpr (MODE == 0) {
+    if (threadIdx.x == 0) a.out[row] = t >= 0 ? lr[t] - m - logf(s) : 0.0f;
   }
   if constexpr (MODE != 0) {
+    __builtin_amdgcn_sched_barrier(0);
     const float go = *a.grad_out;
     const float Bf = (float)a.B;
     const __amdgpu_buffer_rsrc_t rout =
         __builtin_amdgcn_make_buffer_rsrc(a.out + row * a.ld, 0, V * 4, VH_BUF_WORD3);
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const int c = threadIdx.x + k * XE_TEAM;
       const float p = v[k] / s;
-      const float ind = c == t ? 1.0f : 0.0f;
+      const float ind = (int)threadIdx.x == t - k * XE_TEAM ? 1.0f : 0.0f;
       // Units past the row end fall outside the resource and are dropped.
       const float g = go * (p - ind) / Bf;
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, g), rout, voff, k * XE_TEAM * 4, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, g), rout, voff + (k & 1) * XE_TEAM * 4,
+                                            (k >> 1) * XE_TEAM * 8, 0);
+      // At most 2 elements' correctly rounded divisions in flight: their
+      // temporaries then fit beside the cached row without spilling.
+      if (k & 1) __builtin_amdgcn_sched_barrier(0);
     }
+  }
+  if constexpr (MODE == 2) {  // after the row's registers are free
+    if (threadIdx.x == 0) a.row_loss[row] = t >= 0 ? lr[t] - m - logf(s) : 0.0f;
   }
 }
 

@@ -785,7 +785,7 @@ int vh_embedding_bwd(const float* ids, const float* dy, float* dW, int64_t n, in
 
 // --------------------------------------------------------- cross-entropy --
 
-static const int kXE[] = {8, 16, 24, 32, 40, 48, 56, 64, 72, 80, 88, 96, 104, 112, 120, 128};
+static const int kXE[] = {8, 16, 24, 32, 40, 48, 56, 64, 72, 80, 88, 96, 99, 104, 112, 120, 128};
 constexpr int kXeTeam = 512;  // threads per row of the row-cached kernels
 constexpr int kXeMask = 8;    // trailing units they mask
 
