@@ -41,11 +41,18 @@
 
 typedef float vh_f32x16 __attribute__((ext_vector_type(16)));
 
+template <bool B>
+struct GmFlag {
+  static constexpr bool value = B;
+};
+
 // The [NR rows x 32 k] tile (NR = 128 or 64) whose element (r, k) is at
 //   KC:  base[(r0 + r) * ld + k0 + k]      !KC: base[(k0 + k) * ld + r0 + r]
 // into NR/8 staging registers per thread; rows >= R or k >= K read as 0.
 // VEC requires 16-byte aligned base and ld, and K (KC) or R (!KC) % 4 == 0.
-template <bool KC, bool VEC, int NR>
+// CHECK = false: the caller knows the whole tile is inside (no tests, no
+// branches: the loads can be scheduled among the matrix-core products).
+template <bool KC, bool VEC, int NR, bool CHECK = true>
 VH_DEV void gm_load(const float* base, int64_t ld, int64_t r0, int64_t R, int64_t k0, int64_t K, int tid,
                     float (&st)[NR / 8]) {
   if constexpr (KC && VEC) {
@@ -53,7 +60,7 @@ VH_DEV void gm_load(const float* base, int64_t ld, int64_t r0, int64_t R, int64_
     for (int i = 0; i < NR / 32; ++i) {
       const int r = (tid >> 3) + 32 * i, k = (tid & 7) * 4;
       vh_f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (r0 + r < R && k0 + k < K) v = *reinterpret_cast<const vh_f4*>(base + (r0 + r) * ld + k0 + k);
+      if (!CHECK || (r0 + r < R && k0 + k < K)) v = *reinterpret_cast<const vh_f4*>(base + (r0 + r) * ld + k0 + k);
 #pragma unroll
       for (int e = 0; e < 4; ++e) st[4 * i + e] = v[e];
     }
@@ -61,7 +68,7 @@ VH_DEV void gm_load(const float* base, int64_t ld, int64_t r0, int64_t R, int64_
 #pragma unroll
     for (int i = 0; i < NR / 8; ++i) {
       const int r = (tid >> 5) + 8 * i, k = tid & 31;
-      st[i] = (r0 + r < R && k0 + k < K) ? base[(r0 + r) * ld + k0 + k] : 0.0f;
+      st[i] = (!CHECK || (r0 + r < R && k0 + k < K)) ? base[(r0 + r) * ld + k0 + k] : 0.0f;
     }
   } else if constexpr (VEC) {
     constexpr int TPR = NR / 4;  // threads per k row
@@ -69,7 +76,7 @@ VH_DEV void gm_load(const float* base, int64_t ld, int64_t r0, int64_t R, int64_
     for (int i = 0; i < NR / 32; ++i) {
       const int k = tid / TPR + (256 / TPR) * i, r = (tid % TPR) * 4;
       vh_f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (k0 + k < K && r0 + r < R) v = *reinterpret_cast<const vh_f4*>(base + (k0 + k) * ld + r0 + r);
+      if (!CHECK || (k0 + k < K && r0 + r < R)) v = *reinterpret_cast<const vh_f4*>(base + (k0 + k) * ld + r0 + r);
 #pragma unroll
       for (int e = 0; e < 4; ++e) st[4 * i + e] = v[e];
     }
@@ -77,7 +84,7 @@ VH_DEV void gm_load(const float* base, int64_t ld, int64_t r0, int64_t R, int64_
 #pragma unroll
     for (int i = 0; i < NR / 8; ++i) {
       const int k = tid / NR + (256 / NR) * i, r = tid % NR;
-      st[i] = (k0 + k < K && r0 + r < R) ? base[(k0 + k) * ld + r0 + r] : 0.0f;
+      st[i] = (!CHECK || (k0 + k < K && r0 + r < R)) ? base[(k0 + k) * ld + r0 + r] : 0.0f;
     }
   }
 }
@@ -179,53 +186,72 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
     gm_store_lds<B_KC, B_VEC, TN>(Bs[0], tid, sb);
     __syncthreads();
   }
-  // Per k tile: the next tile's global loads go out first; then all of this
-  // tile's fragments are read from LDS at once (the products wait only on the
-  // reads they use, which return in order); the next tile is written to the
-  // other LDS buffer (free since the last barrier) between the last group's
+  // Per k tile: the next tile's global loads go out; then all of this tile's
+  // fragments are read from LDS at once (the products wait only on the reads
+  // they use, which return in order); the next tile is written to the other
+  // LDS buffer (free since the last barrier) between the last group's
   // products. On the last tile that write goes to a buffer nothing reads again
-  // (it keeps the loop body one block, so the order below holds).
+  // (the loop body stays one block, so the order below holds).
+  // A tile entirely inside A, B and K (all but the edge tiles) runs a copy of
+  // the loop without bounds tests or branches around its loads; on the last
+  // k tile they fetch that tile again rather than branch.
   constexpr int RD = 4 * ((A_KC ? 2 : 8) + NTW * (B_KC ? 1 : 4));              // LDS reads per tile
   constexpr int WR = (A_VEC ? GM_TM / 32 : GM_TM / 8) + (B_VEC ? TN / 32 : TN / 8);  // LDS writes per tile
+  constexpr int VM = (A_VEC ? GM_TM / 32 : GM_TM / 8) + (B_VEC ? TN / 32 : TN / 8);  // global loads per tile
   constexpr int MF = 8 * NTW;                                                   // products per 4-k group
-  for (int64_t k0 = kb; k0 < ke; k0 += GM_TK) {
-    const bool more = k0 + GM_TK < ke;
-    if (more) {
-      gm_load<A_KC, A_VEC, GM_TM>(A, a.lda, m0, a.M, k0 + GM_TK, a.K, tid, sa);
-      gm_load<B_KC, B_VEC, TN>(B, a.ldb, n0, a.N, k0 + GM_TK, a.K, tid, sb);
-    }
-    vh_f4 fa[4][2], fb[4][NTW];
+  auto main_loop = [&](auto unchecked) {
+    constexpr bool CHECK = !decltype(unchecked)::value;
+    for (int64_t k0 = kb; k0 < ke; k0 += GM_TK) {
+      const bool more = k0 + GM_TK < ke;
+      if constexpr (CHECK) {
+        if (more) {
+          gm_load<A_KC, A_VEC, GM_TM>(A, a.lda, m0, a.M, k0 + GM_TK, a.K, tid, sa);
+          gm_load<B_KC, B_VEC, TN>(B, a.ldb, n0, a.N, k0 + GM_TK, a.K, tid, sb);
+        }
+      } else {
+        const int64_t kn = more ? k0 + GM_TK : k0;
+        gm_load<A_KC, A_VEC, GM_TM, false>(A, a.lda, m0, a.M, kn, a.K, tid, sa);
+        gm_load<B_KC, B_VEC, TN, false>(B, a.ldb, n0, a.N, kn, a.K, tid, sb);
+      }
+      vh_f4 fa[4][2], fb[4][NTW];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int kc = h * 16 + 4 * q;
-      fa[q][0] = gm_frag<A_KC>(As[s], wm * 64 + li, kc);
-      fa[q][1] = gm_frag<A_KC>(As[s], wm * 64 + 32 + li, kc);
+      for (int q = 0; q < 4; ++q) {
+        const int kc = h * 16 + 4 * q;
+        fa[q][0] = gm_frag<A_KC>(As[s], wm * 64 + li, kc);
+        fa[q][1] = gm_frag<A_KC>(As[s], wm * 64 + 32 + li, kc);
 #pragma unroll
-      for (int nt = 0; nt < NTW; ++nt) fb[q][nt] = gm_frag<B_KC>(Bs[s], wn * (TN / 2) + nt * 32 + li, kc);
-    }
+        for (int nt = 0; nt < NTW; ++nt) fb[q][nt] = gm_frag<B_KC>(Bs[s], wn * (TN / 2) + nt * 32 + li, kc);
+      }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < 4; ++q) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < 4; ++e) {
 #pragma unroll
-        for (int nt = 0; nt < NTW; ++nt) {
-          acc[0][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][0][e], fb[q][nt][e], acc[0][nt], 0, 0, 0);
-          acc[1][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][1][e], fb[q][nt][e], acc[1][nt], 0, 0, 0);
+          for (int nt = 0; nt < NTW; ++nt) {
+            acc[0][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][0][e], fb[q][nt][e], acc[0][nt], 0, 0, 0);
+            acc[1][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][1][e], fb[q][nt][e], acc[1][nt], 0, 0, 0);
+          }
         }
       }
-    }
-    gm_store_lds<A_KC, A_VEC, GM_TM>(As[s ^ 1], tid, sa);
-    gm_store_lds<B_KC, B_VEC, TN>(Bs[s ^ 1], tid, sb);
-    __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);      // all fragment reads
-    __builtin_amdgcn_sched_group_barrier(0x008, 3 * MF, 0);  // groups 0-2
+      gm_store_lds<A_KC, A_VEC, GM_TM>(As[s ^ 1], tid, sa);
+      gm_store_lds<B_KC, B_VEC, TN>(Bs[s ^ 1], tid, sb);
+      if constexpr (!CHECK) __builtin_amdgcn_sched_group_barrier(0x020, VM, 0);  // the next tile's loads
+      __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);                        // all fragment reads
+      __builtin_amdgcn_sched_group_barrier(0x008, 3 * MF, 0);                    // groups 0-2
 #pragma unroll
-    for (int i = 0; i < MF; ++i) {                            // group 3 with the writes
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x200, (WR + MF - 1) / MF, 0);
+      for (int i = 0; i < MF; ++i) {  // group 3 with the writes
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, (WR + MF - 1) / MF, 0);
+      }
+      __syncthreads();
+      s ^= 1;
     }
-    __syncthreads();
-    s ^= 1;
-  }
+  };
+  const bool inside = m0 + GM_TM <= a.M && n0 + TN <= a.N && (ke - kb) % GM_TK == 0 && ke <= a.K;
+  if (inside)
+    main_loop(GmFlag<true>{});
+  else
+    main_loop(GmFlag<false>{});
 
   // Epilogue. Accumulator register r of a 32 x 32 tile holds row
   // 8*(r/4) + 4*h + r%4, column li.
