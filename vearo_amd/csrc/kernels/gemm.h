@@ -152,12 +152,25 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
   __shared__ __attribute__((aligned(16))) float Bs[2][GM_STAGE];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   int tm, tn;
-  gm_tile_of(blockIdx.x, gridDim.x, a.tiles_m, a.tiles_n, tm, tn);
+  int64_t bat = blockIdx.y;  // batch index (both batch dims)
+  if (a.causal >= 2 && a.ksplit <= 1) {
+    // The k range grows with the tile row (k <= m) or shrinks (k >= m): deal
+    // the workgroups longest first across all batches, so the last ones to
+    // start are short (the launch order is x fastest, then y).
+    const int64_t lin = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+    const int64_t rank = lin / gridDim.y;
+    bat = lin % gridDim.y;
+    const int row = (int)(rank / a.tiles_n);
+    tm = a.causal == 2 ? a.tiles_m - 1 - row : row;
+    tn = (int)(rank % a.tiles_n);
+  } else {
+    gm_tile_of(blockIdx.x, gridDim.x, a.tiles_m, a.tiles_n, tm, tn);
+  }
   const int64_t m0 = (int64_t)tm * GM_TM, n0 = (int64_t)tn * TN;
   if (a.causal == 1 && n0 > m0 + GM_TM - 1) return;  // the whole tile is masked
 
   const bool split = a.ksplit > 1;
-  const int64_t b1 = split ? 0 : blockIdx.y / a.nb2, b2 = split ? 0 : blockIdx.y % a.nb2;
+  const int64_t b1 = split ? 0 : bat / a.nb2, b2 = split ? 0 : bat % a.nb2;
   const float* A = a.A + b1 * a.sa1 + b2 * a.sa2;
   const float* B = a.B + b1 * a.sb1 + b2 * a.sb2;
   float* C = a.C + b1 * a.sc1 + b2 * a.sc2;
