@@ -326,7 +326,8 @@ def wl_gpt2_block(vh):
     ops = [("train_step", flops, lambda i: _block.lib.vb_gpt_train_step(g.h, 0.02, 0.9, 0.95, 1e-8, 0.01))]
     # The dominant kernel, timed on its own after the timed loop: the lm_head
     # forward GEMM logits[16384, 50257] = lnf[16384, 768] W^T, through the same
-    # vh_gemm path the step uses, on scratch buffers of the same shapes.
+    # vh_gemm path the step uses (a plain product: vh_gemm hands it to
+    # hipBLASLt), on scratch buffers of the same shapes.
     A = vh.DeviceBuffer.from_array(r.standard_normal((B * S, D), dtype=np.float32))
     W = vh.DeviceBuffer.from_array(params[20])
     C = vh.DeviceBuffer(4 * B * S * V)
@@ -459,7 +460,8 @@ def report_step_ms(args, vh, hip, stream, ops, info, cpu, per, wall, K):
     kernels = {name: {"avg_ms": round(step_s * 1e3, 3), "flops": flops,
                       "tflops": round(flops / step_s / 1e12, 2)},
                pname: {"avg_us": round(p_s * 1e6, 1), "flops": pflops, "tflops": round(achieved, 2)}}
-    roofline = {"bound": "mfma", "kernel": pname, "achieved": round(achieved, 2), "peak": PEAK_F32_MFMA_TFLOPS,
+    roofline = {"bound": "mfma", "kernel": pname, "impl": "hipBLASLt f32 (vh_gemm, plain product)",
+                "achieved": round(achieved, 2), "peak": PEAK_F32_MFMA_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_F32_MFMA_TFLOPS, 4), "traffic": None}
     cpu_res = None
     if not args.no_cpu:

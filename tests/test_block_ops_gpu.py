@@ -354,3 +354,37 @@ def test_cross_entropy_row_stride(vh):
     vh.check(vh.lib.vh_cross_entropy_fwd_bwd_ld(L.ptr, ld, T.ptr, GO.ptr, LOSS2.ptr, DL2.ptr, B, V, None, 0, None))
     np.testing.assert_array_equal(fetch(vh, LOSS2, (1,)), fetch(vh, LOSS, (1,)))
     np.testing.assert_array_equal(fetch(vh, DL2, (B, ld)), dl)
+
+
+@pytest.mark.parametrize("akc,bkc", [(True, True), (True, False), (False, False), (False, True)])
+def test_plain_gemm_library_path(vh, akc, bkc):
+    """Large plain products (no batch, causal range, addend or accumulation)
+    run through hipBLASLt: the oracle's matmul within the parity bar at model
+    scale, the f32 error bound against float64 with N(0,1) operands, and the
+    same bits from a second call (determinism), for every operand layout."""
+    M, N, K = 1024, 3000, 768
+    print("plain gemm", akc, bkc, flush=True)
+    r = np.random.default_rng(int(akc) * 2 + int(bkc))
+    a = r.standard_normal((M, K), dtype=np.float32)
+    b = (r.standard_normal((K, N)) * 0.02).astype(np.float32)
+    b1 = r.standard_normal((K, N), dtype=np.float32)
+    # Store A as [M, K] (k-contiguous) or [K, M] (m-contiguous), B as [N, K] or [K, N].
+    A = dev(vh, a if akc else np.ascontiguousarray(a.T))
+    a_sm, a_sk = (K, 1) if akc else (1, M)
+    for bb, name in ((b, "model scale"), (b1, "N(0,1)")):
+        B = dev(vh, np.ascontiguousarray(bb.T) if bkc else bb)
+        b_sk, b_sn = (1, K) if bkc else (N, 1)
+        C, C2 = out(vh, (M, N)), out(vh, (M, N))
+        d = gemm_desc(vh, M, N, K, A.ptr, a_sm, a_sk, B.ptr, b_sk, b_sn, C.ptr, N)
+        vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+        d2 = gemm_desc(vh, M, N, K, A.ptr, a_sm, a_sk, B.ptr, b_sk, b_sn, C2.ptr, N)
+        vh.check(vh.lib.vh_gemm(ctypes.byref(d2), None))
+        got = fetch(vh, C, (M, N))
+        np.testing.assert_array_equal(got, fetch(vh, C2, (M, N)))
+        exact = a.astype(np.float64) @ bb.astype(np.float64)
+        if bb is b:
+            assert_parity(got, O.matmul(a, bb), exact, name=f"plain {akc} {bkc}")
+        else:
+            u = 2.0 ** -24
+            bound = (K * u / (1 - K * u)) * (np.abs(a).astype(np.float64) @ np.abs(bb).astype(np.float64))
+            assert np.all(np.abs(got - exact) <= bound), f"plain {akc} {bkc}: f32 error bound"

@@ -1,0 +1,155 @@
+// blaslt.cpp -- plain f32 products through hipBLASLt.
+//
+// A product with no batch, no causal range, no addend E and no accumulation
+// (the lm_head products, every weight gradient and every input gradient of the
+// block step) is a plain library GEMM; hipBLASLt's gfx950 kernels (128x128x64
+// macro tiles, stream-K) run these shapes faster than the hand-written kernel
+// in kernels/gemm.h, which keeps every product they do not cover (strided
+// batches, causal ranges, fused epilogues). Compute type HIPBLAS_COMPUTE_32F:
+// f32 products and sums, no reduced-precision path.
+//
+// hipBLASLt is column-major: the row-major C[M, N] = A[M, K] B[K, N] is issued
+// as the column-major C^T[N, M] = B^T[N, K] A^T[K, M], each operand transposed
+// or not by which of its dims has the unit stride. Descriptors and the
+// heuristic's algorithm are cached per problem.
+#include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
+
+#include "../../include/vearo_hip.h"
+#include "rt_internal.h"
+
+namespace {
+
+using vh_rt::fail;
+
+constexpr size_t kWorkspace = size_t(64) << 20;  // bytes the algorithms may use
+
+struct Plan {
+  hipblasLtMatmulDesc_t op = nullptr;
+  hipblasLtMatrixLayout_t lx = nullptr, ly = nullptr, lc = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  bool usable = false;  // the heuristic returned an algorithm
+};
+
+using Key = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int, int>;
+
+struct Lib {
+  std::mutex mu;
+  hipblasLtHandle_t handle = nullptr;
+  void* ws = nullptr;
+  std::map<Key, Plan> plans;
+} g_lib;
+
+int status(hipblasStatus_t st, const char* what) {
+  if (st == HIPBLAS_STATUS_SUCCESS) return VH_OK;
+  return fail(VH_ERR_HIP, std::string("hipBLASLt ") + what + " failed: status " + std::to_string((int)st));
+}
+
+#define LT(expr, what)                       \
+  do {                                       \
+    int rc_ = status((expr), what);          \
+    if (rc_ != VH_OK) return rc_;            \
+  } while (0)
+
+void destroy(Plan& p) {
+  if (p.op) hipblasLtMatmulDescDestroy(p.op);
+  if (p.lx) hipblasLtMatrixLayoutDestroy(p.lx);
+  if (p.ly) hipblasLtMatrixLayoutDestroy(p.ly);
+  if (p.lc) hipblasLtMatrixLayoutDestroy(p.lc);
+  p = Plan{};
+}
+
+int make_plan(const Key& k, Plan* out) {
+  const auto [M, N, K, ldx, ldy, ldc, tx, ty] = k;
+  Plan p;
+  // X = B^T: [N, K] as stored (tx = 0) or the transpose of a stored [K, N].
+  // Y = A^T: [K, M] as stored (ty = 0) or the transpose of a stored [M, K].
+  const hipblasOperation_t opx = tx ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+  const hipblasOperation_t opy = ty ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+  LT(hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F), "MatmulDescCreate");
+  LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &opx, sizeof(opx)), "set TRANSA");
+  LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &opy, sizeof(opy)), "set TRANSB");
+  LT(hipblasLtMatrixLayoutCreate(&p.lx, HIP_R_32F, tx ? K : N, tx ? N : K, ldx), "layout X");
+  LT(hipblasLtMatrixLayoutCreate(&p.ly, HIP_R_32F, ty ? M : K, ty ? K : M, ldy), "layout Y");
+  LT(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc), "layout C");
+  hipblasLtMatmulPreference_t pref = nullptr;
+  LT(hipblasLtMatmulPreferenceCreate(&pref), "PreferenceCreate");
+  uint64_t wsb = kWorkspace;
+  int rc = status(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
+                                                         sizeof(wsb)),
+                  "set workspace");
+  hipblasLtMatmulHeuristicResult_t res[1];
+  int found = 0;
+  if (rc == VH_OK) {
+    const hipblasStatus_t st =
+        hipblasLtMatmulAlgoGetHeuristic(g_lib.handle, p.op, p.lx, p.ly, p.lc, p.lc, pref, 1, res, &found);
+    if (st == HIPBLAS_STATUS_SUCCESS && found > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS &&
+        res[0].workspaceSize <= kWorkspace) {
+      p.algo = res[0].algo;
+      p.usable = true;
+    }
+  }
+  hipblasLtMatmulPreferenceDestroy(pref);
+  if (rc != VH_OK) {
+    destroy(p);
+    return rc;
+  }
+  *out = p;
+  return VH_OK;
+}
+
+}  // namespace
+
+namespace vh_rt {
+
+int blaslt_gemm(const vh_gemm_desc* d, bool akc, bool bkc, void* stream, bool* taken) {
+  *taken = false;
+  const int64_t M = d->M, N = d->N, K = d->K;
+  // X = B^T [N, K]: a k-contiguous B is a stored [K, N] (column-major) to transpose.
+  const int tx = bkc ? 1 : 0;
+  const int64_t ldx = bkc ? (N == 1 ? K : d->b_sn) : (K == 1 ? N : d->b_sk);
+  // Y = A^T [K, M]: a k-contiguous A is a stored [K, M] as is.
+  const int ty = akc ? 0 : 1;
+  const int64_t ldy = akc ? (M == 1 ? K : d->a_sm) : (K == 1 ? M : d->a_sk);
+  const int64_t ldc = M == 1 ? N : d->c_sm;
+  if (ldx < (tx ? K : N) || ldy < (ty ? M : K) || ldc < N) return VH_OK;  // not a layout it takes
+  std::lock_guard<std::mutex> lk(g_lib.mu);
+  if (!g_lib.handle) {
+    LT(hipblasLtCreate(&g_lib.handle), "Create");
+    const hipError_t e = hipMalloc(&g_lib.ws, kWorkspace);
+    if (e != hipSuccess) return fail(VH_ERR_OOM, std::string("hipBLASLt workspace: ") + hipGetErrorString(e));
+  }
+  const Key key{M, N, K, ldx, ldy, ldc, tx, ty};
+  auto it = g_lib.plans.find(key);
+  if (it == g_lib.plans.end()) {
+    Plan p;
+    const int rc = make_plan(key, &p);
+    if (rc != VH_OK) return rc;
+    it = g_lib.plans.emplace(key, p).first;
+  }
+  if (!it->second.usable) return VH_OK;  // no algorithm: the caller's kernel runs it
+  const float alpha = d->alpha, beta = 0.0f;
+  const Plan& p = it->second;
+  LT(hipblasLtMatmul(g_lib.handle, p.op, &alpha, d->b, p.lx, d->a, p.ly, &beta, d->c, p.lc, d->c, p.lc, &p.algo,
+                     g_lib.ws, kWorkspace, stream_of(stream)),
+     "Matmul");
+  *taken = true;
+  return VH_OK;
+}
+
+void blaslt_shutdown() {
+  std::lock_guard<std::mutex> lk(g_lib.mu);
+  for (auto& kv : g_lib.plans) destroy(kv.second);
+  g_lib.plans.clear();
+  if (g_lib.ws) (void)hipFree(g_lib.ws);
+  g_lib.ws = nullptr;
+  if (g_lib.handle) hipblasLtDestroy(g_lib.handle);
+  g_lib.handle = nullptr;
+}
+
+}  // namespace vh_rt

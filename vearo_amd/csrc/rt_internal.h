@@ -5,6 +5,8 @@
 
 #include <string>
 
+#include "../../include/vearo_hip.h"
+
 namespace vh_rt {
 #define VH_RT_HIDDEN __attribute__((visibility("hidden")))
 // Records msg as this thread's vh_last_error() text and returns code.
@@ -13,4 +15,10 @@ VH_RT_HIDDEN int fail(int code, const std::string& msg);
 VH_RT_HIDDEN int require_init();
 // The stream a `void* stream` argument names (NULL: the runtime's own).
 VH_RT_HIDDEN hipStream_t stream_of(void* s);
+// A plain product (no batch, causal range, addend or accumulation) through
+// hipBLASLt; *taken is false when it has no algorithm for the layout, and the
+// caller runs its own kernel. akc / bkc: A / B have their unit stride along k.
+VH_RT_HIDDEN int blaslt_gemm(const vh_gemm_desc* d, bool akc, bool bkc, void* stream, bool* taken);
+// Releases hipBLASLt's handle, workspace and cached plans (vh_shutdown).
+VH_RT_HIDDEN void blaslt_shutdown();
 }  // namespace vh_rt

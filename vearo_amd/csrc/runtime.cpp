@@ -405,6 +405,7 @@ int vh_shutdown(void) {
   std::lock_guard<std::mutex> lk(g_init_mu);
   if (!g_rt.ready) return VH_OK;
   VH_HIP(hipStreamSynchronize(g_rt.stream));
+  vh_rt::blaslt_shutdown();
   {
     std::lock_guard<std::mutex> al(g_arena.mu);
     VH_TRY(g_arena.release_all_cached());
@@ -1066,6 +1067,14 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
     return fail(VH_ERR_UNSUPPORTED, "vh_gemm: B needs a unit stride along k or n");
   const int64_t lda = akc ? (M == 1 ? 0 : d->a_sm) : d->a_sk;
   const int64_t ldb = bkc ? (N == 1 ? 0 : d->b_sn) : d->b_sk;
+  // Large plain products go to hipBLASLt (faster on them, measured); the
+  // kernel below covers every product, and runs these when it has no algorithm.
+  if (d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE && !d->e && !d->accumulate && K > 0 &&
+      (double)M * (double)N * (double)K >= 67108864.0) {
+    bool taken = false;
+    VH_TRY(vh_rt::blaslt_gemm(d, akc, bkc, stream, &taken));
+    if (taken) return VH_OK;
+  }
   const bool avec = K > 0 && gemm_vec_ok(d->a, lda, akc ? K : M, d->a_sb);
   const bool bvec = K > 0 && gemm_vec_ok(d->b, ldb, bkc ? K : N, d->b_sb);
   const GemmPlan plan = gemm_plan(M, N, K, d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE);
