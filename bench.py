@@ -20,8 +20,10 @@ step's own multi-GB traffic), so every kernel reads cold data.
 
 value = algorithmic bytes per step / wall time per step (GB/s); algorithmic
 bytes count each necessary HBM transfer once (the live causal triangle only for
-softmax reads, distinct rows only for embedding gathers). Per-kernel durations
-come from HIP events on the runtime stream around each launch; `roofline`
+softmax reads, distinct rows only for embedding gathers). The timed steps are
+issued back to back with nothing between the ops; per-kernel durations come
+from a second pass of the same steps with HIP events on the runtime stream
+around each launch; `roofline`
 reports the longest kernel, with `traffic` from the committed rocprofv3
 FETCH_SIZE / WRITE_SIZE passes when present. cpu_baseline times the CPU oracle
 (the C restatement of the reference's CPU backend, one thread) on a bounded
@@ -529,9 +531,19 @@ def main():
     vh.sync()
 
     K = args.steps
-    ev = [[hip.event() for _ in range(len(ops) + 1)] for _ in range(K)]
-    hip.sync(stream)
+    # The timed steps carry no instrumentation between the ops: the value is
+    # the wall time of exactly K steps issued back to back.
+    vh.sync()
     t0 = time.perf_counter()
+    for i in range(K):
+        for _, _, call in ops:
+            vh.check(call(i))
+    hip.sync(stream)
+    wall = time.perf_counter() - t0
+    vh.sync()
+    # Per-op times from a second pass of K steps with a HIP event between ops
+    # (the events themselves cost a little; that pass is not the value).
+    ev = [[hip.event() for _ in range(len(ops) + 1)] for _ in range(K)]
     for i in range(K):
         e = ev[i]
         hip.record(e[0], stream)
@@ -539,7 +551,6 @@ def main():
             vh.check(call(i))
             hip.record(e[j + 1], stream)
     hip.sync(stream)
-    wall = time.perf_counter() - t0
     vh.sync()
 
     per = {n: 0.0 for n in names}

@@ -41,7 +41,9 @@ using Key = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int
 struct Lib {
   std::mutex mu;
   hipblasLtHandle_t handle = nullptr;
-  void* ws = nullptr;
+  // One workspace per stream: products on different streams may overlap, and
+  // the work in one stream is ordered, so each stream reuses its own.
+  std::map<hipStream_t, void*> ws;
   std::map<Key, Plan> plans;
 } g_lib;
 
@@ -64,6 +66,8 @@ void destroy(Plan& p) {
   p = Plan{};
 }
 
+// Descriptors for the problem and the heuristic's best algorithm within the
+// workspace (usable = false if it has none). Nothing leaks on a failure.
 int make_plan(const Key& k, Plan* out) {
   const auto [M, N, K, ldx, ldy, ldc, tx, ty] = k;
   Plan p;
@@ -71,21 +75,20 @@ int make_plan(const Key& k, Plan* out) {
   // Y = A^T: [K, M] as stored (ty = 0) or the transpose of a stored [M, K].
   const hipblasOperation_t opx = tx ? HIPBLAS_OP_T : HIPBLAS_OP_N;
   const hipblasOperation_t opy = ty ? HIPBLAS_OP_T : HIPBLAS_OP_N;
-  LT(hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F), "MatmulDescCreate");
-  LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &opx, sizeof(opx)), "set TRANSA");
-  LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &opy, sizeof(opy)), "set TRANSB");
-  LT(hipblasLtMatrixLayoutCreate(&p.lx, HIP_R_32F, tx ? K : N, tx ? N : K, ldx), "layout X");
-  LT(hipblasLtMatrixLayoutCreate(&p.ly, HIP_R_32F, ty ? M : K, ty ? K : M, ldy), "layout Y");
-  LT(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc), "layout C");
   hipblasLtMatmulPreference_t pref = nullptr;
-  LT(hipblasLtMatmulPreferenceCreate(&pref), "PreferenceCreate");
-  uint64_t wsb = kWorkspace;
-  int rc = status(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
-                                                         sizeof(wsb)),
-                  "set workspace");
-  hipblasLtMatmulHeuristicResult_t res[1];
-  int found = 0;
-  if (rc == VH_OK) {
+  auto build = [&]() -> int {
+    LT(hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F), "MatmulDescCreate");
+    LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &opx, sizeof(opx)), "set TRANSA");
+    LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &opy, sizeof(opy)), "set TRANSB");
+    LT(hipblasLtMatrixLayoutCreate(&p.lx, HIP_R_32F, tx ? K : N, tx ? N : K, ldx), "layout X");
+    LT(hipblasLtMatrixLayoutCreate(&p.ly, HIP_R_32F, ty ? M : K, ty ? K : M, ldy), "layout Y");
+    LT(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc), "layout C");
+    LT(hipblasLtMatmulPreferenceCreate(&pref), "PreferenceCreate");
+    uint64_t wsb = kWorkspace;
+    LT(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb)),
+       "set workspace");
+    hipblasLtMatmulHeuristicResult_t res[1];
+    int found = 0;
     const hipblasStatus_t st =
         hipblasLtMatmulAlgoGetHeuristic(g_lib.handle, p.op, p.lx, p.ly, p.lc, p.lc, pref, 1, res, &found);
     if (st == HIPBLAS_STATUS_SUCCESS && found > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS &&
@@ -93,8 +96,10 @@ int make_plan(const Key& k, Plan* out) {
       p.algo = res[0].algo;
       p.usable = true;
     }
-  }
-  hipblasLtMatmulPreferenceDestroy(pref);
+    return VH_OK;
+  };
+  const int rc = build();
+  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
   if (rc != VH_OK) {
     destroy(p);
     return rc;
@@ -118,11 +123,16 @@ int blaslt_gemm(const vh_gemm_desc* d, bool akc, bool bkc, void* stream, bool* t
   const int64_t ldy = akc ? (M == 1 ? K : d->a_sm) : (K == 1 ? M : d->a_sk);
   const int64_t ldc = M == 1 ? N : d->c_sm;
   if (ldx < (tx ? K : N) || ldy < (ty ? M : K) || ldc < N) return VH_OK;  // not a layout it takes
+  const hipStream_t s = stream_of(stream);
   std::lock_guard<std::mutex> lk(g_lib.mu);
-  if (!g_lib.handle) {
-    LT(hipblasLtCreate(&g_lib.handle), "Create");
-    const hipError_t e = hipMalloc(&g_lib.ws, kWorkspace);
-    if (e != hipSuccess) return fail(VH_ERR_OOM, std::string("hipBLASLt workspace: ") + hipGetErrorString(e));
+  if (!g_lib.handle) LT(hipblasLtCreate(&g_lib.handle), "Create");
+  void*& ws = g_lib.ws[s];
+  if (!ws) {
+    const hipError_t e = hipMalloc(&ws, kWorkspace);
+    if (e != hipSuccess) {
+      g_lib.ws.erase(s);
+      return fail(VH_ERR_OOM, std::string("hipBLASLt workspace: ") + hipGetErrorString(e));
+    }
   }
   const Key key{M, N, K, ldx, ldy, ldc, tx, ty};
   auto it = g_lib.plans.find(key);
@@ -136,7 +146,7 @@ int blaslt_gemm(const vh_gemm_desc* d, bool akc, bool bkc, void* stream, bool* t
   const float alpha = d->alpha, beta = 0.0f;
   const Plan& p = it->second;
   LT(hipblasLtMatmul(g_lib.handle, p.op, &alpha, d->b, p.lx, d->a, p.ly, &beta, d->c, p.lc, d->c, p.lc, &p.algo,
-                     g_lib.ws, kWorkspace, stream_of(stream)),
+                     ws, kWorkspace, s),
      "Matmul");
   *taken = true;
   return VH_OK;
@@ -146,8 +156,8 @@ void blaslt_shutdown() {
   std::lock_guard<std::mutex> lk(g_lib.mu);
   for (auto& kv : g_lib.plans) destroy(kv.second);
   g_lib.plans.clear();
-  if (g_lib.ws) (void)hipFree(g_lib.ws);
-  g_lib.ws = nullptr;
+  for (auto& kv : g_lib.ws) (void)hipFree(kv.second);
+  g_lib.ws.clear();
   if (g_lib.handle) hipblasLtDestroy(g_lib.handle);
   g_lib.handle = nullptr;
 }
