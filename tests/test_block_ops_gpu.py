@@ -388,3 +388,30 @@ def test_plain_gemm_library_path(vh, akc, bkc):
             u = 2.0 ** -24
             bound = (K * u / (1 - K * u)) * (np.abs(a).astype(np.float64) @ np.abs(bb).astype(np.float64))
             assert np.all(np.abs(got - exact) <= bound), f"plain {akc} {bkc}: f32 error bound"
+
+
+@pytest.mark.parametrize("accumulate", [0, 1])
+def test_linear_library_path_bias_and_residual(vh, accumulate):
+    """A Linear forward large enough for the library path: y = x W^T + b, and
+    with accumulation h = h0 + (x W^T + b) (the residual form the block step
+    uses), against the oracle's matmul then add; determinism on a repeat."""
+    M, K, N = 2048, 3072, 768
+    r = np.random.default_rng(40 + accumulate)
+    x = r.standard_normal((M, K), dtype=np.float32)
+    w = (r.standard_normal((N, K)) * 0.02).astype(np.float32)  # Linear weight [out, in]
+    bias = (r.standard_normal(N) * 0.02).astype(np.float32)
+    h0 = r.standard_normal((M, N), dtype=np.float32)
+    X, W, BI = dev(vh, x), dev(vh, w), dev(vh, bias)
+    outs = []
+    for _ in range(2):
+        C = dev(vh, h0 if accumulate else np.zeros((M, N), np.float32))
+        d = gemm_desc(vh, M, N, K, X.ptr, K, 1, W.ptr, 1, K, C.ptr, N, e=BI.ptr, e_sm=0, e_sn=1,
+                      accumulate=accumulate)
+        vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+        outs.append(fetch(vh, C, (M, N)))
+    np.testing.assert_array_equal(outs[0], outs[1])
+    lin = O.matmul(x, np.ascontiguousarray(w.T)) + bias
+    lin64 = x.astype(np.float64) @ w.T.astype(np.float64) + bias
+    ref = (h0 + lin) if accumulate else lin
+    ref64 = (h0.astype(np.float64) + lin64) if accumulate else lin64
+    assert_parity(outs[0], ref, ref64, name=f"linear library path acc={accumulate}")

@@ -1,11 +1,13 @@
 // blaslt.cpp -- plain f32 products through hipBLASLt.
 //
-// A product with no batch, no causal range, no addend E and no accumulation
-// (the lm_head products, every weight gradient and every input gradient of the
-// block step) is a plain library GEMM; hipBLASLt's gfx950 kernels (128x128x64
-// macro tiles, stream-K) run these shapes faster than the hand-written kernel
-// in kernels/gemm.h, which keeps every product they do not cover (strided
-// batches, causal ranges, fused epilogues). Compute type HIPBLAS_COMPUTE_32F:
+// A product with no batch and no causal range, whose addend E is absent or a
+// bias over the output columns, with or without accumulation into C (the
+// lm_head products, the Linear forwards, every weight and input gradient of
+// the block step) is a library GEMM: D = alpha A B (+ C) (+ bias), the bias
+// through hipBLASLt's bias epilogue. Its gfx950 kernels (128x128x64 macro
+// tiles, stream-K) run these shapes faster than the hand-written kernel in
+// kernels/gemm.h, which keeps every product they do not cover (strided
+// batches, causal ranges, other addends). Compute type HIPBLAS_COMPUTE_32F:
 // f32 products and sums, no reduced-precision path.
 //
 // hipBLASLt is column-major: the row-major C[M, N] = A[M, K] B[K, N] is issued
@@ -36,7 +38,8 @@ struct Plan {
   bool usable = false;  // the heuristic returned an algorithm
 };
 
-using Key = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int, int>;
+// M, N, K, ldx, ldy, ldc, tx, ty, bias epilogue
+using Key = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int, int, int>;
 
 struct Lib {
   std::mutex mu;
@@ -69,7 +72,7 @@ void destroy(Plan& p) {
 // Descriptors for the problem and the heuristic's best algorithm within the
 // workspace (usable = false if it has none). Nothing leaks on a failure.
 int make_plan(const Key& k, Plan* out) {
-  const auto [M, N, K, ldx, ldy, ldc, tx, ty] = k;
+  const auto [M, N, K, ldx, ldy, ldc, tx, ty, bias] = k;
   Plan p;
   // X = B^T: [N, K] as stored (tx = 0) or the transpose of a stored [K, N].
   // Y = A^T: [K, M] as stored (ty = 0) or the transpose of a stored [M, K].
@@ -80,6 +83,14 @@ int make_plan(const Key& k, Plan* out) {
     LT(hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F), "MatmulDescCreate");
     LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &opx, sizeof(opx)), "set TRANSA");
     LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &opy, sizeof(opy)), "set TRANSB");
+    if (bias) {
+      // A bias of length N (D's rows in the column-major view) on every column.
+      const uint32_t epi = HIPBLASLT_EPILOGUE_BIAS;
+      const int32_t bt = HIP_R_32F;
+      LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi)), "set EPILOGUE");
+      LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt)),
+         "set BIAS_DATA_TYPE");
+    }
     LT(hipblasLtMatrixLayoutCreate(&p.lx, HIP_R_32F, tx ? K : N, tx ? N : K, ldx), "layout X");
     LT(hipblasLtMatrixLayoutCreate(&p.ly, HIP_R_32F, ty ? M : K, ty ? K : M, ldy), "layout Y");
     LT(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc), "layout C");
@@ -134,7 +145,9 @@ int blaslt_gemm(const vh_gemm_desc* d, bool akc, bool bkc, void* stream, bool* t
       return fail(VH_ERR_OOM, std::string("hipBLASLt workspace: ") + hipGetErrorString(e));
     }
   }
-  const Key key{M, N, K, ldx, ldy, ldc, tx, ty};
+  const int bias = d->e ? 1 : 0;
+  if (bias && !(d->e_sm == 0 && d->e_sn == 1)) return VH_OK;  // only a bias over the columns
+  const Key key{M, N, K, ldx, ldy, ldc, tx, ty, bias};
   auto it = g_lib.plans.find(key);
   if (it == g_lib.plans.end()) {
     Plan p;
@@ -143,8 +156,13 @@ int blaslt_gemm(const vh_gemm_desc* d, bool akc, bool bkc, void* stream, bool* t
     it = g_lib.plans.emplace(key, p).first;
   }
   if (!it->second.usable) return VH_OK;  // no algorithm: the caller's kernel runs it
-  const float alpha = d->alpha, beta = 0.0f;
+  const float alpha = d->alpha, beta = d->accumulate ? 1.0f : 0.0f;
   const Plan& p = it->second;
+  if (bias) {
+    const void* bp = d->e;
+    LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bp, sizeof(bp)),
+       "set BIAS_POINTER");
+  }
   LT(hipblasLtMatmul(g_lib.handle, p.op, &alpha, d->b, p.lx, d->a, p.ly, &beta, d->c, p.lc, d->c, p.lc, &p.algo,
                      ws, kWorkspace, s),
      "Matmul");

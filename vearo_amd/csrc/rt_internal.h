@@ -15,9 +15,10 @@ VH_RT_HIDDEN int fail(int code, const std::string& msg);
 VH_RT_HIDDEN int require_init();
 // The stream a `void* stream` argument names (NULL: the runtime's own).
 VH_RT_HIDDEN hipStream_t stream_of(void* s);
-// A plain product (no batch, causal range, addend or accumulation) through
-// hipBLASLt; *taken is false when it has no algorithm for the layout, and the
-// caller runs its own kernel. akc / bkc: A / B have their unit stride along k.
+// An unbatched dense product (no addend, or a bias over the output columns;
+// accumulation allowed) through hipBLASLt; *taken is false when it does not
+// take the layout or has no algorithm, and the caller runs its own kernel.
+// akc / bkc: A / B have their unit stride along k.
 VH_RT_HIDDEN int blaslt_gemm(const vh_gemm_desc* d, bool akc, bool bkc, void* stream, bool* taken);
 // Releases hipBLASLt's handle, workspace and cached plans (vh_shutdown).
 VH_RT_HIDDEN void blaslt_shutdown();

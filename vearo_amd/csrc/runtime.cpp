@@ -1067,10 +1067,11 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
     return fail(VH_ERR_UNSUPPORTED, "vh_gemm: B needs a unit stride along k or n");
   const int64_t lda = akc ? (M == 1 ? 0 : d->a_sm) : d->a_sk;
   const int64_t ldb = bkc ? (N == 1 ? 0 : d->b_sn) : d->b_sk;
-  // Large plain products go to hipBLASLt (faster on them, measured); the
-  // kernel below covers every product, and runs these when it has no algorithm.
-  if (d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE && !d->e && !d->accumulate && K > 0 &&
-      (double)M * (double)N * (double)K >= 67108864.0) {
+  // Large unbatched dense products, with no addend or a bias over the output
+  // columns, go to hipBLASLt (faster on them, measured); the kernel below
+  // covers every product, and runs these when the library has no algorithm.
+  if (d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE && (!d->e || (d->e_sm == 0 && d->e_sn == 1)) &&
+      K > 0 && (double)M * (double)N * (double)K >= 67108864.0) {
     bool taken = false;
     VH_TRY(vh_rt::blaslt_gemm(d, akc, bkc, stream, &taken));
     if (taken) return VH_OK;
