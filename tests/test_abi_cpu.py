@@ -118,6 +118,9 @@ def launcher_kernel_names():
         for b in ("k4", "k1", "n4", "n1"):
             names.add(f"vh_gemm_{a}_{b}")
             names.add(f"vh_gemm_{a}_{b}_t64")
+    for a in ("k4", "m4"):
+        for b in ("k4", "n4"):
+            names.add(f"vh_gemmp_{a}_{b}")
     return names
 
 

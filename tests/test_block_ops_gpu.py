@@ -179,6 +179,59 @@ def test_gemm_causal_modes(vh):
     assert_parity(got[il], ref[il], name="skip upper")
 
 
+@pytest.mark.parametrize("akc,bkc", [(True, True), (True, False), (False, True), (False, False)])
+def test_gemm_persistent_short_k(vh, akc, bkc):
+    """Batched products with K <= 256 and 128-bit operand layouts run the
+    persistent kernel (vh_gemmp_*, one workgroup per resident slot walking the
+    tiles): edge tiles, a ragged last k tile, the causal triangle, an addend
+    (per element and a broadcast bias), alpha and accumulation, and more work
+    items than resident workgroups (the 120-batch cases)."""
+    r = np.random.default_rng(11)
+    cases = ((3, 5, 200, 300, 40, 0, "full", 0), (2, 3, 300, 300, 64, 1, None, 1),
+             (6, 20, 384, 384, 64, 1, None, 0), (4, 30, 256, 384, 96, 0, "bias", 1))
+    for B0, B1, M, N, K, causal, ekind, acc in cases:
+        a = r.standard_normal((B0, B1, M, K), dtype=np.float32)
+        b = (r.standard_normal((B0, B1, K, N)) * 0.1).astype(np.float32)
+        c0 = r.standard_normal((B0, B1, M, N), dtype=np.float32)
+        # A stored k-contiguous [.., M, K] or as its transpose [.., K, M]; B as
+        # [.., N, K] (k-contiguous) or [.., K, N].
+        A = dev(vh, a if akc else np.swapaxes(a, -1, -2))
+        Bb = dev(vh, np.swapaxes(b, -1, -2) if bkc else b)
+        C = dev(vh, c0)
+        d = gemm_desc(vh, M, N, K, A.ptr, K if akc else 1, 1 if akc else M, Bb.ptr, 1 if bkc else N,
+                      K if bkc else 1, C.ptr, N, alpha=0.125, accumulate=acc, causal=causal)
+        d.batch[0], d.batch[1] = B0, B1
+        d.a_sb[0], d.a_sb[1] = B1 * M * K, M * K
+        d.b_sb[0], d.b_sb[1] = B1 * K * N, K * N
+        d.c_sb[0], d.c_sb[1] = B1 * M * N, M * N
+        e = np.zeros((B0, B1, M, N), np.float32)
+        keep = None
+        if ekind == "full":
+            e = r.standard_normal((B0, B1, M, N), dtype=np.float32)
+            keep = dev(vh, e)
+            d.e, d.e_sm, d.e_sn = keep.ptr, N, 1
+            d.e_sb[0], d.e_sb[1] = B1 * M * N, M * N
+        elif ekind == "bias":
+            bias = r.standard_normal(N, dtype=np.float32)
+            e = np.broadcast_to(bias, (B0, B1, M, N))
+            keep = dev(vh, bias)
+            d.e, d.e_sm, d.e_sn = keep.ptr, 0, 1
+        vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+        got = fetch(vh, C, (B0, B1, M, N))
+        mm = O.matmul(a, b)
+        cpu = mm * np.float32(0.125) + e
+        ref64 = np.matmul(a.astype(np.float64), b) * 0.125 + e
+        if acc:
+            cpu = c0 + cpu
+            ref64 = c0 + ref64
+        name = f"persistent {B0}x{B1} {M}x{N}x{K} causal={causal} e={ekind} acc={acc} akc={akc} bkc={bkc}"
+        if causal:
+            il = np.tril_indices(M)
+            got, cpu, ref64 = got[..., il[0], il[1]], cpu[..., il[0], il[1]], ref64[..., il[0], il[1]]
+        assert_parity(got, cpu, ref64, name=name)
+        del keep
+
+
 def attention_gpu(vh, q, k, v, mask, causal, go=None, layout="bhsd"):
     """Fused attention fwd (and bwd when go is given) on the device. layout
     'bshd' stores q/k/v/out as [B, S, H, Dk] and passes [B, H, S, Dk] views."""

@@ -144,12 +144,71 @@ VH_DEV void gm_tile_of(int bid, int nblk, int tiles_m, int tiles_n, int& tm, int
   tn = in / gsize;
 }
 
+// The epilogue of one output element from its product sum v: the raw partial
+// under split-K (raw), else alpha v (+ E[m, n]) (+ old = out[m, n]).
+VH_DEV float gm_finish(const GemmArgs& a, const float* E, bool raw, float v, int64_t m, int64_t n, float old) {
+  if (raw) return v;
+  v = v * a.alpha;
+  if (E) v = v + E[m * a.sem + n * a.sen];
+  if (a.accumulate) v = old + v;
+  return v;
+}
+
+// A wave's 64 x TN/2 quadrant of the tile at (m0, n0) straight from its
+// accumulators: register r of a 32 x 32 tile holds row 8*(r/4) + 4*h + r%4,
+// column li; elements outside M x N are dropped. NT: streaming (nontemporal)
+// stores, which do not allocate the written lines in L2.
+template <int NTW, bool NT = false>
+VH_DEV void gm_store_direct(const GemmArgs& a, const vh_f32x16 (&acc)[2][NTW], float* out, int64_t ldo,
+                            const float* E, bool raw, int64_t m0, int64_t n0, int wm, int wn, int li, int h) {
+  if (m0 + GM_TM <= a.M && n0 + NTW * 64 <= a.N && !E && (raw || !a.accumulate)) {
+    // A whole tile that reads nothing back: the stores go out back to back
+    // (a conditional load of C among them makes each wait for all earlier
+    // stores, as the memory counter covers both).
+    const float alpha = raw ? 1.0f : a.alpha;
+    float* base = out + (m0 + wm * 64 + 4 * h) * ldo + n0 + wn * (NTW * 32) + li;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float* cp = base + (mt * 32 + 8 * (r >> 2) + (r & 3)) * ldo + nt * 32;
+          const float v = raw ? acc[mt][nt][r] : acc[mt][nt][r] * alpha;
+          if constexpr (NT)
+            __builtin_nontemporal_store(v, cp);
+          else
+            *cp = v;
+        }
+    return;
+  }
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int nt = 0; nt < NTW; ++nt) {
+      const int64_t n = n0 + wn * (NTW * 32) + nt * 32 + li;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (m < a.M && n < a.N) {
+          float* cp = out + m * ldo + n;
+          const float v = gm_finish(a, E, raw, acc[mt][nt][r], m, n, a.accumulate && !raw ? *cp : 0.0f);
+          if constexpr (NT)
+            __builtin_nontemporal_store(v, cp);
+          else
+            *cp = v;
+        }
+      }
+    }
+  }
+}
+
 template <bool A_KC, bool A_VEC, bool B_KC, bool B_VEC, int TN>
 VH_DEV void gemm_f32_impl(const GemmArgs& a) {
   static_assert(TN == 128 || TN == 64, "C tile width");
   constexpr int NTW = TN / 64;  // 32-wide n tiles per wave
-  __shared__ __attribute__((aligned(16))) float As[2][GM_STAGE];
-  __shared__ __attribute__((aligned(16))) float Bs[2][GM_STAGE];
+  // L[0..1]: A's two k stages, L[2..3]: B's; after the k loop, the C tile.
+  __shared__ __attribute__((aligned(16))) float L[4][GM_STAGE];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   int tm, tn;
   int64_t bat = blockIdx.y;  // batch index (both batch dims)
@@ -195,8 +254,8 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
   if (kb < ke) {
     gm_load<A_KC, A_VEC, GM_TM>(A, a.lda, m0, a.M, kb, a.K, tid, sa);
     gm_load<B_KC, B_VEC, TN>(B, a.ldb, n0, a.N, kb, a.K, tid, sb);
-    gm_store_lds<A_KC, A_VEC, GM_TM>(As[0], tid, sa);
-    gm_store_lds<B_KC, B_VEC, TN>(Bs[0], tid, sb);
+    gm_store_lds<A_KC, A_VEC, GM_TM>(L[0], tid, sa);
+    gm_store_lds<B_KC, B_VEC, TN>(L[2], tid, sb);
     __syncthreads();
   }
   // Per k tile: the next tile's global loads go out; then all of this tile's
@@ -230,10 +289,10 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int kc = h * 16 + 4 * q;
-        fa[q][0] = gm_frag<A_KC>(As[s], wm * 64 + li, kc);
-        fa[q][1] = gm_frag<A_KC>(As[s], wm * 64 + 32 + li, kc);
+        fa[q][0] = gm_frag<A_KC>(L[s], wm * 64 + li, kc);
+        fa[q][1] = gm_frag<A_KC>(L[s], wm * 64 + 32 + li, kc);
 #pragma unroll
-        for (int nt = 0; nt < NTW; ++nt) fb[q][nt] = gm_frag<B_KC>(Bs[s], wn * (TN / 2) + nt * 32 + li, kc);
+        for (int nt = 0; nt < NTW; ++nt) fb[q][nt] = gm_frag<B_KC>(L[2 + s], wn * (TN / 2) + nt * 32 + li, kc);
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -246,8 +305,8 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
           }
         }
       }
-      gm_store_lds<A_KC, A_VEC, GM_TM>(As[s ^ 1], tid, sa);
-      gm_store_lds<B_KC, B_VEC, TN>(Bs[s ^ 1], tid, sb);
+      gm_store_lds<A_KC, A_VEC, GM_TM>(L[s ^ 1], tid, sa);
+      gm_store_lds<B_KC, B_VEC, TN>(L[2 + (s ^ 1)], tid, sb);
       if constexpr (!CHECK) __builtin_amdgcn_sched_group_barrier(0x020, VM, 0);  // the next tile's loads
       __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);                        // all fragment reads
       __builtin_amdgcn_sched_group_barrier(0x008, 3 * MF, 0);                    // groups 0-2
@@ -266,41 +325,196 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
   else
     main_loop(GmFlag<false>{});
 
-  // Epilogue. Accumulator register r of a 32 x 32 tile holds row
-  // 8*(r/4) + 4*h + r%4, column li.
-  if (split) {  // raw partial sums; the reduce applies the epilogue
-    float* W = a.ws + (int64_t)blockIdx.y * a.M * a.N;
+  // Epilogue. Straight from the accumulators, one wave store covers two
+  // 128-byte row pieces; a tile wholly inside C with 16-byte aligned rows goes
+  // through LDS instead (the k loop's last barrier has freed it), so that each
+  // store writes 16 bytes and a half-wave a whole 512-byte row.
+  float* out = split ? a.ws + (int64_t)blockIdx.y * a.M * a.N : C;
+  const int64_t ldo = split ? a.N : a.ldc;
+  const float* E = !split && a.E ? a.E + b1 * a.se1 + b2 * a.se2 : nullptr;
+  const bool whole = m0 + GM_TM <= a.M && n0 + TN <= a.N && (ldo & 3) == 0 &&
+                     (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  if (whole) {
+    constexpr int CS = TN + 8;  // row stride (floats): rows 4 apart are 32 banks apart
+    static_assert(GM_TM * CS <= 4 * GM_STAGE, "C tile fits the operand LDS");
+    float* Cs = &L[0][0];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NTW; ++nt) {
-        const int64_t n = n0 + wn * (TN / 2) + nt * 32 + li;
+      for (int nt = 0; nt < NTW; ++nt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t m = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (m < a.M && n < a.N) W[m * a.N + n] = acc[mt][nt][r];
-        }
+        for (int r = 0; r < 16; ++r)
+          Cs[(wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3)) * CS + wn * (TN / 2) + nt * 32 + li] =
+              acc[mt][nt][r];
+    __syncthreads();
+    constexpr int Q = TN / 4;      // 16-byte pieces per row
+    constexpr int RP = 256 / Q;    // rows per pass
+    const int c = (tid % Q) * 4, r0 = tid / Q;
+#pragma unroll 4
+    for (int i = 0; i < GM_TM / RP; ++i) {
+      const int row = r0 + RP * i;
+      const int64_t m = m0 + row, n = n0 + c;
+      vh_f4 v = *reinterpret_cast<const vh_f4*>(Cs + row * CS + c);
+      vh_f4* op = reinterpret_cast<vh_f4*>(out + m * ldo + n);
+      if (!split) {
+        const vh_f4 old = a.accumulate ? *op : vh_f4{};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = gm_finish(a, E, false, v[e], m, n + e, old[e]);
       }
+      *op = v;
+    }
     return;
   }
-  const float* E = a.E ? a.E + b1 * a.se1 + b2 * a.se2 : nullptr;
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) {
-      const int64_t n = n0 + wn * (TN / 2) + nt * 32 + li;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + wm * 64 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (m < a.M && n < a.N) {
-          float v = acc[mt][nt][r] * a.alpha;
-          if (E) v = v + E[m * a.sem + n * a.sen];
-          float* cp = C + m * a.ldc + n;
-          if (a.accumulate) v = *cp + v;
-          *cp = v;
-        }
-      }
+  gm_store_direct<NTW>(a, acc, out, ldo, E, split, m0, n0, wm, wn, li, h);
+}
+
+// Persistent form for batched products with a short k range (attention's
+// scores q k^T and dP = dO v^T: K = Dk = 64, 2 k tiles per C tile). Launched
+// as one workgroup per resident slot (a multiple of 8), each walks a list of
+// C tiles as one continuous k loop: the last k step of a tile loads the
+// first k tile of the next one, so its global loads are in flight under the
+// current tile's products and epilogue instead of exposed at the start of a
+// short-lived workgroup. Work items are the live tiles of every batch, batch
+// major (causal 1: the tn <= tm triangle of a square tile grid, tiles_n >=
+// tiles_m); XCD x (= workgroup id % 8, the hardware's round-robin) takes the
+// x-th contiguous eighth of the items, so one XCD works on one or two batches
+// at a time and its L2 holds their operands. Tile width 128; no split, causal
+// 0 or 1 only (the host guarantees both).
+template <bool A_KC, bool A_VEC, bool B_KC, bool B_VEC>
+VH_DEV void gemm_f32_persist(const GemmArgs& a) {
+  constexpr int TN = 128, NTW = 2;
+  __shared__ __attribute__((aligned(16))) float L[4][GM_STAGE];  // A stages 0-1, B stages 2-3
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w >> 1, wn = w & 1, li = lane & 31, h = lane >> 5;
+  const int64_t live = a.causal == 1 ? (int64_t)a.tiles_m * (a.tiles_m + 1) / 2 : (int64_t)a.tiles_m * a.tiles_n;
+  const int64_t total = live * a.nbat;
+  const int nloc = (int)(gridDim.x / 8), x = (int)(blockIdx.x % 8);
+  const int64_t per = (total + 7) / 8;
+  const int64_t end = (x + 1) * per < total ? (x + 1) * per : total;
+  int64_t item = x * per + (int64_t)(blockIdx.x / 8);
+  if (item >= end) return;
+
+  struct Tile {
+    const float* A;
+    const float* B;
+    float* C;
+    const float* E;
+    int64_t m0, n0;
+    bool inside;  // the whole tile and its k range are inside A, B and C
+  };
+  auto decode = [&](int64_t it, Tile& t) {
+    const int64_t bat = it / live;
+    const int64_t u = it % live;
+    int64_t tm, tn;
+    if (a.causal == 1) {  // u = tm (tm + 1) / 2 + tn, tn <= tm
+      tm = (int64_t)((sqrtf(8.0f * (float)u + 1.0f) - 1.0f) * 0.5f);
+      while (tm * (tm + 1) / 2 > u) --tm;
+      while ((tm + 1) * (tm + 2) / 2 <= u) ++tm;
+      tn = u - tm * (tm + 1) / 2;
+    } else {
+      tm = u / a.tiles_n;
+      tn = u % a.tiles_n;
     }
+    const int64_t b1 = bat / a.nb2, b2 = bat % a.nb2;
+    t.A = a.A + b1 * a.sa1 + b2 * a.sa2;
+    t.B = a.B + b1 * a.sb1 + b2 * a.sb2;
+    t.C = a.C + b1 * a.sc1 + b2 * a.sc2;
+    t.E = a.E ? a.E + b1 * a.se1 + b2 * a.se2 : nullptr;
+    t.m0 = tm * GM_TM;
+    t.n0 = tn * TN;
+    t.inside = t.m0 + GM_TM <= a.M && t.n0 + TN <= a.N && a.K % GM_TK == 0;
+  };
+
+  Tile cur, nxt;
+  decode(item, cur);
+  float sa[GM_TM / 8], sb[TN / 8];
+  gm_load<A_KC, A_VEC, GM_TM>(cur.A, a.lda, cur.m0, a.M, 0, a.K, tid, sa);
+  gm_load<B_KC, B_VEC, TN>(cur.B, a.ldb, cur.n0, a.N, 0, a.K, tid, sb);
+  gm_store_lds<A_KC, A_VEC, GM_TM>(L[0], tid, sa);
+  gm_store_lds<B_KC, B_VEC, TN>(L[2], tid, sb);
+  __syncthreads();
+  int s = 0;
+
+  constexpr int RD = 4 * ((A_KC ? 2 : 8) + NTW * (B_KC ? 1 : 4));
+  constexpr int WR = (A_VEC ? GM_TM / 32 : GM_TM / 8) + (B_VEC ? TN / 32 : TN / 8);
+  constexpr int VM = WR;
+  constexpr int MF = 8 * NTW;
+  for (;;) {
+    const int64_t nit = item + nloc;
+    const bool has_next = nit < end;
+    if (has_next)
+      decode(nit, nxt);
+    else
+      nxt = cur;
+    vh_f32x16 acc[2][NTW];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) acc[i][j] = vh_f32x16{};
+    // One k step: the next stage (this tile's next k tile, else the next
+    // tile's first, else this one's last again) is loaded, this stage is
+    // multiplied, and the loaded one is staged into the other LDS buffer.
+    auto k_loop = [&](auto unchecked) {
+      constexpr bool CHECK = !decltype(unchecked)::value;
+      for (int64_t k0 = 0; k0 < a.K; k0 += GM_TK) {
+        const bool more = k0 + GM_TK < a.K;
+        const float* An = more ? cur.A : nxt.A;
+        const float* Bn = more ? cur.B : nxt.B;
+        const int64_t mn = more ? cur.m0 : nxt.m0, nn = more ? cur.n0 : nxt.n0;
+        const int64_t kn = more ? k0 + GM_TK : (has_next ? 0 : k0);
+        if constexpr (CHECK) {
+          if (more || has_next) {
+            gm_load<A_KC, A_VEC, GM_TM>(An, a.lda, mn, a.M, kn, a.K, tid, sa);
+            gm_load<B_KC, B_VEC, TN>(Bn, a.ldb, nn, a.N, kn, a.K, tid, sb);
+          }
+        } else {
+          gm_load<A_KC, A_VEC, GM_TM, false>(An, a.lda, mn, a.M, kn, a.K, tid, sa);
+          gm_load<B_KC, B_VEC, TN, false>(Bn, a.ldb, nn, a.N, kn, a.K, tid, sb);
+        }
+        vh_f4 fa[4][2], fb[4][NTW];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int kc = h * 16 + 4 * q;
+          fa[q][0] = gm_frag<A_KC>(L[s], wm * 64 + li, kc);
+          fa[q][1] = gm_frag<A_KC>(L[s], wm * 64 + 32 + li, kc);
+#pragma unroll
+          for (int nt = 0; nt < NTW; ++nt) fb[q][nt] = gm_frag<B_KC>(L[2 + s], wn * (TN / 2) + nt * 32 + li, kc);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt) {
+              acc[0][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][0][e], fb[q][nt][e], acc[0][nt], 0, 0, 0);
+              acc[1][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][1][e], fb[q][nt][e], acc[1][nt], 0, 0, 0);
+            }
+          }
+        }
+        gm_store_lds<A_KC, A_VEC, GM_TM>(L[s ^ 1], tid, sa);
+        gm_store_lds<B_KC, B_VEC, TN>(L[2 + (s ^ 1)], tid, sb);
+        if constexpr (!CHECK) __builtin_amdgcn_sched_group_barrier(0x020, VM, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 3 * MF, 0);
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x200, (WR + MF - 1) / MF, 0);
+        }
+        __syncthreads();
+        s ^= 1;
+      }
+    };
+    if (cur.inside && nxt.inside)
+      k_loop(GmFlag<true>{});
+    else
+      k_loop(GmFlag<false>{});
+    // Streaming stores: with normal ones the write of a score-sized output
+    // runs at ~1.8 TB/s here, with these at ~2.8 TB/s (measured).
+    gm_store_direct<NTW, true>(a, acc, cur.C, a.ldc, cur.E, false, cur.m0, cur.n0, wm, wn, li, h);
+    if (!has_next) break;
+    item = nit;
+    cur = nxt;
   }
 }
 

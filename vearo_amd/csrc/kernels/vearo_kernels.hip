@@ -175,6 +175,13 @@ K_GEMM(false, false, true, true, vh_gemm_m1_k4)
 K_GEMM(false, false, true, false, vh_gemm_m1_k1)
 K_GEMM(false, false, false, true, vh_gemm_m1_n4)
 K_GEMM(false, false, false, false, vh_gemm_m1_n1)
+// Persistent form of the 128-bit-load layouts (batched products with short k).
+#define K_GEMMP(AK, BK, NAME) \
+  extern "C" __global__ void __launch_bounds__(256, 2) NAME(GemmArgs a) { gemm_f32_persist<AK, true, BK, true>(a); }
+K_GEMMP(true, true, vh_gemmp_k4_k4)
+K_GEMMP(true, false, vh_gemmp_k4_n4)
+K_GEMMP(false, true, vh_gemmp_m4_k4)
+K_GEMMP(false, false, vh_gemmp_m4_n4)
 
 extern "C" __global__ void __launch_bounds__(256) vh_gemm_reduce(GemmReduceArgs a) { gemm_reduce_impl(a); }
 

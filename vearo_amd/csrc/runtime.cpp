@@ -1118,6 +1118,48 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
       return rc;
     }
   }
+  // Batched products with a short k range (attention's q k^T and dO v^T,
+  // K = Dk): one workgroup per resident slot walks the tiles of all batches,
+  // loading each tile's operands under the previous tile's products
+  // (gemm_f32_persist). A workgroup per tile spends most of its short life
+  // waiting for its first loads there.
+  const int64_t nbat = d->batch[0] * d->batch[1];
+  if (nbat > 1 && K > 0 && K <= 256 && avec && bvec && !plan.narrow &&
+      (d->causal == VH_GEMM_DENSE || (d->causal == VH_GEMM_SKIP_UPPER && tiles_n >= tiles_m))) {
+    GemmArgs g{};
+    g.A = d->a;
+    g.B = d->b;
+    g.C = d->c;
+    g.E = d->e;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.lda = lda;
+    g.ldb = ldb;
+    g.ldc = d->c_sm;
+    g.sa1 = d->a_sb[0];
+    g.sa2 = d->a_sb[1];
+    g.sb1 = d->b_sb[0];
+    g.sb2 = d->b_sb[1];
+    g.sc1 = d->c_sb[0];
+    g.sc2 = d->c_sb[1];
+    g.se1 = d->e_sb[0];
+    g.se2 = d->e_sb[1];
+    g.sem = d->e_sm;
+    g.sen = d->e_sn;
+    g.nb2 = (int32_t)d->batch[1];
+    g.tiles_m = (int32_t)tiles_m;
+    g.tiles_n = (int32_t)tiles_n;
+    g.accumulate = d->accumulate ? 1 : 0;
+    g.causal = d->causal;
+    g.alpha = d->alpha;
+    g.nbat = nbat;
+    const int64_t live = d->causal == VH_GEMM_SKIP_UPPER ? tiles_m * (tiles_m + 1) / 2 : tiles;
+    const int64_t slots = 8 * std::max<int64_t>(1, 2 * std::max(g_rt.cu_count, 1) / 8);
+    const int64_t grid = std::min<int64_t>(slots, 8 * cdiv(live * nbat, 8));
+    const std::string pname = std::string("vh_gemmp_") + (akc ? "k4" : "m4") + "_" + (bkc ? "k4" : "n4");
+    return launch(pname, (unsigned)grid, 1, 256, 0, s, g);
+  }
   // Grid y covers both batch dims; runs of the outer one keep it under 65535.
   const int64_t outer_chunk = std::max<int64_t>(1, 65535 / d->batch[1]);
   if (d->batch[1] > 65535) return fail(VH_ERR_UNSUPPORTED, "vh_gemm: inner batch too large");

@@ -97,6 +97,7 @@ struct GemmArgs {
   int32_t ksplit;
   int64_t kchunk;
   float* ws;
+  int64_t nbat;  // persistent form (vh_gemmp_*): batches in the launch (grid y is 1)
 };
 
 // Fixed-order sum of the split-K partials plus the GEMM epilogue.
