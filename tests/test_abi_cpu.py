@@ -103,6 +103,8 @@ def launcher_kernel_names():
                       f"vh_sm_fwd_t{t}_n{v}_v{vw}_r2", f"vh_sm_bwd_t{t}_n{v}_v{vw}_r2"}
         for v in (1, 2, 3, 4):
             names.add(f"vh_ln_bwd_t64_n{v}_v{vw}_b1024")
+            if vw == 4:
+                names |= {f"vh_ln_bwd_t64_n{v}_v4_b1024_f", f"vh_ln_fwd_t64_n{v}_v4_r4_f"}
         for v in nv:
             names |= {f"vh_gelu_bias_fwd_n{v}_v{vw}", f"vh_gelu_bias_bwd_n{v}_v{vw}"}
         names |= {f"vh_gelu_fwd_v{vw}", f"vh_gelu_gradmul_v{vw}", f"vh_emb_fwd_v{vw}",

@@ -19,8 +19,10 @@ def rng(tag):
 
 
 # ------------------------------------------------------------------ layernorm
+# (33, 256), (9, 512), (16384, 768), (70, 1024): the full-row kernel forms
+# (C = 64 lanes x 1..4 units x 4 floats), with ragged row counts.
 LN_SHAPES = [(2048, 128), (16384, 768), (1, 5), (3, 33), (7, 64), (130, 100), (64, 1000),
-             (17, 1030), (8, 4096), (4, 20000), (5, 1)]
+             (17, 1030), (8, 4096), (4, 20000), (5, 1), (33, 256), (9, 512), (70, 1024)]
 
 
 @pytest.mark.parametrize("rows,C", LN_SHAPES)

@@ -39,6 +39,13 @@ ROW_CFG_ALL(K_LN_FWD, 1)
 ROW_CFG_ALL(K_LN_FWD, 4)
 ROW_CFG_MULTI(K_LN_FWD_M, 1)
 ROW_CFG_MULTI(K_LN_FWD_M, 4)
+// Full-row forms (C == T * N * 4) of the wave-team configurations.
+#define K_LN_FWD_F(T, N)                                                          \
+  extern "C" __global__ void __launch_bounds__(BS_OF(T))                          \
+      vh_ln_fwd_t##T##_n##N##_v4_r4_f(LnFwdArgs a) {                              \
+    ln_fwd_impl<T, N, 4, 4, true>(a);                                             \
+  }
+K_LN_FWD_F(64, 1) K_LN_FWD_F(64, 2) K_LN_FWD_F(64, 3) K_LN_FWD_F(64, 4)
 
 #define K_LN_BWD_B(T, N, VW, BS)                                                  \
   extern "C" __global__ void __launch_bounds__(BS)                                \
@@ -58,6 +65,12 @@ ROW_CFG_SMALL(K_LN_BWD, 4)
 // Wave teams with rows up to 1024 units: 16 row-groups per workgroup.
 K_LN_BWD_1024(64, 1, 1) K_LN_BWD_1024(64, 2, 1) K_LN_BWD_1024(64, 3, 1) K_LN_BWD_1024(64, 4, 1)
 K_LN_BWD_1024(64, 1, 4) K_LN_BWD_1024(64, 2, 4) K_LN_BWD_1024(64, 3, 4) K_LN_BWD_1024(64, 4, 4)
+#define K_LN_BWD_F(T, N)                                                          \
+  extern "C" __global__ void __launch_bounds__(1024) vh_ln_bwd_t##T##_n##N##_v4_b1024_f(LnBwdArgs a) { \
+    extern __shared__ float dyn_lds[];                                            \
+    ln_bwd_impl<T, N, 4, 1024, true>(a, dyn_lds);                                 \
+  }
+K_LN_BWD_F(64, 1) K_LN_BWD_F(64, 2) K_LN_BWD_F(64, 3) K_LN_BWD_F(64, 4)
 
 #define K_SM_FWD_R(T, N, VW, R)                                                   \
   extern "C" __global__ void __launch_bounds__(BS_OF(T))                          \

@@ -211,8 +211,9 @@ int fill(void* p, float value, int64_t n, hipStream_t s) {
 // --------------------------------------------------------- row engine cfg --
 struct RowCfg {
   int team, nv, vw;
-  int rpw = 1;  // rows per team (forward kernels)
-  int bs = 0;   // workgroup size (0: max(team, 256))
+  int rpw = 1;        // rows per team (forward kernels)
+  int bs = 0;         // workgroup size (0: max(team, 256))
+  bool full = false;  // a "_f" form: every unit of the row live, no bounds tests
 };
 
 // Rows per team for short rows (wave or sub-wave teams holding <= 4 units per
@@ -262,8 +263,17 @@ std::string row_base(const char* base, const RowCfg& c) {
          std::to_string(c.vw);
 }
 // Forward kernels carry the rows-per-team suffix, backward LayerNorm the block size.
-std::string fwd_kernel(const char* base, const RowCfg& c) { return row_base(base, c) + "_r" + std::to_string(c.rpw); }
-std::string bwd_kernel(const char* base, const RowCfg& c) { return row_base(base, c) + "_b" + std::to_string(block_of(c)); }
+std::string fwd_kernel(const char* base, const RowCfg& c) {
+  return row_base(base, c) + "_r" + std::to_string(c.rpw) + (c.full ? "_f" : "");
+}
+std::string bwd_kernel(const char* base, const RowCfg& c) {
+  return row_base(base, c) + "_b" + std::to_string(block_of(c)) + (c.full ? "_f" : "");
+}
+// The LayerNorm kernels come in full-row forms for wave teams of 128-bit
+// units with up to 4 units per lane when C fills them exactly.
+void set_ln_full(RowCfg* c, int64_t C) {
+  c->full = c->team == 64 && c->vw == 4 && c->nv <= 4 && C == (int64_t)c->team * c->nv * c->vw;
+}
 
 // Multi-row variants exist for teams <= 64 lanes holding <= 4 units per lane.
 void set_rpw(RowCfg* c, int rpw) { c->rpw = (c->team <= 64 && c->nv <= 4) ? rpw : 1; }
@@ -513,6 +523,8 @@ int vh_layernorm_fwd(const float* x, const float* w, const float* b, float* y, i
   if (!pick_row_cfg(C, vec, 16, &c))
     return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_fwd: C=" + std::to_string(C) + " exceeds 65536");
   set_rpw(&c, kLnFwdRpw);
+  set_ln_full(&c, C);
+  if (c.full && c.rpw != 4) c.full = false;
   const int bs = block_of(c);
   const int64_t rpb = (int64_t)(bs / c.team) * c.rpw;
   LnFwdArgs a{x, w, b, y, rows, (int32_t)C, eps};
@@ -552,6 +564,8 @@ int vh_layernorm_bwd(const float* x, const float* w, const float* dy, float* dx,
   if (!pick_row_cfg(C, vec, 8, &c))
     return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_bwd: C=" + std::to_string(C) + " exceeds 32768");
   set_ln_bwd_bs(&c);
+  set_ln_full(&c, C);
+  if (c.full && block_of(c) != 1024) c.full = false;
   const int64_t G = ln_bwd_blocks(rows, c);
   const size_t need = align256((size_t)G * 2 * (size_t)C * sizeof(float));
   Scratch sc;
