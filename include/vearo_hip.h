@@ -305,8 +305,10 @@ size_t vh_fused_attention_scratch_bytes(int64_t B, int64_t H, int64_t S, int bac
 /* The backward from the probabilities the forward computed: a caller-supplied
  * forward scratch holds P [B, H, S, S] on return, and passing it here as P skips
  * recomputing it (same results as vh_fused_attention_bwd; P already carries the
- * mask). No counterpart in the reference, whose backward always recomputes;
- * for a training step that keeps the forward's scratch alive.
+ * mask). With causal = 1 the forward leaves the 128 x 128 tiles of P wholly
+ * above the diagonal unwritten and this call does not read them. No
+ * counterpart in the reference, whose backward always recomputes; for a
+ * training step that keeps the forward's scratch alive.
  * scratch: NULL or vh_fused_attention_scratch_bytes(B, H, S, 0) bytes. */
 int vh_fused_attention_bwd_probs(const float* P, const float* q, const vh_layout* ql,
                                  const float* k, const vh_layout* kl, const float* v,

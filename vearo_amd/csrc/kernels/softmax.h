@@ -15,11 +15,23 @@
 // fraction); bwd reads the live prefix of y (or x) and dy, writes dx. All row
 // traffic is non-temporal (single use). Rows are held whole in registers before
 // anything is written, so in == out (in place) is allowed.
+// ztile > 0 (the fused attention's own score block only): the masked zeros of a
+// causal row are written only up to the end of its ztile-row tile, the part
+// the causal products read; the tiles wholly above the diagonal are left as
+// they are (44 % of the row writes at T = 1024).
 // attn = 1 follows the CPU fused attention instead (cpu:2451-2458, 2583-2590):
 // p = e * inv with inv = 1/(sum + 1e-9), and the backward's sum of dy*y is a
 // fused multiply-add chain.
 #pragma once
 #include "common.h"
+
+// End of the columns a row writes, given its live length L (causal: L - 1 is
+// the row's index in its T x T block).
+VH_DEV int zero_end(const SoftmaxArgs& a, int L) {
+  if (!a.causal || a.ztile <= 0) return a.T;
+  const int e = ((L - 1) / a.ztile + 1) * a.ztile;
+  return e < a.T ? e : a.T;
+}
 
 template <int TEAM, int NV, int VW, int RPW>
 VH_DEV void softmax_fwd_impl(const SoftmaxArgs& a) {
@@ -79,10 +91,11 @@ VH_DEV void softmax_fwd_impl(const SoftmaxArgs& a) {
     const float inv = 1.0f / (s + 1e-9f);
     if (active) {
       float* yr = a.y + row * (int64_t)T;
+      const int Z = zero_end(a, L[r]);
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
         const int u = lane + k * TEAM;
-        if (u < U) {
+        if (u < U && u * VW < Z) {
           Unit<VW> o;
 #pragma unroll
           for (int j = 0; j < VW; ++j)
@@ -168,10 +181,11 @@ VH_DEV void softmax_bwd_impl(const SoftmaxArgs& a) {
     dot = team_sum<TEAM>(dot, red);
     if (active) {
       float* dxr = a.y + row * (int64_t)T;
+      const int Z = zero_end(a, L[r]);
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
         const int u = lane + k * TEAM;
-        if (u < U) {
+        if (u < U && u * VW < Z) {
           Unit<VW> o;
 #pragma unroll
           for (int j = 0; j < VW; ++j)

@@ -663,7 +663,7 @@ int vh_gelu_bias_bwd(const float* x, const float* bias, const float* dy, float* 
 
 static int softmax_common(const char* base, int cap, int rpw, const float* in, const float* dy,
                           float* out, int64_t rows, int64_t T, int causal, int input_is_x, hipStream_t s,
-                          int attn = 0) {
+                          int attn = 0, int ztile = 0) {
   RowCfg c;
   const bool vec = aligned16(in) && aligned16(out) && (!dy || aligned16(dy));
   if (!pick_row_cfg(T, vec, cap, &c))
@@ -671,7 +671,7 @@ static int softmax_common(const char* base, int cap, int rpw, const float* in, c
   set_rpw(&c, rpw);
   const int bs = block_of(c);
   const int64_t rpb = (int64_t)(bs / c.team) * c.rpw;
-  SoftmaxArgs a{in, dy, out, rows, (int32_t)T, causal ? 1 : 0, input_is_x ? 1 : 0, attn};
+  SoftmaxArgs a{in, dy, out, rows, (int32_t)T, causal ? 1 : 0, input_is_x ? 1 : 0, attn, ztile};
   return launch(fwd_kernel(base, c), (unsigned)cdiv(rows, rpb), 1, bs, 0, s, a);
 }
 
@@ -1386,7 +1386,9 @@ int attn_probs(const float* q, const vh_layout* ql, const float* k, const vh_lay
   d.alpha = scale;
   d.causal = causal ? VH_GEMM_SKIP_UPPER : VH_GEMM_DENSE;
   VH_TRY(vh_gemm(&d, s));
-  return softmax_common("vh_sm_fwd", 16, kSmFwdRpw, P, nullptr, P, sh.B * sh.H * sh.S, sh.S, causal, 0, s, 1);
+  // The causal products read P only up to the end of each row's C tile.
+  return softmax_common("vh_sm_fwd", 16, kSmFwdRpw, P, nullptr, P, sh.B * sh.H * sh.S, sh.S, causal, 0, s, 1,
+                        VH_GEMM_TILE_M);
 }
 }  // namespace
 
@@ -1424,7 +1426,8 @@ int attn_bwd_from_probs(const float* P, float* G, const float* q, const vh_layou
   d.causal = causal ? VH_GEMM_SKIP_UPPER : VH_GEMM_DENSE;
   VH_TRY(vh_gemm(&d, s));
   // 3. dS = P * (dP - sum(dP * P)) in place over G.
-  VH_TRY(softmax_common("vh_sm_bwd", 8, kSmBwdRpw, P, G, G, sh.B * sh.H * sh.S, sh.S, causal, 0, s, 1));
+  VH_TRY(softmax_common("vh_sm_bwd", 8, kSmBwdRpw, P, G, G, sh.B * sh.H * sh.S, sh.S, causal, 0, s, 1,
+                        VH_GEMM_TILE_M));
   // 4. dq = (dS k) * scale.
   vh_gemm_desc e{};
   e.M = sh.S;

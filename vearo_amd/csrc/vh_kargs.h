@@ -70,6 +70,8 @@ struct SoftmaxArgs {
   int32_t causal;   // 1: row r keeps columns [0, r % T], the rest are known masked
   int32_t input_is_x;
   int32_t attn;     // 1: fused-attention numerics (p = e * (1/(sum + 1e-9)), fma sum of dy*y)
+  int32_t ztile;    // causal, > 0: a row's masked zeros are written only up to the end of
+                    // its ztile-row tile (what the causal products read); 0: the whole row
 };
 
 // C tile of one GEMM workgroup (host and device agree on the grid).
