@@ -1056,6 +1056,43 @@ GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool may_split) {
 }
 }  // namespace
 
+namespace {
+// Kernel arguments for descriptor d from outer batch index b0 on (the pointers
+// advanced to it; the kernel walks the batches from there).
+GemmArgs gemm_args(const vh_gemm_desc* d, int64_t lda, int64_t ldb, int64_t tiles_m, int64_t tiles_n,
+                   int64_t b0 = 0) {
+  GemmArgs g{};
+  g.A = d->a ? d->a + b0 * d->a_sb[0] : nullptr;
+  g.B = d->b ? d->b + b0 * d->b_sb[0] : nullptr;
+  g.C = d->c + b0 * d->c_sb[0];
+  g.E = d->e ? d->e + b0 * d->e_sb[0] : nullptr;
+  g.M = d->M;
+  g.N = d->N;
+  g.K = d->K;
+  g.lda = lda;
+  g.ldb = ldb;
+  g.ldc = d->c_sm;
+  g.sa1 = d->a_sb[0];
+  g.sa2 = d->a_sb[1];
+  g.sb1 = d->b_sb[0];
+  g.sb2 = d->b_sb[1];
+  g.sc1 = d->c_sb[0];
+  g.sc2 = d->c_sb[1];
+  g.se1 = d->e_sb[0];
+  g.se2 = d->e_sb[1];
+  g.sem = d->e_sm;
+  g.sen = d->e_sn;
+  g.nb2 = (int32_t)d->batch[1];
+  g.tiles_m = (int32_t)tiles_m;
+  g.tiles_n = (int32_t)tiles_n;
+  g.accumulate = d->accumulate ? 1 : 0;
+  g.causal = d->causal;
+  g.alpha = d->alpha;
+  g.ksplit = 1;
+  return g;
+}
+}  // namespace
+
 int vh_gemm(const vh_gemm_desc* d, void* stream) {
   VH_TRY(require_init());
   if (!d) return fail(VH_ERR_INVALID, "vh_gemm: null descriptor");
@@ -1104,20 +1141,10 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
     if (ks > 1) {
       void* ws = nullptr;
       VH_TRY(g_arena.alloc((size_t)(ks * M * N) * sizeof(float), &ws));
-      GemmArgs g{};
-      g.A = d->a;
-      g.B = d->b;
-      g.C = d->c;
-      g.M = M;
-      g.N = N;
-      g.K = K;
-      g.lda = lda;
-      g.ldb = ldb;
-      g.ldc = d->c_sm;
-      g.nb2 = 1;
-      g.tiles_m = (int32_t)tiles_m;
-      g.tiles_n = (int32_t)tiles_n;
-      g.alpha = d->alpha;
+      // Raw partials: the reduce applies alpha, the addend and accumulation.
+      GemmArgs g = gemm_args(d, lda, ldb, tiles_m, tiles_n);
+      g.E = nullptr;
+      g.accumulate = 0;
       g.ksplit = (int32_t)ks;
       g.kchunk = kchunk;
       g.ws = static_cast<float*>(ws);
@@ -1140,33 +1167,7 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
   const int64_t nbat = d->batch[0] * d->batch[1];
   if (nbat > 1 && K > 0 && K <= 256 && avec && bvec && !plan.narrow &&
       (d->causal == VH_GEMM_DENSE || (d->causal == VH_GEMM_SKIP_UPPER && tiles_n >= tiles_m))) {
-    GemmArgs g{};
-    g.A = d->a;
-    g.B = d->b;
-    g.C = d->c;
-    g.E = d->e;
-    g.M = M;
-    g.N = N;
-    g.K = K;
-    g.lda = lda;
-    g.ldb = ldb;
-    g.ldc = d->c_sm;
-    g.sa1 = d->a_sb[0];
-    g.sa2 = d->a_sb[1];
-    g.sb1 = d->b_sb[0];
-    g.sb2 = d->b_sb[1];
-    g.sc1 = d->c_sb[0];
-    g.sc2 = d->c_sb[1];
-    g.se1 = d->e_sb[0];
-    g.se2 = d->e_sb[1];
-    g.sem = d->e_sm;
-    g.sen = d->e_sn;
-    g.nb2 = (int32_t)d->batch[1];
-    g.tiles_m = (int32_t)tiles_m;
-    g.tiles_n = (int32_t)tiles_n;
-    g.accumulate = d->accumulate ? 1 : 0;
-    g.causal = d->causal;
-    g.alpha = d->alpha;
+    GemmArgs g = gemm_args(d, lda, ldb, tiles_m, tiles_n);
     g.nbat = nbat;
     const int64_t live = d->causal == VH_GEMM_SKIP_UPPER ? tiles_m * (tiles_m + 1) / 2 : tiles;
     const int64_t slots = 8 * std::max<int64_t>(1, 2 * std::max(g_rt.cu_count, 1) / 8);
@@ -1179,33 +1180,7 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
   if (d->batch[1] > 65535) return fail(VH_ERR_UNSUPPORTED, "vh_gemm: inner batch too large");
   for (int64_t b0 = 0; b0 < d->batch[0]; b0 += outer_chunk) {
     const int64_t nb = std::min(outer_chunk, d->batch[0] - b0);
-    GemmArgs g{};
-    g.A = d->a ? d->a + b0 * d->a_sb[0] : nullptr;
-    g.B = d->b ? d->b + b0 * d->b_sb[0] : nullptr;
-    g.C = d->c + b0 * d->c_sb[0];
-    g.E = d->e ? d->e + b0 * d->e_sb[0] : nullptr;
-    g.M = M;
-    g.N = N;
-    g.K = K;
-    g.lda = lda;
-    g.ldb = ldb;
-    g.ldc = d->c_sm;
-    g.sa1 = d->a_sb[0];
-    g.sa2 = d->a_sb[1];
-    g.sb1 = d->b_sb[0];
-    g.sb2 = d->b_sb[1];
-    g.sc1 = d->c_sb[0];
-    g.sc2 = d->c_sb[1];
-    g.se1 = d->e_sb[0];
-    g.se2 = d->e_sb[1];
-    g.sem = d->e_sm;
-    g.sen = d->e_sn;
-    g.nb2 = (int32_t)d->batch[1];
-    g.tiles_m = (int32_t)tiles_m;
-    g.tiles_n = (int32_t)tiles_n;
-    g.accumulate = d->accumulate ? 1 : 0;
-    g.causal = d->causal;
-    g.alpha = d->alpha;
+    const GemmArgs g = gemm_args(d, lda, ldb, tiles_m, tiles_n, b0);
     VH_TRY(launch(name, (unsigned)(tiles_m * tiles_n), (unsigned)(nb * d->batch[1]), 256, 0, s, g));
   }
   return VH_OK;
