@@ -63,9 +63,13 @@ def test_matmul_reference_kats(vh):
     assert run_matmul(vh, a, b.T, b_view="T").tolist() == O.matmul(a, b.T).tolist()
 
 
+# N <= 64 takes the 128 x 64 tile; with 128-bit loads its k tiles run two
+# steps ahead in pairs: (128, 32, 64) one step, (256, 96, 64) and
+# (384, 160, 64) odd step counts, (200, 288, 60) edge tiles with the checked loop.
 @pytest.mark.parametrize("M,K,N", [(1, 1, 1), (5, 7, 3), (128, 32, 128), (129, 33, 131),
                                    (300, 768, 200), (64, 1000, 96), (257, 64, 513),
-                                   (300, 200, 64), (257, 96, 33), (1024, 1024, 64)])
+                                   (300, 200, 64), (257, 96, 33), (1024, 1024, 64),
+                                   (128, 32, 64), (256, 96, 64), (384, 160, 64), (200, 288, 60)])
 def test_matmul_shapes(vh, M, K, N):
     """Parity at the block step's scale (activations ~N(0,1), weights
     ~N(0,0.02)); and, with both operands ~N(0,1), the error bound every f32

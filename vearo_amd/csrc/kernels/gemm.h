@@ -271,52 +271,87 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
   constexpr int WR = (A_VEC ? GM_TM / 32 : GM_TM / 8) + (B_VEC ? TN / 32 : TN / 8);  // LDS writes per tile
   constexpr int VM = (A_VEC ? GM_TM / 32 : GM_TM / 8) + (B_VEC ? TN / 32 : TN / 8);  // global loads per tile
   constexpr int MF = 8 * NTW;                                                   // products per 4-k group
+  // One k step on the k tile staged in stage sc: the loads of k tile kl go
+  // out into (la, lb), this tile's products run, and (wa, wb) -- the k tile
+  // that follows this one -- are staged into the other LDS buffers.
+  auto kstep = [&](auto unchecked, int sc, float (&la)[GM_TM / 8], float (&lb)[TN / 8],
+                   const float (&wa)[GM_TM / 8], const float (&wb)[TN / 8], int64_t kl, bool load) {
+    constexpr bool CHECK = !decltype(unchecked)::value;
+    if constexpr (CHECK) {
+      if (load) {
+        gm_load<A_KC, A_VEC, GM_TM>(A, a.lda, m0, a.M, kl, a.K, tid, la);
+        gm_load<B_KC, B_VEC, TN>(B, a.ldb, n0, a.N, kl, a.K, tid, lb);
+      }
+    } else {
+      gm_load<A_KC, A_VEC, GM_TM, false>(A, a.lda, m0, a.M, kl, a.K, tid, la);
+      gm_load<B_KC, B_VEC, TN, false>(B, a.ldb, n0, a.N, kl, a.K, tid, lb);
+    }
+    vh_f4 fa[4][2], fb[4][NTW];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int kc = h * 16 + 4 * q;
+      fa[q][0] = gm_frag<A_KC>(L[sc], wm * 64 + li, kc);
+      fa[q][1] = gm_frag<A_KC>(L[sc], wm * 64 + 32 + li, kc);
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) fb[q][nt] = gm_frag<B_KC>(L[2 + sc], wn * (TN / 2) + nt * 32 + li, kc);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) {
+          acc[0][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][0][e], fb[q][nt][e], acc[0][nt], 0, 0, 0);
+          acc[1][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][1][e], fb[q][nt][e], acc[1][nt], 0, 0, 0);
+        }
+      }
+    }
+    gm_store_lds<A_KC, A_VEC, GM_TM>(L[sc ^ 1], tid, wa);
+    gm_store_lds<B_KC, B_VEC, TN>(L[2 + (sc ^ 1)], tid, wb);
+    if constexpr (!CHECK) __builtin_amdgcn_sched_group_barrier(0x020, VM, 0);  // the loads
+    __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);                        // all fragment reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 3 * MF, 0);                    // groups 0-2
+#pragma unroll
+    for (int i = 0; i < MF; ++i) {  // group 3 with the writes
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x200, (WR + MF - 1) / MF, 0);
+    }
+    __syncthreads();
+  };
+  // 128 x 128 tiles: the next k tile's loads are in flight during one step
+  // (1.7 us of products). 128 x 64 tiles have half the products per step, less
+  // than the load latency under load, so with 128-bit loads (registers to
+  // spare) theirs run two steps ahead through a second register set: step 0
+  // of a pair computes stage 0, loads k tile k0+64 into (sa, sb) and stages
+  // (sa2, sb2) = k0+32; step 1 the reverse. Unchecked loads past the range
+  // fetch the last k tile again.
+  constexpr bool DEEP = TN == 64 && A_VEC && B_VEC;
   auto main_loop = [&](auto unchecked) {
     constexpr bool CHECK = !decltype(unchecked)::value;
-    for (int64_t k0 = kb; k0 < ke; k0 += GM_TK) {
-      const bool more = k0 + GM_TK < ke;
-      if constexpr (CHECK) {
-        if (more) {
-          gm_load<A_KC, A_VEC, GM_TM>(A, a.lda, m0, a.M, k0 + GM_TK, a.K, tid, sa);
-          gm_load<B_KC, B_VEC, TN>(B, a.ldb, n0, a.N, k0 + GM_TK, a.K, tid, sb);
-        }
-      } else {
-        const int64_t kn = more ? k0 + GM_TK : k0;
-        gm_load<A_KC, A_VEC, GM_TM, false>(A, a.lda, m0, a.M, kn, a.K, tid, sa);
-        gm_load<B_KC, B_VEC, TN, false>(B, a.ldb, n0, a.N, kn, a.K, tid, sb);
+    auto kn = [&](int64_t k) { return CHECK || k < ke ? k : ke - GM_TK; };
+    if constexpr (!DEEP) {
+      for (int64_t k0 = kb; k0 < ke; k0 += GM_TK) {
+        kstep(unchecked, s, sa, sb, sa, sb, kn(k0 + GM_TK), k0 + GM_TK < ke);
+        s ^= 1;
       }
-      vh_f4 fa[4][2], fb[4][NTW];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int kc = h * 16 + 4 * q;
-        fa[q][0] = gm_frag<A_KC>(L[s], wm * 64 + li, kc);
-        fa[q][1] = gm_frag<A_KC>(L[s], wm * 64 + 32 + li, kc);
-#pragma unroll
-        for (int nt = 0; nt < NTW; ++nt) fb[q][nt] = gm_frag<B_KC>(L[2 + s], wn * (TN / 2) + nt * 32 + li, kc);
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-#pragma unroll
-          for (int nt = 0; nt < NTW; ++nt) {
-            acc[0][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][0][e], fb[q][nt][e], acc[0][nt], 0, 0, 0);
-            acc[1][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q][1][e], fb[q][nt][e], acc[1][nt], 0, 0, 0);
+    } else {
+      float sa2[GM_TM / 8] = {}, sb2[TN / 8] = {};
+      if (kb < ke) {
+        if constexpr (CHECK) {
+          if (kb + GM_TK < ke) {
+            gm_load<A_KC, A_VEC, GM_TM>(A, a.lda, m0, a.M, kb + GM_TK, a.K, tid, sa2);
+            gm_load<B_KC, B_VEC, TN>(B, a.ldb, n0, a.N, kb + GM_TK, a.K, tid, sb2);
           }
+        } else {
+          gm_load<A_KC, A_VEC, GM_TM, false>(A, a.lda, m0, a.M, kn(kb + GM_TK), a.K, tid, sa2);
+          gm_load<B_KC, B_VEC, TN, false>(B, a.ldb, n0, a.N, kn(kb + GM_TK), a.K, tid, sb2);
         }
       }
-      gm_store_lds<A_KC, A_VEC, GM_TM>(L[s ^ 1], tid, sa);
-      gm_store_lds<B_KC, B_VEC, TN>(L[2 + (s ^ 1)], tid, sb);
-      if constexpr (!CHECK) __builtin_amdgcn_sched_group_barrier(0x020, VM, 0);  // the next tile's loads
-      __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);                        // all fragment reads
-      __builtin_amdgcn_sched_group_barrier(0x008, 3 * MF, 0);                    // groups 0-2
-#pragma unroll
-      for (int i = 0; i < MF; ++i) {  // group 3 with the writes
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x200, (WR + MF - 1) / MF, 0);
+      for (int64_t k0 = kb; k0 < ke; k0 += 2 * GM_TK) {
+        kstep(unchecked, 0, sa, sb, sa2, sb2, kn(k0 + 2 * GM_TK), k0 + 2 * GM_TK < ke);
+        if (k0 + GM_TK >= ke) break;
+        kstep(unchecked, 1, sa2, sb2, sa, sb, kn(k0 + 3 * GM_TK), k0 + 3 * GM_TK < ke);
       }
-      __syncthreads();
-      s ^= 1;
     }
   };
   const bool inside = m0 + GM_TM <= a.M && n0 + TN <= a.N && (ke - kb) % GM_TK == 0 && ke <= a.K;
