@@ -192,7 +192,8 @@ def test_gemm_persistent_short_k(vh, akc, bkc):
     items than resident workgroups (the 120-batch cases)."""
     r = np.random.default_rng(11)
     cases = ((3, 5, 200, 300, 40, 0, "full", 0), (2, 3, 300, 300, 64, 1, None, 1),
-             (6, 20, 384, 384, 64, 1, None, 0), (4, 30, 256, 384, 96, 0, "bias", 1))
+             (6, 20, 384, 384, 64, 1, None, 0), (4, 30, 256, 384, 96, 0, "bias", 1),
+             (2, 2, 256, 384, 64, 1, "full", 1))
     for B0, B1, M, N, K, causal, ekind, acc in cases:
         a = r.standard_normal((B0, B1, M, K), dtype=np.float32)
         b = (r.standard_normal((B0, B1, K, N)) * 0.1).astype(np.float32)
@@ -229,8 +230,8 @@ def test_gemm_persistent_short_k(vh, akc, bkc):
             cpu = c0 + cpu
             ref64 = c0 + ref64
         name = f"persistent {B0}x{B1} {M}x{N}x{K} causal={causal} e={ekind} acc={acc} akc={akc} bkc={bkc}"
-        if causal:
-            il = np.tril_indices(M)
+        if causal:  # entries on and below the diagonal are defined
+            il = np.tril_indices(M, 0, N)
             got, cpu, ref64 = got[..., il[0], il[1]], cpu[..., il[0], il[1]], ref64[..., il[0], il[1]]
         assert_parity(got, cpu, ref64, name=name)
         del keep
