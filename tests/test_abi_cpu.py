@@ -108,7 +108,7 @@ def launcher_kernel_names():
         for v in nv:
             names |= {f"vh_gelu_bias_fwd_n{v}_v{vw}", f"vh_gelu_bias_bwd_n{v}_v{vw}"}
         names |= {f"vh_gelu_fwd_v{vw}", f"vh_gelu_gradmul_v{vw}", f"vh_emb_fwd_v{vw}",
-                  f"vh_emb_rows_v{vw}", f"vh_binary_contig_v{vw}"}
+                  f"vh_emb_rows_v{vw}", f"vh_emb_heavy_final_v{vw}", f"vh_binary_contig_v{vw}"}
     for v in list(range(8, 129, 8)) + [99]:
         names |= {f"vh_xent_fwd_n{v}", f"vh_xent_bwd_n{v}", f"vh_xent_fb_n{v}"}
     names |= {"vh_xent_fwd_stream", "vh_xent_bwd_stream", "vh_xent_reduce", "vh_col_reduce",

@@ -16,16 +16,22 @@
 //   3. emb_place  : light positions drop into their row's 16 fixed slots; heavy
 //                   hits are counted per block of positions (512 or more)
 //   4. emb_rows   : the leading workgroups run heavy tasks while the rest stream
-//      + heavy      the vocabulary rows, one wave per row: zeros for an unused
+//                   the vocabulary rows, one wave per row: zeros for an unused
 //                   row; for a light row, its <= 16 positions sorted in registers
 //                   and the dy rows added in ascending position order from 0.0 --
 //                   the CPU loop's exact f32 order, so those rows are bit-exact.
 //                   A heavy task gathers the positions of its 32 ranks (visiting
-//                   only blocks that hold them), sums their rows in order into a
-//                   partial row; the last task of each group of 8 adds the group's
-//                   partials in order, and the last group adds the group sums in
-//                   order into dW (a fixed grouping of the same sum:
-//                   deterministic, within f32 rounding of the CPU's order).
+//                   only blocks that hold them) and sums their rows in order into
+//                   a partial row, as one wave per 64-unit column slice (one unit
+//                   per lane, 16 rows in flight).
+//   5. emb_heavy_final: one wave per (heavy row, column slice) adds the row's
+//                   partials: each group of 8 in task order, then the group sums
+//                   in group order, into dW (a fixed grouping of the same sum:
+//                   deterministic, within f32 rounding of the CPU's order). A
+//                   kernel of its own: an in-kernel completion tree needs
+//                   device-scope fences, and on this GPU each one writes back
+//                   and invalidates an XCD's whole L2 (measured: they made the
+//                   Zipf case 1.8x slower once the tasks were split in slices).
 #pragma once
 #include "common.h"
 
@@ -133,8 +139,8 @@ VH_DEV void emb_tokens_impl(const EmbTokArgs& a) {
 }
 
 // Step 2. One thread per vocabulary row. Rows with more than EMB_LIGHT hits are
-// registered as heavy: an entry, a run of ceil(hits/32) tasks, a zeroed
-// per-block hit-count row and zeroed completion counters. Entries and tasks are
+// registered as heavy: an entry, a run of ceil(hits/32) tasks and a zeroed
+// per-block hit-count row. Entries and tasks are
 // claimed with one atomic per wave (a wave prefix sum, then one atomicAdd of the
 // totals); their order varies run to run but no row's result depends on it.
 VH_DEV void emb_alloc_impl(const EmbAllocArgs& a) {
@@ -168,12 +174,8 @@ VH_DEV void emb_alloc_impl(const EmbAllocArgs& a) {
     a.heavy[4 * h + 1] = tb;
     a.heavy[4 * h + 2] = nch;
     a.heavy[4 * h + 3] = c;
-    for (int32_t k = 0; k < nch; ++k) {
-      a.taskmap[tb + k] = h;
-      a.gdone[tb + k] = 0;
-    }
+    for (int32_t k = 0; k < nch; ++k) a.taskmap[tb + k] = h;
     for (int32_t b = 0; b < a.nblk; ++b) a.blkcnt[(int64_t)h * a.nblk + b] = 0;
-    a.hdone[h] = 0;
   }
   a.heavy_index[v] = h;
 }
@@ -220,42 +222,59 @@ VH_DEV int nth_set_bit(unsigned long long m, int n) {
   return pos;
 }
 
-// dst = sum over c < cnt of rows base + c * stride, added in c order from 0.0.
-template <int VW>
-VH_DEV void emb_sum_rows(const float* base, int64_t stride, int cnt, float* dst, bool stream_out, int lane,
-                         int U) {
-  for (int u0 = 0; u0 < U; u0 += 64 * EMB_Q) {
-    Unit<VW> acc[EMB_Q];
+#define EMB_BATCH 16  // rows in flight per lane in a heavy task's slice
+
+// acc += rows[r] at unit u (one unit per lane) for the first `cnt` of R rows, in
+// row order; all R loads are issued before any add. NT as in emb_add_rows.
+template <int VW, bool NT, int R>
+VH_DEV void emb_add_slice(Unit<VW>& acc, const float* const (&src)[R], int cnt, int u, int U) {
+  Unit<VW> d[R];
 #pragma unroll
-    for (int q = 0; q < EMB_Q; ++q) acc[q] = zero_unit<VW>();
-    for (int c = 0; c < cnt; c += 4) {
-      const float* src[4];
+  for (int r = 0; r < R; ++r) {
+    if (r < cnt && u < U)
+      d[r] = NT ? load_stream<VW>(src[r] + u * VW) : load_unit<VW>(src[r] + u * VW);
+    else
+      d[r] = zero_unit<VW>();
+  }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) src[r] = base + (int64_t)(c + r < cnt ? c + r : c) * stride;
-      emb_add_rows<VW, false>(acc, src, cnt - c < 4 ? cnt - c : 4, u0, lane, U);
-    }
+  for (int r = 0; r < R; ++r) {
+    if (r < cnt) {
 #pragma unroll
-    for (int q = 0; q < EMB_Q; ++q) {
-      const int u = u0 + lane + q * 64;
-      if (u < U) {
-        if (stream_out)
-          store_stream<VW>(dst + u * VW, acc[q]);
-        else
-          store_unit<VW>(dst + u * VW, acc[q]);
-      }
+      for (int j = 0; j < VW; ++j) acc.v[j] += d[r].v[j];
     }
   }
 }
 
-// Heavy task k: the hits of rank [32c, 32c+32) of its token (ranks in position
-// order). Lane j first gathers the position of the j-th of them, visiting only
-// blocks whose hit count overlaps the rank window; then the dy rows are summed
-// in position order into partial[k]. Completion is a two-level tree in fixed
-// order: the last task of each group of EMB_GROUP sums the group's partials
-// into the group's first slot, the last group sums the group slots into dW.
+// dst at unit u = sum over c < cnt of rows base + c * stride at unit u, added
+// in c order from 0.0.
 template <int VW>
-VH_DEV void emb_heavy_task(const EmbSegArgs& a, int64_t k, int lane) {
+VH_DEV void emb_sum_slice(const float* base, int64_t stride, int cnt, float* dst, bool stream_out, int u, int U) {
+  Unit<VW> acc = zero_unit<VW>();
+  for (int c = 0; c < cnt; c += EMB_BATCH) {
+    const float* src[EMB_BATCH];
+#pragma unroll
+    for (int r = 0; r < EMB_BATCH; ++r) src[r] = base + (int64_t)(c + r < cnt ? c + r : c) * stride;
+    emb_add_slice<VW, false, EMB_BATCH>(acc, src, cnt - c < EMB_BATCH ? cnt - c : EMB_BATCH, u, U);
+  }
+  if (u < U) {
+    if (stream_out)
+      store_stream<VW>(dst + u * VW, acc);
+    else
+      store_unit<VW>(dst + u * VW, acc);
+  }
+}
+
+// Heavy work item = (task k, column slice sl): task k covers the hits of rank
+// [32c, 32c+32) of its token (ranks in position order). Lane j first gathers
+// the position of the j-th of them, visiting only blocks whose hit count
+// overlaps the rank window; then the dy rows are summed in position order into
+// the slice's columns of partial[k], lane l owning unit 64 sl + l.
+template <int VW>
+VH_DEV void emb_heavy_task(const EmbSegArgs& a, int64_t item, int lane) {
   const int U = a.D / VW;
+  const int64_t k = item / a.slices;
+  const int sl = (int)(item % a.slices);
+  const int u = sl * 64 + lane;
   const int32_t h = a.taskmap[k];
   const int32_t tok = a.heavy[4 * h + 0], tb = a.heavy[4 * h + 1], nch = a.heavy[4 * h + 2];
   const int32_t m = a.heavy[4 * h + 3];
@@ -307,51 +326,19 @@ VH_DEV void emb_heavy_task(const EmbSegArgs& a, int64_t k, int lane) {
     rr += __shfl(inc, 63, 64);
   }
   float* part = a.partial + k * (int64_t)a.D;
-  for (int u0 = 0; u0 < U; u0 += 64 * EMB_Q) {
-    Unit<VW> acc[EMB_Q];
+  Unit<VW> acc = zero_unit<VW>();
+  for (int j = 0; j < got; j += EMB_BATCH) {  // ascending positions, 16 rows per batch
+    const float* src[EMB_BATCH];
 #pragma unroll
-    for (int q = 0; q < EMB_Q; ++q) acc[q] = zero_unit<VW>();
-    for (int j = 0; j < got; j += 4) {  // ascending positions, 4 rows per batch
-      const float* src[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) src[r] = a.dy + (int64_t)__shfl(mypos, j + r < got ? j + r : j, 64) * a.D;
-      emb_add_rows<VW, true>(acc, src, got - j < 4 ? got - j : 4, u0, lane, U);
-    }
-#pragma unroll
-    for (int q = 0; q < EMB_Q; ++q) {
-      const int u = u0 + lane + q * 64;
-      if (u < U) store_unit<VW>(part + u * VW, acc[q]);
-    }
+    for (int r = 0; r < EMB_BATCH; ++r) src[r] = a.dy + (int64_t)__shfl(mypos, j + r < got ? j + r : j, 64) * a.D;
+    emb_add_slice<VW, true, EMB_BATCH>(acc, src, got - j < EMB_BATCH ? got - j : EMB_BATCH, u, U);
   }
-  // Level 1: the group's last task sums the group's partials in task order.
-  const int32_t g = c / EMB_GROUP;
-  const int32_t g0 = tb + g * EMB_GROUP;
-  const int32_t gsize = min(EMB_GROUP, nch - g * EMB_GROUP);
-  const int32_t ngrp = (nch + EMB_GROUP - 1) / EMB_GROUP;
-  __threadfence();
-  int32_t done = 0;
-  if (lane == 0) done = atomicAdd(&a.gdone[g0], 1);
-  done = __shfl(done, 0, 64);
-  if (done != gsize - 1) return;
-  __threadfence();
-  float* row = a.dW + (int64_t)tok * a.D;
-  if (ngrp == 1) {
-    emb_sum_rows<VW>(a.partial + (int64_t)g0 * a.D, a.D, gsize, row, true, lane, U);
-    return;
-  }
-  // Each lane reads its own units of slot g0 before it overwrites them.
-  emb_sum_rows<VW>(a.partial + (int64_t)g0 * a.D, a.D, gsize, a.partial + (int64_t)g0 * a.D, false, lane, U);
-  // Level 2: the last group sums the group slots in group order.
-  __threadfence();
-  if (lane == 0) done = atomicAdd(&a.hdone[h], 1);
-  done = __shfl(done, 0, 64);
-  if (done != ngrp - 1) return;
-  __threadfence();
-  emb_sum_rows<VW>(a.partial + (int64_t)tb * a.D, (int64_t)EMB_GROUP * a.D, ngrp, row, true, lane, U);
+  if (u < U) store_unit<VW>(part + u * VW, acc);
 }
 
-// Step 4. Blocks [0, heavy_blocks): heavy tasks, one per wave, strided over the
-// device-side task count; dispatched first, so they overlap the row stream.
+// Step 4. Blocks [0, heavy_blocks): heavy work items (task, column slice), one
+// per wave, strided over the device-side task count times the slices;
+// dispatched first, so they overlap the row stream.
 // Blocks beyond: one wave per vocabulary row (zeros, or a light row's bit-exact
 // sequential sum; heavy rows are left to their tasks).
 template <int VW>
@@ -387,6 +374,39 @@ VH_DEV void emb_rows_impl(const EmbSegArgs& a) {
   }
   const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int64_t nworkers = (int64_t)a.heavy_blocks * 4;
-  const int32_t ntasks = a.ctr[1];
-  for (int64_t k = wid; k < ntasks; k += nworkers) emb_heavy_task<VW>(a, k, lane);
+  const int64_t nitems = (int64_t)a.ctr[1] * a.slices;
+  for (int64_t k = wid; k < nitems; k += nworkers) emb_heavy_task<VW>(a, k, lane);
+}
+
+// Step 5. Wave w = (heavy entry h, column slice sl), over the device-side count
+// of heavy entries: dW[tok] at the slice's units = sum over groups (in order,
+// from 0.0) of the group's partials summed in task order from 0.0; a row with
+// one group takes that group's sum as it is.
+template <int VW>
+VH_DEV void emb_heavy_final_impl(const EmbFinalArgs& a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t h = w / a.slices;
+  if (h >= a.ctr[0]) return;
+  const int U = a.D / VW;
+  const int u = (int)(w % a.slices) * 64 + lane;
+  const int32_t tok = a.heavy[4 * h + 0], tb = a.heavy[4 * h + 1], nch = a.heavy[4 * h + 2];
+  const int32_t ngrp = (nch + EMB_GROUP - 1) / EMB_GROUP;
+  Unit<VW> total = zero_unit<VW>();
+  for (int32_t g = 0; g < ngrp; ++g) {
+    const int32_t gsize = min(EMB_GROUP, nch - g * EMB_GROUP);
+    const float* src[EMB_GROUP];
+#pragma unroll
+    for (int r = 0; r < EMB_GROUP; ++r)
+      src[r] = a.partial + (int64_t)(tb + g * EMB_GROUP + (r < gsize ? r : 0)) * a.D;
+    Unit<VW> gs = zero_unit<VW>();
+    emb_add_slice<VW, false, EMB_GROUP>(gs, src, gsize, u, U);
+    if (ngrp == 1) {
+      total = gs;
+    } else {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) total.v[j] += gs.v[j];
+    }
+  }
+  if (u < U) store_stream<VW>(a.dW + (int64_t)tok * a.D + u * VW, total);
 }

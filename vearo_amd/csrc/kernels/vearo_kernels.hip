@@ -130,6 +130,8 @@ extern "C" __global__ void __launch_bounds__(256) vh_emb_alloc(EmbAllocArgs a) {
 extern "C" __global__ void __launch_bounds__(256) vh_emb_place(EmbPlaceArgs a) { emb_place_impl(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_emb_rows_v1(EmbSegArgs a) { emb_rows_impl<1>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_emb_rows_v4(EmbSegArgs a) { emb_rows_impl<4>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_emb_heavy_final_v1(EmbFinalArgs a) { emb_heavy_final_impl<1>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_emb_heavy_final_v4(EmbFinalArgs a) { emb_heavy_final_impl<4>(a); }
 
 // Cross-entropy
 // Up to NV = 104 (V <= 53,248) the kernels are held to 128 VGPRs: 4 waves per

@@ -722,8 +722,7 @@ constexpr int64_t kEmbLight = 16, kEmbChunkHits = 32;
 constexpr int kEmbMinBlkShift = 9;
 constexpr int64_t kEmbMaxBlkTable = int64_t(1) << 22;
 struct EmbScratchLayout {
-  size_t tok, counts, cursor, ctr, zero_end, heavy_index, heavy, taskmap, hdone, gdone, blkcnt, pos, partial,
-      total;
+  size_t tok, counts, cursor, ctr, zero_end, heavy_index, heavy, taskmap, blkcnt, pos, partial, total;
   int64_t nblk;
   int blk_shift;
 };
@@ -748,8 +747,6 @@ EmbScratchLayout emb_layout(int64_t n, int64_t V, int64_t D) {
   L.heavy_index = take((size_t)V);
   L.heavy = take(4 * (size_t)heavy_max);
   L.taskmap = take((size_t)tasks_max);
-  L.hdone = take((size_t)heavy_max);
-  L.gdone = take((size_t)tasks_max);
   L.blkcnt = take((size_t)heavy_max * (size_t)L.nblk);
   L.pos = take((size_t)V * kEmbLight);
   L.partial = take((size_t)tasks_max * (size_t)D);
@@ -784,20 +781,27 @@ int vh_embedding_bwd(const float* ids, const float* dy, float* dW, int64_t n, in
   EmbTokArgs k1{ids, I(L.tok), I(L.counts), g_rt.err, n, (int32_t)V};
   VH_TRY(launch("vh_emb_tokens", (unsigned)cdiv(n, 256), 1, 256, 0, s, k1));
   if (V == 0 || D == 0) return VH_OK;  // ids validated, nothing to write
-  EmbAllocArgs k2{I(L.counts), I(L.heavy_index), I(L.heavy), I(L.taskmap), I(L.blkcnt), I(L.hdone),
-                  I(L.gdone), I(L.ctr), (int32_t)V, (int32_t)L.nblk};
+  const bool vec = D % 4 == 0 && aligned16(dy) && aligned16(dW);
+  const int32_t slices = (int32_t)cdiv(D / (vec ? 4 : 1), 64);  // 64-unit column slices of a heavy row
+  EmbAllocArgs k2{I(L.counts), I(L.heavy_index), I(L.heavy), I(L.taskmap), I(L.blkcnt), I(L.ctr), (int32_t)V,
+                  (int32_t)L.nblk};
   VH_TRY(launch("vh_emb_alloc", (unsigned)cdiv(V, 256), 1, 256, 0, s, k2));
   EmbPlaceArgs k3{I(L.tok), I(L.heavy_index), I(L.cursor), I(L.pos), I(L.blkcnt), n, (int32_t)L.nblk,
                   L.blk_shift};
   VH_TRY(launch("vh_emb_place", (unsigned)cdiv(n, 256), 1, 256, 0, s, k3));
-  const bool vec = D % 4 == 0 && aligned16(dy) && aligned16(dW);
-  // Up to 1024 worker waves for heavy tasks (there are at most tasks_max).
-  const int64_t heavy_blocks = std::min<int64_t>(256, cdiv(n / kEmbChunkHits + n / (kEmbLight + 1) + 2, 4));
-  EmbSegArgs k4{I(L.counts), I(L.pos), I(L.tok), I(L.heavy), I(L.taskmap), I(L.blkcnt), I(L.hdone),
-                I(L.gdone), I(L.ctr), reinterpret_cast<float*>(base + L.partial), dy, dW, n, (int32_t)V,
-                (int32_t)D, (int32_t)L.nblk, L.blk_shift, (int32_t)heavy_blocks};
-  return launch(vec ? "vh_emb_rows_v4" : "vh_emb_rows_v1", (unsigned)(heavy_blocks + cdiv(V, 4)), 1, 256, 0,
-                s, k4);
+  // Up to 2048 worker waves for the heavy work items (at most tasks_max x slices).
+  const int64_t heavy_blocks =
+      std::min<int64_t>(512, cdiv((n / kEmbChunkHits + n / (kEmbLight + 1) + 2) * slices, 4));
+  float* partial = reinterpret_cast<float*>(base + L.partial);
+  EmbSegArgs k4{I(L.counts), I(L.pos), I(L.tok), I(L.heavy), I(L.taskmap), I(L.blkcnt), I(L.ctr), partial,
+                dy, dW, n, (int32_t)V, (int32_t)D, (int32_t)L.nblk, L.blk_shift, (int32_t)heavy_blocks, slices};
+  VH_TRY(launch(vec ? "vh_emb_rows_v4" : "vh_emb_rows_v1", (unsigned)(heavy_blocks + cdiv(V, 4)), 1, 256, 0,
+                s, k4));
+  // One wave per (possible heavy entry, slice); waves past the device-side count return.
+  const int64_t heavy_max = n / (kEmbLight + 1) + 1;
+  EmbFinalArgs k5{I(L.heavy), I(L.ctr), partial, dW, (int32_t)D, slices};
+  return launch(vec ? "vh_emb_heavy_final_v4" : "vh_emb_heavy_final_v1", (unsigned)cdiv(heavy_max * slices, 4), 1,
+                256, 0, s, k5);
 }
 
 // --------------------------------------------------------- cross-entropy --

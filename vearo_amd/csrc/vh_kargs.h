@@ -170,8 +170,6 @@ struct EmbAllocArgs {
   int32_t* heavy;         // [4 * max] token, first task, task count, hits
   int32_t* taskmap;       // [tasks] heavy entry of each task
   int32_t* blkcnt;        // [max][nblk] heavy hits per position block
-  int32_t* hdone;         // [max] finished task groups per heavy entry
-  int32_t* gdone;         // [tasks] finished tasks per group of 8 (at the group's first task)
   int32_t* ctr;           // [2]: heavy entries, tasks (zeroed by the host)
   int32_t V;
   int32_t nblk;
@@ -195,8 +193,6 @@ struct EmbSegArgs {
   const int32_t* heavy;
   const int32_t* taskmap;
   const int32_t* blkcnt;
-  int32_t* hdone;
-  int32_t* gdone;
   const int32_t* ctr;
   float* partial;  // [tasks][D] heavy partial rows
   const float* dy;
@@ -207,6 +203,17 @@ struct EmbSegArgs {
   int32_t nblk;
   int32_t blk_shift;
   int32_t heavy_blocks;  // leading workgroups that run heavy tasks
+  int32_t slices;        // column slices per heavy task (64 units of VW floats each)
+};
+
+// Heavy rows' final sums: one wave per (heavy entry, column slice).
+struct EmbFinalArgs {
+  const int32_t* heavy;   // [4 * max] token, first task, task count, hits
+  const int32_t* ctr;     // [0]: heavy entries
+  const float* partial;   // [tasks][D]
+  float* dW;
+  int32_t D;
+  int32_t slices;
 };
 
 struct XentArgs {
