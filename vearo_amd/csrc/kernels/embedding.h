@@ -378,35 +378,60 @@ VH_DEV void emb_rows_impl(const EmbSegArgs& a) {
   for (int64_t k = wid; k < nitems; k += nworkers) emb_heavy_task<VW>(a, k, lane);
 }
 
-// Step 5. Wave w = (heavy entry h, column slice sl), over the device-side count
-// of heavy entries: dW[tok] at the slice's units = sum over groups (in order,
-// from 0.0) of the group's partials summed in task order from 0.0; a row with
-// one group takes that group's sum as it is.
+// Step 5. Work item w = (heavy entry h, column slice sl), one wave at a time,
+// strided over the device-side count of heavy entries: dW[tok] at the slice's
+// units = sum over groups (in order, from 0.0) of the group's partials summed
+// in task order from 0.0; a row with one group takes that group's sum as it
+// is. Four groups' partials are loaded at once.
+#define EMB_FINAL_GROUPS 4
 template <int VW>
 VH_DEV void emb_heavy_final_impl(const EmbFinalArgs& a) {
   const int lane = threadIdx.x & 63;
-  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t h = w / a.slices;
-  if (h >= a.ctr[0]) return;
   const int U = a.D / VW;
-  const int u = (int)(w % a.slices) * 64 + lane;
-  const int32_t tok = a.heavy[4 * h + 0], tb = a.heavy[4 * h + 1], nch = a.heavy[4 * h + 2];
-  const int32_t ngrp = (nch + EMB_GROUP - 1) / EMB_GROUP;
-  Unit<VW> total = zero_unit<VW>();
-  for (int32_t g = 0; g < ngrp; ++g) {
-    const int32_t gsize = min(EMB_GROUP, nch - g * EMB_GROUP);
-    const float* src[EMB_GROUP];
+  const int64_t nitems = (int64_t)a.ctr[0] * a.slices;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); w < nitems; w += nwaves) {
+    const int64_t h = w / a.slices;
+    const int u = (int)(w % a.slices) * 64 + lane;
+    const int32_t tok = a.heavy[4 * h + 0], tb = a.heavy[4 * h + 1], nch = a.heavy[4 * h + 2];
+    const int32_t ngrp = (nch + EMB_GROUP - 1) / EMB_GROUP;
+    Unit<VW> total = zero_unit<VW>();
+    for (int32_t g0 = 0; g0 < ngrp; g0 += EMB_FINAL_GROUPS) {
+      Unit<VW> d[EMB_FINAL_GROUPS][EMB_GROUP];
 #pragma unroll
-    for (int r = 0; r < EMB_GROUP; ++r)
-      src[r] = a.partial + (int64_t)(tb + g * EMB_GROUP + (r < gsize ? r : 0)) * a.D;
-    Unit<VW> gs = zero_unit<VW>();
-    emb_add_slice<VW, false, EMB_GROUP>(gs, src, gsize, u, U);
-    if (ngrp == 1) {
-      total = gs;
-    } else {
+      for (int q = 0; q < EMB_FINAL_GROUPS; ++q) {
+        const int32_t g = g0 + q;
+        const int32_t gsize = g < ngrp ? min(EMB_GROUP, nch - g * EMB_GROUP) : 0;
 #pragma unroll
-      for (int j = 0; j < VW; ++j) total.v[j] += gs.v[j];
+        for (int r = 0; r < EMB_GROUP; ++r) {
+          if (r < gsize && u < U)
+            d[q][r] = load_unit<VW>(a.partial + (int64_t)(tb + g * EMB_GROUP + r) * a.D + u * VW);
+          else
+            d[q][r] = zero_unit<VW>();
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < EMB_FINAL_GROUPS; ++q) {
+        const int32_t g = g0 + q;
+        if (g < ngrp) {
+          const int32_t gsize = min(EMB_GROUP, nch - g * EMB_GROUP);
+          Unit<VW> gs = zero_unit<VW>();
+#pragma unroll
+          for (int r = 0; r < EMB_GROUP; ++r) {
+            if (r < gsize) {
+#pragma unroll
+              for (int j = 0; j < VW; ++j) gs.v[j] += d[q][r].v[j];
+            }
+          }
+          if (ngrp == 1) {
+            total = gs;
+          } else {
+#pragma unroll
+            for (int j = 0; j < VW; ++j) total.v[j] += gs.v[j];
+          }
+        }
+      }
     }
+    if (u < U) store_stream<VW>(a.dW + (int64_t)tok * a.D + u * VW, total);
   }
-  if (u < U) store_stream<VW>(a.dW + (int64_t)tok * a.D + u * VW, total);
 }

@@ -789,19 +789,19 @@ int vh_embedding_bwd(const float* ids, const float* dy, float* dW, int64_t n, in
   EmbPlaceArgs k3{I(L.tok), I(L.heavy_index), I(L.cursor), I(L.pos), I(L.blkcnt), n, (int32_t)L.nblk,
                   L.blk_shift};
   VH_TRY(launch("vh_emb_place", (unsigned)cdiv(n, 256), 1, 256, 0, s, k3));
-  // Up to 2048 worker waves for the heavy work items (at most tasks_max x slices).
+  // Up to 1024 worker waves for the heavy work items (at most tasks_max x slices).
   const int64_t heavy_blocks =
-      std::min<int64_t>(512, cdiv((n / kEmbChunkHits + n / (kEmbLight + 1) + 2) * slices, 4));
+      std::min<int64_t>(256, cdiv((n / kEmbChunkHits + n / (kEmbLight + 1) + 2) * slices, 4));
   float* partial = reinterpret_cast<float*>(base + L.partial);
   EmbSegArgs k4{I(L.counts), I(L.pos), I(L.tok), I(L.heavy), I(L.taskmap), I(L.blkcnt), I(L.ctr), partial,
                 dy, dW, n, (int32_t)V, (int32_t)D, (int32_t)L.nblk, L.blk_shift, (int32_t)heavy_blocks, slices};
   VH_TRY(launch(vec ? "vh_emb_rows_v4" : "vh_emb_rows_v1", (unsigned)(heavy_blocks + cdiv(V, 4)), 1, 256, 0,
                 s, k4));
-  // One wave per (possible heavy entry, slice); waves past the device-side count return.
+  // Up to 512 waves striding over the (heavy entry, slice) items the device counted.
   const int64_t heavy_max = n / (kEmbLight + 1) + 1;
   EmbFinalArgs k5{I(L.heavy), I(L.ctr), partial, dW, (int32_t)D, slices};
-  return launch(vec ? "vh_emb_heavy_final_v4" : "vh_emb_heavy_final_v1", (unsigned)cdiv(heavy_max * slices, 4), 1,
-                256, 0, s, k5);
+  return launch(vec ? "vh_emb_heavy_final_v4" : "vh_emb_heavy_final_v1",
+                (unsigned)std::min<int64_t>(128, cdiv(heavy_max * slices, 4)), 1, 256, 0, s, k5);
 }
 
 // --------------------------------------------------------- cross-entropy --
