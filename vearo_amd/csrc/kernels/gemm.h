@@ -410,11 +410,11 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
 // first k tile of the next one, so its global loads are in flight under the
 // current tile's products and epilogue instead of exposed at the start of a
 // short-lived workgroup. Work items are the live tiles of every batch, batch
-// major (causal 1: the tn <= tm triangle of a square tile grid, tiles_n >=
-// tiles_m); XCD x (= workgroup id % 8, the hardware's round-robin) takes the
-// x-th contiguous eighth of the items, so one XCD works on one or two batches
-// at a time and its L2 holds their operands. Tile width 128; no split, causal
-// 0 or 1 only (the host guarantees both).
+// major (causal 1: the tiles with tn <= tm, which with tiles_n >= tiles_m are
+// T (T + 1) / 2 for T = tiles_m); XCD x (= workgroup id % 8, the hardware's
+// round-robin) takes the x-th contiguous eighth of the items, so one XCD works
+// on one or two batches at a time and its L2 holds their operands. Tile width
+// 128; no split, causal 0 or 1 only (the host guarantees both).
 template <bool A_KC, bool A_VEC, bool B_KC, bool B_VEC>
 VH_DEV void gemm_f32_persist(const GemmArgs& a) {
   constexpr int TN = 128, NTW = 2;
