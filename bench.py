@@ -491,7 +491,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
-                    help="only run 4 device-to-device copies of 256 MiB (a copy kernel of known "
+                    help="only run 4 device-to-device copies of 1 GiB (a copy kernel of known "
                          "size, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -505,7 +505,9 @@ def main():
     hip = Hip()
     stream = vh.lib.vh_stream()
     if args.calibrate_copy:
-        nb = 256 << 20
+        # 1 GiB each way: four times the 256 MB last-level cache in front of
+        # HBM, so the copies stream from and to HBM.
+        nb = 1 << 30
         src, dst = vh.DeviceBuffer(nb, zero=True), vh.DeviceBuffer(nb)
         vh.sync()
         e0, e1 = hip.event(), hip.event()

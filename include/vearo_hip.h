@@ -95,7 +95,8 @@ int vh_free(void* ptr);
  * write (cuda:114-122) and read (cuda:124-132) hooks. */
 int vh_h2d(void* dst, const void* src, size_t bytes);
 int vh_d2h(void* dst, const void* src, size_t bytes);
-/* Asynchronous device-to-device copy on `stream`. */
+/* Asynchronous device-to-device copy on `stream` (the regions must not
+ * overlap). 16-byte aligned copies run the library's streaming copy kernel. */
 int vh_d2d(void* dst, const void* src, size_t bytes, void* stream);
 /* out[i] = value for i < n (a fill kernel, never hipMemset). */
 int vh_fill_f32(float* out, float value, int64_t n, void* stream);

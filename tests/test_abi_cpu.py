@@ -112,7 +112,7 @@ def launcher_kernel_names():
     for v in list(range(8, 129, 8)) + [99]:
         names |= {f"vh_xent_fwd_n{v}", f"vh_xent_bwd_n{v}", f"vh_xent_fb_n{v}"}
     names |= {"vh_xent_fwd_stream", "vh_xent_bwd_stream", "vh_xent_reduce", "vh_col_reduce",
-              "vh_emb_tokens", "vh_emb_alloc", "vh_emb_place", "vh_fill",
+              "vh_emb_tokens", "vh_emb_alloc", "vh_emb_place", "vh_fill", "vh_stream_copy",
               "vh_binary_strided_i32", "vh_binary_strided_i64", "vh_reduce_thread",
               "vh_reduce_wave", "vh_strided_copy_i32", "vh_strided_copy_i64", "vh_col_partial",
               "vh_adamw_v1", "vh_adamw_v4", "vh_gemm_reduce"}

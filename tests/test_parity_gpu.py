@@ -5,6 +5,8 @@ bit-exact, and so are embedding-gradient rows of tokens with at most 16 hits
 Shapes cover the BASELINE configs (or a row-subset of them where the oracle
 would take minutes) plus the ragged / tiny / large-row variants of each kernel
 family. Full-size properties of the biggest configs run in test_properties_gpu.py."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -348,3 +350,21 @@ def test_arena_reuse_and_zeroing(vh):
     after = vh.mem_stats()
     assert after.live_bytes == before.live_bytes
     assert after.hip_bytes <= before.hip_bytes + 4 * (1 << 20)
+
+
+@pytest.mark.parametrize("nbytes,soff,doff", [(16, 0, 0), (20, 0, 0), (4, 0, 0), (1_000_004, 0, 0),
+                                              (64 * 2**20 + 12, 0, 0), (1000, 4, 0), (4096, 16, 32),
+                                              (3 * 2**20, 8, 8)])
+def test_device_copy_is_exact(vh, nbytes, soff, doff):
+    """vh_d2d: 16-byte aligned copies through the library's streaming kernel
+    (with the runtime's copy for a tail under 16 bytes), other alignments
+    through the runtime's copy; bytes around the destination stay untouched."""
+    r = np.random.default_rng(nbytes)
+    src = r.integers(0, 256, size=nbytes + soff, dtype=np.uint8)
+    guard = np.full(nbytes + doff + 64, 0xA5, np.uint8)
+    S, D = vh.DeviceBuffer.from_array(src), vh.DeviceBuffer.from_array(guard)
+    vh.check(vh.lib.vh_d2d(ctypes.c_void_p(D.ptr + doff), ctypes.c_void_p(S.ptr + soff), nbytes, None))
+    vh.sync()
+    got = D.to_array((guard.size,), np.uint8)
+    assert got[doff:doff + nbytes].tobytes() == src[soff:].tobytes()
+    assert (got[:doff] == 0xA5).all() and (got[doff + nbytes:] == 0xA5).all()

@@ -164,6 +164,7 @@ extern "C" __global__ void __launch_bounds__(256) vh_reduce_wave(ReduceArgs a) {
 extern "C" __global__ void __launch_bounds__(256) vh_strided_copy_i32(CopyArgs a) { strided_copy_impl<uint32_t>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_strided_copy_i64(CopyArgs a) { strided_copy_impl<uint64_t>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_fill(FillArgs a) { fill_impl(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_stream_copy(StreamCopyArgs a) { stream_copy_impl(a); }
 
 // Matrix multiply: vh_gemm_<A><B>, each operand k-contiguous ("k") or
 // m/n-contiguous ("m"/"n"), with 128-bit ("4") or 32-bit ("1") global loads.

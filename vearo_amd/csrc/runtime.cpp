@@ -482,6 +482,17 @@ int vh_d2h(void* dst, const void* src, size_t bytes) {
 int vh_d2d(void* dst, const void* src, size_t bytes, void* stream) {
   VH_TRY(require_init());
   if (bytes == 0) return VH_OK;
+  // 16-byte aligned copies: the library's streaming copy kernel for the whole
+  // units, the runtime's copy for a tail of under 16 bytes.
+  const size_t n4 = bytes / 16;
+  if (aligned16(dst) && aligned16(src) && n4 > 0 && cdiv((int64_t)n4, 256) <= INT32_MAX) {
+    StreamCopyArgs a{static_cast<const float*>(src), static_cast<float*>(dst), (int64_t)n4};
+    VH_TRY(launch("vh_stream_copy", (unsigned)cdiv((int64_t)n4, 256), 1, 256, 0, S(stream), a));
+    if (bytes == n4 * 16) return VH_OK;
+    VH_HIP(hipMemcpyAsync(static_cast<char*>(dst) + n4 * 16, static_cast<const char*>(src) + n4 * 16,
+                          bytes - n4 * 16, hipMemcpyDeviceToDevice, S(stream)));
+    return VH_OK;
+  }
   VH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, S(stream)));
   return VH_OK;
 }

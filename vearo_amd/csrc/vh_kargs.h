@@ -275,3 +275,10 @@ struct FillArgs {
   int64_t n;
   float value;
 };
+
+// Device-to-device copy of n4 16-byte units (both pointers 16-byte aligned).
+struct StreamCopyArgs {
+  const float* src;
+  float* dst;
+  int64_t n4;
+};
