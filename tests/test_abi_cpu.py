@@ -106,7 +106,8 @@ def launcher_kernel_names():
             if vw == 4:
                 names |= {f"vh_ln_bwd_t64_n{v}_v4_b1024_f", f"vh_ln_fwd_t64_n{v}_v4_r4_f"}
         for v in nv:
-            names |= {f"vh_gelu_bias_fwd_n{v}_v{vw}", f"vh_gelu_bias_bwd_n{v}_v{vw}"}
+            names.add(f"vh_gelu_bias_fwd_n{v}_v{vw}")
+        names.add(f"vh_gelu_bias_bwd_tile_v{vw}")
         names |= {f"vh_gelu_fwd_v{vw}", f"vh_gelu_gradmul_v{vw}", f"vh_emb_fwd_v{vw}",
                   f"vh_emb_rows_v{vw}", f"vh_emb_heavy_final_v{vw}", f"vh_binary_contig_v{vw}"}
     for v in list(range(8, 129, 8)) + [99]:

@@ -6,10 +6,13 @@
 // same f32 constants and the same rounding order (built with -ffp-contract=off).
 // The bias add h = x + b[c] is the Linear bias add (cpu lib.rs:183-196 broadcast).
 //
-// Layout: x, dy, y, dx [rows, C] row-major; bias, dbias [C]. The bias kernels are
-// column-stationary: a 256-thread workgroup keeps its columns' bias (and dbias
-// partials) in VGPRs and walks a contiguous range of rows, so every tensor byte
-// moves once (fwd 8 B/elem, bwd 12 B/elem) and dbias needs no atomics.
+// Layout: x, dy, y, dx [rows, C] row-major; bias, dbias [C]. The forward bias
+// kernel takes one row per 256-thread workgroup with the row's bias in VGPRs.
+// The backward takes a tile of 64 column units by one row block per
+// workgroup, one unit per lane, so every wave streams 64 consecutive units of
+// a row (the layout a plain copy streams best in) and the dbias partial of the
+// tile's columns is summed in the workgroup. Every tensor byte moves once (fwd
+// 8 B/elem, bwd 12 B/elem) and dbias needs no atomics.
 #pragma once
 #include "common.h"
 
@@ -83,46 +86,60 @@ VH_DEV void gelu_bias_fwd_impl(const GeluBiasBwdArgs& a) {
   }
 }
 
-// dx[r, c] = dy[r, c] * gelu_mask(x[r, c] + bias[c]); part[blk][c] = sum over the
-// workgroup's rows (ascending) of dx[r, c].
-template <int NV, int VW>
-VH_DEV void gelu_bias_bwd_impl(const GeluBiasBwdArgs& a) {
+// dx[r, c] = dy[r, c] * gelu_mask(x[r, c] + bias[c]); part[blk][c] = sum of
+// dx[r, c] over the rows of row block blk = [blk * rpb, blk * rpb + rpb).
+// Workgroup (column tile blockIdx.x of 64 VW-float units, row block
+// blockIdx.y): each lane holds one unit, so a wave reads and writes 64
+// consecutive units of a row; wave w takes rows r0 + w, r0 + w + 4, ... (RPT
+// rows' loads issued together), sums them in ascending order, and the four
+// waves' sums are added in wave order through LDS. The partials depend on
+// (rows, C) only.
+template <int VW, int RPT>
+VH_DEV void gelu_bias_bwd_tile_impl(const GeluBiasBwdArgs& a) {
+  __shared__ Unit<VW> lds[3][64];
   const int C = a.C;
   const int U = C / VW;
-  Unit<VW> b[NV], acc[NV];
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int u = threadIdx.x + k * 256;
-    b[k] = u < U ? load_unit<VW>(a.bias + u * VW) : zero_unit<VW>();
-    acc[k] = zero_unit<VW>();
-  }
-  const int64_t r0 = (int64_t)blockIdx.x * a.rows_per_block;
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int u = blockIdx.x * 64 + lane;
+  const bool cu = u < U;
+  const Unit<VW> b = cu ? load_unit<VW>(a.bias + u * VW) : zero_unit<VW>();
+  Unit<VW> acc = zero_unit<VW>();
+  const int64_t r0 = (int64_t)blockIdx.y * a.rows_per_block;
   int64_t r1 = r0 + a.rows_per_block;
   if (r1 > a.rows) r1 = a.rows;
-  for (int64_t r = r0; r < r1; ++r) {
-    const float* xr = a.x + r * C;
-    const float* gr = a.dy + r * C;
-    float* dr = a.dx + r * C;
+  for (int64_t base = r0 + w; base < r1; base += 4 * RPT) {
+    Unit<VW> x[RPT], g[RPT];
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int u = threadIdx.x + k * 256;
-      if (u < U) {
-        const Unit<VW> x = load_stream<VW>(xr + u * VW);
-        const Unit<VW> g = load_stream<VW>(gr + u * VW);
+    for (int i = 0; i < RPT; ++i) {
+      const int64_t r = base + 4 * i;
+      x[i] = g[i] = zero_unit<VW>();
+      if (cu && r < r1) {
+        x[i] = load_stream<VW>(a.x + r * C + u * VW);
+        g[i] = load_stream<VW>(a.dy + r * C + u * VW);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int64_t r = base + 4 * i;
+      if (cu && r < r1) {
         Unit<VW> o;
 #pragma unroll
         for (int j = 0; j < VW; ++j) {
-          o.v[j] = g.v[j] * gelu_mask_f(x.v[j] + b[k].v[j]);
-          acc[k].v[j] += o.v[j];
+          o.v[j] = g[i].v[j] * gelu_mask_f(x[i].v[j] + b.v[j]);
+          acc.v[j] += o.v[j];
         }
-        store_stream<VW>(dr + u * VW, o);
+        store_stream<VW>(a.dx + r * C + u * VW, o);
       }
     }
   }
-  float* p = a.part + (size_t)blockIdx.x * C;
+  if (w > 0) lds[w - 1][lane] = acc;
+  __syncthreads();
+  if (w == 0 && cu) {
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int u = threadIdx.x + k * 256;
-    if (u < U) store_unit<VW>(p + u * VW, acc[k]);
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+      for (int j = 0; j < VW; ++j) acc.v[j] += lds[q][lane].v[j];
+    store_unit<VW>(a.part + (int64_t)blockIdx.y * C + u * VW, acc);
   }
 }

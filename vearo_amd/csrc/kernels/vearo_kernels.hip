@@ -112,15 +112,14 @@ extern "C" __global__ void __launch_bounds__(256) vh_gelu_gradmul_v4(EltArgs a) 
       vh_gelu_bias_fwd_n##N##_v##VW(GeluBiasBwdArgs a) {                          \
     gelu_bias_fwd_impl<N, VW>(a);                                                 \
   }
-#define K_GB_BWD(N, VW)                                                           \
-  extern "C" __global__ void __launch_bounds__(256)                               \
-      vh_gelu_bias_bwd_n##N##_v##VW(GeluBiasBwdArgs a) {                          \
-    gelu_bias_bwd_impl<N, VW>(a);                                                 \
+#define K_GB_BWD(VW)                                                                      \
+  extern "C" __global__ void __launch_bounds__(256) vh_gelu_bias_bwd_tile_v##VW(GeluBiasBwdArgs a) { \
+    gelu_bias_bwd_tile_impl<VW, 2>(a);                                                    \
   }
 GB_CFG(K_GB_FWD, 1)
 GB_CFG(K_GB_FWD, 4)
-GB_CFG(K_GB_BWD, 1)
-GB_CFG(K_GB_BWD, 4)
+K_GB_BWD(1)
+K_GB_BWD(4)
 
 // Embedding
 extern "C" __global__ void __launch_bounds__(256) vh_emb_fwd_v1(EmbFwdArgs a) { emb_fwd_impl<1>(a); }
