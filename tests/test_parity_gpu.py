@@ -257,7 +257,8 @@ def test_embedding_bad_ids_report_cpu_panic(vh, bad, msg):
 
 
 # -------------------------------------------------------------- cross-entropy
-@pytest.mark.parametrize("B,V", [(512, 50257), (3, 5), (64, 1000), (7, 70000), (1, 1)])
+# (1500, 3000): more rows than the GPU holds row-cached workgroups at once.
+@pytest.mark.parametrize("B,V", [(512, 50257), (3, 5), (64, 1000), (7, 70000), (1, 1), (1500, 3000)])
 def test_cross_entropy_fwd_bwd(vh, B, V):
     print(f"cross_entropy B={B} V={V}", flush=True)
     r = rng(4)
