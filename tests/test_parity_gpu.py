@@ -90,7 +90,10 @@ def test_layernorm_explicit_scratch_and_errors(vh):
 
 
 # ----------------------------------------------------------------------- gelu
-@pytest.mark.parametrize("rows,C", [(16384, 3072), (3, 5), (33, 100), (7, 4096), (5, 5000)])
+# (2500, 768) and (20000, 192): row blocks of 3 and 20 rows (at most 1024
+# dbias partials), so a block's rows end partway through a batch of loads.
+@pytest.mark.parametrize("rows,C", [(16384, 3072), (3, 5), (33, 100), (7, 4096), (5, 5000), (2500, 768),
+                                    (20000, 192)])
 def test_gelu_bias_fwd_bwd(vh, rows, C):
     print(f"gelu_bias rows={rows} C={C}", flush=True)
     r = rng(1)
