@@ -29,7 +29,14 @@ FETCH_SIZE / WRITE_SIZE passes when present. cpu_baseline times the CPU oracle
 (the C restatement of the reference's CPU backend, one thread) on a bounded
 sample of the same workload, counting the same algorithmic bytes.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload NAME] [--no-cpu]
+Warmup is at least --warmup steps and at least --min-warmup-ms of them: after
+the second or so of host-side input generation the GPU has lowered its clocks,
+and a few milliseconds of work do not bring them back (measured: the softmax
+backward runs 262 us back to back, 270-336 us for the first ~10 ms after a 1 s
+idle). The JSON's "warmup" is the number of warmup steps run; the timed region
+is exactly --steps steps either way.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--min-warmup-ms 500] [--workload NAME] [--no-cpu]
 """
 import argparse
 import ctypes
@@ -487,6 +494,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--min-warmup-ms", type=float, default=500.0,
+                    help="keep warming up until this much wall time has passed (GPU clocks recover "
+                         "from the idle of input generation)")
     ap.add_argument("--workload", default="ln_softmax", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -527,10 +537,16 @@ def main():
     ops, info, cpu, keep, traffic_file = WORKLOADS[args.workload](vh)
     vh.sync()
     names = [o[0] for o in ops]
-    for i in range(args.warmup):
+    warm = 0
+    t_w = time.perf_counter()
+    while warm < args.warmup or time.perf_counter() - t_w < args.min_warmup_ms / 1e3:
         for _, _, call in ops:
-            vh.check(call(i))
+            vh.check(call(warm))
+        warm += 1
+        if warm % 8 == 0:
+            vh.sync()  # wall time then tracks the GPU's, not the launch queue's
     vh.sync()
+    args.warmup = warm
 
     K = args.steps
     # The timed steps carry no instrumentation between the ops: the value is
