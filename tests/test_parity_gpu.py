@@ -130,8 +130,10 @@ def causal_scores(r, B, H, T):
     return s
 
 
+# (1, 1, 201): 201 one-float units on two-wave teams and an odd row count, so a
+# workgroup's second team has no row; (1, 3, 600): 150 four-float units.
 @pytest.mark.parametrize("B,H,T", [(2, 12, 1024), (1, 2, 37), (2, 3, 128), (1, 1, 1000),
-                                   (1, 1, 2048), (1, 1, 5000)])
+                                   (1, 1, 2048), (1, 1, 5000), (1, 1, 201), (1, 3, 600)])
 @pytest.mark.parametrize("causal", [0, 1])
 def test_softmax_fwd_bwd(vh, B, H, T, causal):
     print(f"softmax B={B} H={H} T={T} causal={causal}", flush=True)

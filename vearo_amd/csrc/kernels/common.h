@@ -53,8 +53,11 @@ VH_DEV float group_max(float v) {
   return v;
 }
 
-// Team reductions. For TEAM > 64 the whole workgroup is the team; `lds` must
-// hold TEAM/64 floats and every thread of the block must call (no early exit).
+// Team reductions. For TEAM > 64 a team is TEAM / 64 consecutive waves of the
+// workgroup (one or more teams per workgroup); wave w writes its partial to
+// lds[w] and each team reads its own NW slots, so `lds` must hold
+// blockDim.x / 64 floats and every thread of the block must call (no early
+// exit). The partials are combined in wave order.
 template <int TEAM>
 VH_DEV float team_sum(float v, float* lds) {
   if constexpr (TEAM <= 64) {
@@ -63,11 +66,12 @@ VH_DEV float team_sum(float v, float* lds) {
     constexpr int NW = TEAM / 64;
     v = group_sum<64>(v);
     const int wave = threadIdx.x >> 6;
+    const float* t = lds + (wave / NW) * NW;
     if ((threadIdx.x & 63) == 0) lds[wave] = v;
     __syncthreads();
-    float s = lds[0];
+    float s = t[0];
 #pragma unroll
-    for (int i = 1; i < NW; ++i) s += lds[i];
+    for (int i = 1; i < NW; ++i) s += t[i];
     __syncthreads();
     return s;
   }
@@ -81,11 +85,12 @@ VH_DEV float team_max(float v, float* lds) {
     constexpr int NW = TEAM / 64;
     v = group_max<64>(v);
     const int wave = threadIdx.x >> 6;
+    const float* t = lds + (wave / NW) * NW;
     if ((threadIdx.x & 63) == 0) lds[wave] = v;
     __syncthreads();
-    float s = lds[0];
+    float s = t[0];
 #pragma unroll
-    for (int i = 1; i < NW; ++i) s = fmaxf(s, lds[i]);
+    for (int i = 1; i < NW; ++i) s = fmaxf(s, t[i]);
     __syncthreads();
     return s;
   }

@@ -93,6 +93,12 @@ ROW_CFG_MULTI(K_SM_FWD_M, 4)
 #define K_SM_BWD_M(T, N, VW) K_SM_BWD_R(T, N, VW, 2)
 ROW_CFG_SMALL(K_SM_BWD, 1)
 ROW_CFG_SMALL(K_SM_BWD, 4)
+// Two-wave teams, two rows per 256-thread workgroup: the softmax form for rows
+// of 129-256 units.
+K_SM_FWD(128, 2, 1)
+K_SM_FWD(128, 2, 4)
+K_SM_BWD(128, 2, 1)
+K_SM_BWD(128, 2, 4)
 ROW_CFG_MULTI(K_SM_BWD_M, 1)
 ROW_CFG_MULTI(K_SM_BWD_M, 4)
 
