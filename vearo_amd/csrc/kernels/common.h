@@ -174,6 +174,25 @@ VH_DEV Unit<VW> zero_unit() {
   return u;
 }
 
+// a / b correctly rounded (the IEEE quotient, bit for bit), given y = RN(1/b),
+// for divisors 1 <= |b| <= 2^24 (row lengths, softmax sums). Markstein's
+// correction: q = RN(a*y) is within one ulp of a/b, the remainder r = a - b*q
+// is exact in one fused multiply-add, and RN(q + r*y) is the correctly rounded
+// quotient (Markstein, "IA-64 and Elementary Functions", 2000, Thm 8.10).
+// Three instructions instead of the ~10 of the general division sequence.
+// |a| outside [2^-100, 2^100) (zero, subnormal, huge, inf, nan) takes the
+// general division, so q and r never leave the normal range. Checked
+// exhaustively on one binade of a (every significand) for 200 divisors.
+VH_DEV float div_rn(float a, float b, float y) {
+  const float m = fabsf(a);
+  if (m >= 0x1p-100f && m < 0x1p100f) {
+    const float q = a * y;
+    const float r = fmaf(-q, b, a);
+    return fmaf(r, y, q);
+  }
+  return a / b;
+}
+
 // Rust `value.round() as usize` followed by the `< bound` check, on device.
 // Returns -1 for a value the CPU backend would reject.
 VH_DEV int32_t checked_index(float v, int32_t bound) {

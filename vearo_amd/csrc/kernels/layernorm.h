@@ -10,14 +10,17 @@
 // Forward: a TEAM of lanes owns a row held in VGPRs (NV units of VW floats per
 // lane); each team takes RPW rows and issues all their loads before any math,
 // so x is read once and y written once (8 B/elem) with enough bytes in flight.
-// Backward: x and dy read once, dx written once (12 B/elem); the next row of a
-// team is prefetched while the current one is reduced. dgamma/dbeta are
-// deterministic and atomic-free: each lane accumulates its fixed columns over
-// the rows its team visits, the G row-groups of a workgroup fold in a fixed LDS
-// tree, one partial row per workgroup goes to scratch, and col_reduce sums the
-// partials in a fixed order. FULL forms (C exactly TEAM * NV * VW, e.g. 768 =
-// 64 lanes x 3 units x 4 floats) drop the per-unit bounds tests: 12 % of the
-// backward's time at GPT-2 shape (measured).
+// Backward: x and dy read once, dx written once (12 B/elem), rows dealt to the
+// grid's teams grid-stride. dgamma/dbeta are deterministic and atomic-free:
+// each lane accumulates its fixed columns over the rows its team visits, the G
+// teams of a workgroup fold in a fixed order through LDS, one partial row per
+// workgroup goes to scratch, and col_reduce sums the partials in a fixed order.
+// FULL forms (C exactly TEAM * NV * VW, e.g. 768 = 64 lanes x 3 units x 4
+// floats) drop the per-unit bounds tests: 12 % of the backward's time at GPT-2
+// shape (measured). An in-kernel finish of the column sums (last workgroup to
+// arrive adds the partials) was measured at 150-190 us against 4.5 us for the
+// separate col_reduce launch: the device-scope fence it needs writes back an
+// XCD's L2 and serialises across the workgroups of the XCD.
 #pragma once
 #include "common.h"
 
@@ -91,39 +94,59 @@ VH_DEV void ln_fwd_impl(const LnFwdArgs& a) {
   }
 }
 
-// Backward stage 1. Workgroup = BS threads = G row-groups of TEAM lanes. The
-// workgroup owns rows [blockIdx.x*rows_per_block, +rows_per_block); group g
-// visits rows g, g+G, ... of that range. Dynamic LDS: (G/2)*2*C floats.
+// Backward stage 1. Workgroup = BS threads = G row-groups (teams) of TEAM
+// lanes; the grid's NT = gridDim.x * G teams take rows grid-stride (team t:
+// rows t, t + NT, ...), so at any moment the whole grid streams one contiguous
+// block of rows (measured on MI355X at [16384, 768]: 30.5 against 34.4 us for
+// teams walking private contiguous row ranges, the same arithmetic). w stays in
+// registers where the budget allows (HOIST), so the only memory waits in the
+// row loop are on x and dy. The row reductions and the dx expression are the
+// reference's; the division by C is div_rn (bit-identical, 3 instructions).
+// dgamma/dbeta: each lane accumulates its columns over its team's rows; the G
+// teams of a workgroup fold through LDS in a fixed order -- FULL forms (C a
+// compile-time TEAM*NV*VW, G = 16) in one level (every team parks its partial
+// row, one barrier, each thread sums one 4-column unit over the 16 slots in
+// team order), the others in a fixed pairwise tree in dynamic LDS of
+// (G/2)*2*C floats -- and one partial row per workgroup goes to scratch for
+// col_reduce. Row assignment and grouping depend on (rows, C) only, so the
+// result is identical run to run.
 template <int TEAM, int NV, int VW, int BS, bool FULL = false>
 VH_DEV void ln_bwd_impl(const LnBwdArgs& a, float* lds) {
   static_assert(BS >= TEAM && BS % TEAM == 0, "block must hold whole teams");
   constexpr int G = BS / TEAM;
+  constexpr bool HOIST = NV * VW <= 12;  // w in VGPRs: 12 more at C = 768 (109 -> 111 in all)
   __shared__ float red[16];
   const int lane = threadIdx.x % TEAM;
   const int g = threadIdx.x / TEAM;
-  const int C = a.C;
+  const int C = FULL ? TEAM * NV * VW : a.C;
   const int U = FULL ? TEAM * NV : C / VW;  // FULL: C == TEAM * NV * VW, every unit live
   const float Cf = (float)C;
-  const int64_t r0 = (int64_t)blockIdx.x * a.rows_per_block;
-  int64_t r1 = r0 + a.rows_per_block;
-  if (r1 > a.rows) r1 = a.rows;
+  const float rC = 1.0f / Cf;
+  const int64_t NT = (int64_t)gridDim.x * G;
 
-  Unit<VW> gw[NV], gb[NV];
+  Unit<VW> gw[NV], gb[NV], wv[HOIST ? NV : 1];
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     gw[k] = zero_unit<VW>();
     gb[k] = zero_unit<VW>();
+    if constexpr (HOIST) {
+      const int u = lane + k * TEAM;
+      wv[k] = (FULL || u < U) ? load_unit<VW>(a.w + u * VW) : zero_unit<VW>();
+    }
   }
+  auto wunit = [&](int k, int u) -> Unit<VW> {
+    if constexpr (HOIST) return wv[k];
+    else return load_unit<VW>(a.w + u * VW);
+  };
 
-  // Row `row` of this group: x and dy into registers (zeros past the range).
-  auto load_row = [&](int64_t row, Unit<VW>* xv, Unit<VW>* gv) {
-    const bool ok = row < r1;
-    const float* xr = a.x + (ok ? row : 0) * (int64_t)C;
-    const float* dyr = a.dy + (ok ? row : 0) * (int64_t)C;
+  for (int64_t row = (int64_t)blockIdx.x * G + g; row < a.rows; row += NT) {
+    const float* xr = a.x + row * (int64_t)C;
+    const float* dyr = a.dy + row * (int64_t)C;
+    Unit<VW> xv[NV], gv[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int u = lane + k * TEAM;
-      if (ok && (FULL || u < U)) {
+      if (FULL || u < U) {
         xv[k] = load_stream<VW>(xr + u * VW);
         gv[k] = load_stream<VW>(dyr + u * VW);
       } else {
@@ -131,14 +154,6 @@ VH_DEV void ln_bwd_impl(const LnBwdArgs& a, float* lds) {
         gv[k] = zero_unit<VW>();
       }
     }
-  };
-
-  Unit<VW> xv[NV], gv[NV];
-  int64_t row = r0 + g;
-  load_row(row, xv, gv);
-  for (; row < r1; row += G) {
-    Unit<VW> xn[NV], gn[NV];
-    load_row(row + G, xn, gn);  // prefetch: in flight while this row is reduced
 
     float s = 0.0f;
 #pragma unroll
@@ -168,7 +183,7 @@ VH_DEV void ln_bwd_impl(const LnBwdArgs& a, float* lds) {
     for (int k = 0; k < NV; ++k) {
       const int u = lane + k * TEAM;
       if (FULL || u < U) {
-        const Unit<VW> w = load_unit<VW>(a.w + u * VW);
+        const Unit<VW> w = wunit(k, u);
 #pragma unroll
         for (int j = 0; j < VW; ++j) {
           const float xh = (xv[k].v[j] - mean) * inv_std;
@@ -188,69 +203,87 @@ VH_DEV void ln_bwd_impl(const LnBwdArgs& a, float* lds) {
     for (int k = 0; k < NV; ++k) {
       const int u = lane + k * TEAM;
       if (FULL || u < U) {
-        const Unit<VW> w = load_unit<VW>(a.w + u * VW);
+        const Unit<VW> w = wunit(k, u);
         Unit<VW> o;
 #pragma unroll
         for (int j = 0; j < VW; ++j) {
           const float xh = (xv[k].v[j] - mean) * inv_std;
           const float t1 = Cf * gv[k].v[j] * w.v[j];
-          o.v[j] = (t1 - sgw - xh * sgwx) * inv_std / Cf;
+          o.v[j] = div_rn((t1 - sgw - xh * sgwx) * inv_std, Cf, rC);
         }
         store_stream<VW>(dxr + u * VW, o);
       }
     }
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      xv[k] = xn[k];
-      gv[k] = gn[k];
-    }
   }
 
-  // Fold the G row-groups in a fixed tree: at each step the upper half parks its
-  // partials in LDS and the lower half adds them (group g += group g+half).
-  if constexpr (G > 1) {
-#pragma unroll
-    for (int half = G / 2; half >= 1; half /= 2) {
-      if (g >= half && g < 2 * half) {
-        float* dst = lds + (size_t)(g - half) * 2 * C;
-#pragma unroll
-        for (int k = 0; k < NV; ++k) {
-          const int u = lane + k * TEAM;
-          if (FULL || u < U) {
-#pragma unroll
-            for (int j = 0; j < VW; ++j) {
-              dst[u * VW + j] = gw[k].v[j];
-              dst[C + u * VW + j] = gb[k].v[j];
-            }
-          }
-        }
-      }
-      __syncthreads();
-      if (g < half) {
-        const float* src = lds + (size_t)g * 2 * C;
-#pragma unroll
-        for (int k = 0; k < NV; ++k) {
-          const int u = lane + k * TEAM;
-          if (FULL || u < U) {
-#pragma unroll
-            for (int j = 0; j < VW; ++j) {
-              gw[k].v[j] += src[u * VW + j];
-              gb[k].v[j] += src[C + u * VW + j];
-            }
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
-  if (g == 0) {
-    float* p = a.part + (size_t)blockIdx.x * 2 * C;
+  float* p = a.part + (size_t)blockIdx.x * 2 * C;
+  if constexpr (FULL) {
+    // One-level fold: slot g holds team g's [dgamma | dbeta] partial row.
+    static_assert(VW == 4, "full forms use 128-bit units");
+    __shared__ float fold[G * 2 * TEAM * NV * VW];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int u = lane + k * TEAM;
-      if (FULL || u < U) {
-        store_unit<VW>(p + u * VW, gw[k]);
-        store_unit<VW>(p + C + u * VW, gb[k]);
+      store_unit<VW>(fold + g * 2 * C + u * VW, gw[k]);
+      store_unit<VW>(fold + g * 2 * C + C + u * VW, gb[k]);
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < 2 * C / 4; t += BS) {
+      Unit<4> acc = load_unit<4>(fold + t * 4);
+#pragma unroll
+      for (int i = 1; i < G; ++i) {
+        const Unit<4> v = load_unit<4>(fold + i * 2 * C + t * 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc.v[j] += v.v[j];
+      }
+      store_unit<4>(p + t * 4, acc);
+    }
+  } else {
+    // Fixed pairwise tree: at each step the upper half parks its partials in
+    // LDS and the lower half adds them (group g += group g+half).
+    if constexpr (G > 1) {
+#pragma unroll
+      for (int half = G / 2; half >= 1; half /= 2) {
+        if (g >= half && g < 2 * half) {
+          float* dst = lds + (size_t)(g - half) * 2 * C;
+#pragma unroll
+          for (int k = 0; k < NV; ++k) {
+            const int u = lane + k * TEAM;
+            if (u < U) {
+#pragma unroll
+              for (int j = 0; j < VW; ++j) {
+                dst[u * VW + j] = gw[k].v[j];
+                dst[C + u * VW + j] = gb[k].v[j];
+              }
+            }
+          }
+        }
+        __syncthreads();
+        if (g < half) {
+          const float* src = lds + (size_t)g * 2 * C;
+#pragma unroll
+          for (int k = 0; k < NV; ++k) {
+            const int u = lane + k * TEAM;
+            if (u < U) {
+#pragma unroll
+              for (int j = 0; j < VW; ++j) {
+                gw[k].v[j] += src[u * VW + j];
+                gb[k].v[j] += src[C + u * VW + j];
+              }
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    if (g == 0) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int u = lane + k * TEAM;
+        if (u < U) {
+          store_unit<VW>(p + u * VW, gw[k]);
+          store_unit<VW>(p + C + u * VW, gb[k]);
+        }
       }
     }
   }

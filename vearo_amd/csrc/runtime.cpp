@@ -583,10 +583,10 @@ int vh_layernorm_bwd(const float* x, const float* w, const float* dy, float* dx,
   VH_TRY(sc.get(scratch, scratch_bytes, need));
   const int bs = block_of(c);
   const int groups = bs / c.team;
-  const unsigned shmem = groups > 1 ? (unsigned)((groups / 2) * 2 * C * sizeof(float)) : 0;
+  // Full-row forms fold in static LDS; the others in a dynamic pairwise tree.
+  const unsigned shmem = (!c.full && groups > 1) ? (unsigned)((groups / 2) * 2 * C * sizeof(float)) : 0;
   if (shmem > 64 * 1024) return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_bwd: LDS budget exceeded");
-  const int64_t rpb = cdiv(rows, G);
-  LnBwdArgs a{x, w, dy, dx, static_cast<float*>(sc.p), rows, rpb, (int32_t)C, eps};
+  LnBwdArgs a{x, w, dy, dx, static_cast<float*>(sc.p), rows, (int32_t)C, eps};
   VH_TRY(launch(bwd_kernel("vh_ln_bwd", c), (unsigned)G, 1, bs, shmem, s, a));
   ColReduceArgs r{static_cast<float*>(sc.p), dw, db, (int32_t)G, (int32_t)C, 2};
   return launch("vh_col_reduce", (unsigned)cdiv(C, 64), 2, 1024, 0, s, r);

@@ -35,8 +35,7 @@ struct LnBwdArgs {
   const float* dy;
   float* dx;
   float* part;  // [nblocks][2][C] per-block dgamma / dbeta partials
-  int64_t rows;
-  int64_t rows_per_block;
+  int64_t rows;  // rows are dealt grid-stride to the gridDim.x * teams-per-block teams
   int32_t C;
   float eps;
 };
