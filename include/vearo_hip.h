@@ -120,6 +120,24 @@ int vh_layernorm_bwd(const float* x, const float* w, const float* dy, float* dx,
                      void* scratch, size_t scratch_bytes, void* stream);
 size_t vh_layernorm_bwd_scratch_bytes(int64_t rows, int64_t C);
 
+/* Size of the device-resident scratch each GPU holds for the allocation-free
+ * entry points (a file-scope device array, one copy per GPU for the life of
+ * the process). */
+#define VH_NOALLOC_SCRATCH_BYTES (4u << 20)
+
+/* vh_layernorm_bwd with its dgamma/dbeta partials in the device-resident
+ * scratch: no hipMalloc, no hipFree and no allocating library call, for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid it). No counterpart in the reference; the same
+ * kernels and results as vh_layernorm_bwd. Returns VH_ERR_UNSUPPORTED when
+ * vh_layernorm_bwd_scratch_bytes(rows, C) exceeds VH_NOALLOC_SCRATCH_BYTES
+ * (e.g. [16384, 768] needs 1.5 MiB; C above 1024 with many rows does not fit).
+ * Every call on one GPU shares that GPU's scratch: calls that overlap on one
+ * GPU (different streams, or threads) race. */
+int vh_layernorm_bwd_noalloc(const float* x, const float* w, const float* dy, float* dx,
+                             float* dw, float* db, int64_t rows, int64_t C, float eps,
+                             void* stream);
+
 /* -------------------------------------------------------- hot path: gelu -- */
 
 /* y = gelu(x) elementwise, tanh form. Replaces BackendOps.gelu (tensor.rs:1129;

@@ -99,6 +99,7 @@ SIGNATURES = {
         [fp, fp, fp, fp, fp, fp, c_int64, c_int64, c_float, c_void_p, c_size_t, c_void_p],
     ),
     "vh_layernorm_bwd_scratch_bytes": (c_size_t, [c_int64, c_int64]),
+    "vh_layernorm_bwd_noalloc": (c_int, [fp, fp, fp, fp, fp, fp, c_int64, c_int64, c_float, c_void_p]),
     "vh_gelu_fwd": (c_int, [fp, fp, c_int64, c_void_p]),
     "vh_gelu_bias_fwd": (c_int, [fp, fp, fp, c_int64, c_int64, c_void_p]),
     "vh_gelu_grad_mul": (c_int, [fp, fp, fp, c_int64, c_void_p]),

@@ -22,4 +22,9 @@ VH_RT_HIDDEN hipStream_t stream_of(void* s);
 VH_RT_HIDDEN int blaslt_gemm(const vh_gemm_desc* d, bool akc, bool bkc, void* stream, bool* taken);
 // Releases hipBLASLt's handle, workspace and cached plans (vh_shutdown).
 VH_RT_HIDDEN void blaslt_shutdown();
+// Takes the current device's address of the device-resident scratch
+// (noalloc.hip) once per device; vh_init calls it with `device` current.
+VH_RT_HIDDEN int noalloc_setup(int device);
+// That address (VH_NOALLOC_SCRATCH_BYTES bytes), or NULL before setup.
+VH_RT_HIDDEN void* noalloc_scratch(int device);
 }  // namespace vh_rt

@@ -406,6 +406,7 @@ int vh_init(int device) {
   g_rt.err = static_cast<VhErrRecord*>(e);
   VhErrRecord clean{VH_ERR_NONE, VH_ERR_NONE, 0, 0};
   VH_HIP(hipMemcpy(g_rt.err, &clean, sizeof clean, hipMemcpyHostToDevice));
+  VH_TRY(vh_rt::noalloc_setup(device));
   g_rt.device = device;
   g_rt.ready = true;
   return VH_OK;
@@ -557,39 +558,97 @@ size_t vh_layernorm_bwd_scratch_bytes(int64_t rows, int64_t C) {
   return need;
 }
 
-int vh_layernorm_bwd(const float* x, const float* w, const float* dy, float* dx, float* dw,
-                     float* db, int64_t rows, int64_t C, float eps, void* scratch,
-                     size_t scratch_bytes, void* stream) {
-  VH_TRY(require_init());
-  if (rows < 0 || C < 0) return fail(VH_ERR_INVALID, "vh_layernorm_bwd: negative size");
-  hipStream_t s = S(stream);
+}  // extern "C"
+
+namespace {
+// The LayerNorm backward plan for (rows, C) and the operands' alignment: the
+// row configuration, workgroup count and scratch bytes.
+struct LnBwdPlan {
+  RowCfg c;
+  int64_t G;
+  size_t need;
+};
+
+int ln_bwd_plan(int64_t rows, int64_t C, bool vec, LnBwdPlan* p) {
+  if (!pick_row_cfg(C, vec, 8, &p->c))
+    return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_bwd: C=" + std::to_string(C) + " exceeds 32768");
+  set_ln_bwd_bs(&p->c);
+  set_ln_full(&p->c, C);
+  if (p->c.full && block_of(p->c) != 1024) p->c.full = false;
+  p->G = ln_bwd_blocks(rows, p->c);
+  p->need = align256((size_t)p->G * 2 * (size_t)C * sizeof(float));
+  return VH_OK;
+}
+
+// Launches the backward with `part` as the partials buffer (at least p.need bytes).
+int ln_bwd_launch(const LnBwdPlan& p, const float* x, const float* w, const float* dy, float* dx, float* dw,
+                  float* db, int64_t rows, int64_t C, float eps, float* part, hipStream_t s) {
+  const int bs = block_of(p.c);
+  const int groups = bs / p.c.team;
+  // Full-row forms fold in static LDS; the others in a dynamic pairwise tree.
+  const unsigned shmem = (!p.c.full && groups > 1) ? (unsigned)((groups / 2) * 2 * C * sizeof(float)) : 0;
+  if (shmem > 64 * 1024) return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_bwd: LDS budget exceeded");
+  LnBwdArgs a{x, w, dy, dx, part, rows, (int32_t)C, eps};
+  VH_TRY(launch(bwd_kernel("vh_ln_bwd", p.c), (unsigned)p.G, 1, bs, shmem, s, a));
+  ColReduceArgs r{part, dw, db, (int32_t)p.G, (int32_t)C, 2};
+  return launch("vh_col_reduce", (unsigned)cdiv(C, 64), 2, 1024, 0, s, r);
+}
+
+// Argument checks shared by both entries; *done is set when nothing is left
+// to launch (C == 0, or rows == 0 after zero-filling dw and db).
+int ln_bwd_check(const char* fn, const float* x, const float* w, const float* dy, float* dx, float* dw, float* db,
+                 int64_t rows, int64_t C, hipStream_t s, bool* done) {
+  *done = true;
+  if (rows < 0 || C < 0) return fail(VH_ERR_INVALID, std::string(fn) + ": negative size");
   if (C == 0) return VH_OK;
-  if (!dw || !db) return fail(VH_ERR_INVALID, "vh_layernorm_bwd: null pointer");
+  if (!dw || !db) return fail(VH_ERR_INVALID, std::string(fn) + ": null pointer");
   if (rows == 0) {  // reference returns zero gradients (cpu:752-758)
     VH_TRY(fill(dw, 0.0f, C, s));
     return fill(db, 0.0f, C, s);
   }
-  if (!x || !w || !dy || !dx) return fail(VH_ERR_INVALID, "vh_layernorm_bwd: null pointer");
-  RowCfg c;
+  if (!x || !w || !dy || !dx) return fail(VH_ERR_INVALID, std::string(fn) + ": null pointer");
+  *done = false;
+  return VH_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int vh_layernorm_bwd(const float* x, const float* w, const float* dy, float* dx, float* dw,
+                     float* db, int64_t rows, int64_t C, float eps, void* scratch,
+                     size_t scratch_bytes, void* stream) {
+  VH_TRY(require_init());
+  hipStream_t s = S(stream);
+  bool done;
+  VH_TRY(ln_bwd_check("vh_layernorm_bwd", x, w, dy, dx, dw, db, rows, C, s, &done));
+  if (done) return VH_OK;
   const bool vec = aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx);
-  if (!pick_row_cfg(C, vec, 8, &c))
-    return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_bwd: C=" + std::to_string(C) + " exceeds 32768");
-  set_ln_bwd_bs(&c);
-  set_ln_full(&c, C);
-  if (c.full && block_of(c) != 1024) c.full = false;
-  const int64_t G = ln_bwd_blocks(rows, c);
-  const size_t need = align256((size_t)G * 2 * (size_t)C * sizeof(float));
+  LnBwdPlan p;
+  VH_TRY(ln_bwd_plan(rows, C, vec, &p));
   Scratch sc;
-  VH_TRY(sc.get(scratch, scratch_bytes, need));
-  const int bs = block_of(c);
-  const int groups = bs / c.team;
-  // Full-row forms fold in static LDS; the others in a dynamic pairwise tree.
-  const unsigned shmem = (!c.full && groups > 1) ? (unsigned)((groups / 2) * 2 * C * sizeof(float)) : 0;
-  if (shmem > 64 * 1024) return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_bwd: LDS budget exceeded");
-  LnBwdArgs a{x, w, dy, dx, static_cast<float*>(sc.p), rows, (int32_t)C, eps};
-  VH_TRY(launch(bwd_kernel("vh_ln_bwd", c), (unsigned)G, 1, bs, shmem, s, a));
-  ColReduceArgs r{static_cast<float*>(sc.p), dw, db, (int32_t)G, (int32_t)C, 2};
-  return launch("vh_col_reduce", (unsigned)cdiv(C, 64), 2, 1024, 0, s, r);
+  VH_TRY(sc.get(scratch, scratch_bytes, p.need));
+  return ln_bwd_launch(p, x, w, dy, dx, dw, db, rows, C, eps, static_cast<float*>(sc.p), s);
+}
+
+int vh_layernorm_bwd_noalloc(const float* x, const float* w, const float* dy, float* dx, float* dw,
+                             float* db, int64_t rows, int64_t C, float eps, void* stream) {
+  VH_TRY(require_init());
+  hipStream_t s = S(stream);
+  bool done;
+  VH_TRY(ln_bwd_check("vh_layernorm_bwd_noalloc", x, w, dy, dx, dw, db, rows, C, s, &done));
+  if (done) return VH_OK;
+  const bool vec = aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx);
+  LnBwdPlan p;
+  VH_TRY(ln_bwd_plan(rows, C, vec, &p));
+  if (p.need > VH_NOALLOC_SCRATCH_BYTES)
+    return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_bwd_noalloc: rows=" + std::to_string(rows) + ", C=" +
+                                        std::to_string(C) + " needs " + std::to_string(p.need) +
+                                        " bytes of scratch, more than the " +
+                                        std::to_string(VH_NOALLOC_SCRATCH_BYTES) +
+                                        "-byte device-resident scratch; use vh_layernorm_bwd");
+  void* part = vh_rt::noalloc_scratch(g_rt.device);
+  if (!part) return fail(VH_ERR_NOT_INIT, "vh_layernorm_bwd_noalloc: device-resident scratch not set up");
+  return ln_bwd_launch(p, x, w, dy, dx, dw, db, rows, C, eps, static_cast<float*>(part), s);
 }
 
 // ------------------------------------------------------------------ gelu --
