@@ -412,6 +412,30 @@ def test_cross_entropy_row_stride(vh):
     vh.check(vh.lib.vh_cross_entropy_fwd_bwd_ld(L.ptr, ld, T.ptr, GO.ptr, LOSS2.ptr, DL2.ptr, B, V, None, 0, None))
     np.testing.assert_array_equal(fetch(vh, LOSS2, (1,)), fetch(vh, LOSS, (1,)))
     np.testing.assert_array_equal(fetch(vh, DL2, (B, ld)), dl)
+    # In place (dlogits == logits): the target logit is read before the row's
+    # gradient stores, so the loss and gradients are the same bits again.
+    LOSS3, IP = out(vh, (1,)), dev(vh, padded)
+    vh.check(vh.lib.vh_cross_entropy_fwd_bwd_ld(IP.ptr, ld, T.ptr, GO.ptr, LOSS3.ptr, IP.ptr, B, V, None, 0, None))
+    np.testing.assert_array_equal(fetch(vh, LOSS3, (1,)), fetch(vh, LOSS, (1,)))
+    ip = fetch(vh, IP, (B, ld))
+    np.testing.assert_array_equal(ip[:, :V], dl[:, :V])
+    assert np.all(ip[:, V:] == 7.0)
+
+
+@pytest.mark.parametrize("B,V", [(64, 50257), (48, 70001)])
+def test_cross_entropy_fwd_bwd_in_place(vh, B, V):
+    """The fused pass in place at the GPT-2 vocabulary (row-cached kernel) and
+    past it (streaming kernels): loss and dlogits equal the out-of-place call's."""
+    r = np.random.default_rng(B)
+    logits = r.standard_normal((B, V), dtype=np.float32)
+    tg = r.integers(0, V, size=B).astype(np.float32)
+    L, T, GO = dev(vh, logits), dev(vh, tg), dev(vh, np.float32([1.0]))
+    LOSS, DL, LOSS2 = out(vh, (1,)), out(vh, (B, V)), out(vh, (1,))
+    vh.check(vh.lib.vh_cross_entropy_fwd_bwd_ld(L.ptr, V, T.ptr, GO.ptr, LOSS.ptr, DL.ptr, B, V, None, 0, None))
+    vh.check(vh.lib.vh_cross_entropy_fwd_bwd_ld(L.ptr, V, T.ptr, GO.ptr, LOSS2.ptr, L.ptr, B, V, None, 0, None))
+    np.testing.assert_array_equal(fetch(vh, LOSS2, (1,)), fetch(vh, LOSS, (1,)))
+    np.testing.assert_array_equal(fetch(vh, L, (B, V)), fetch(vh, DL, (B, V)))
+    assert_parity(fetch(vh, LOSS, (1,)), O.cross_entropy(logits, tg), name="loss")
 
 
 @pytest.mark.parametrize("akc,bkc", [(True, True), (True, False), (False, False), (False, True)])

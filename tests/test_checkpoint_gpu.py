@@ -119,6 +119,25 @@ def test_device_load_panics_and_io_errors(vh, tmp_path):
     assert not (tmp_path / "t.ve").exists()
 
 
+def test_device_load_length_mismatch_after_a_multi_chunk_tensor(vh, tmp_path):
+    """A first tensor of two staging chunks, then a second whose element count
+    disagrees with its dims: the error comes back with the reference's text and
+    the first tensor is fully loaded (its copies finish before the discarded
+    block reuses the staging buffer)."""
+    r = np.random.default_rng(9)
+    big = r.standard_normal(12_000_000, dtype=np.float32)  # 48 MB: two 32 MiB chunks
+    head = np.uint32([2, 1, big.size, big.size]).tobytes()
+    # Second tensor: rank 1, dims [2], but a length field of 3 and three values.
+    tail = np.uint32([1, 2, 3]).tobytes() + np.float32([1, 2, 3]).tobytes()
+    p = tmp_path / "len.ve"
+    p.write_bytes(head + big.tobytes() + tail)
+    b1 = dev(vh, np.zeros(big.size, np.float32))
+    b2 = dev(vh, np.zeros(2, np.float32))
+    rc = load_rc(vh, p, [b1, b2], [vh.layout((big.size,)), vh.layout((2,))])
+    assert rc == vh.VH_ERR_INVALID and "Source slice length must match tensor numel" in vh.last_error()
+    assert fetch(vh, b1, (big.size,)).tobytes() == big.tobytes()
+
+
 def test_gpt_checkpoint_round_trip(vh, tmp_path):
     """vb_gpt_save writes model.parameters() as the reference would; loading it
     back after a training step restores every parameter bit for bit."""

@@ -231,6 +231,11 @@ int vh_checkpoint_load(const char* path, int32_t n, float* const* tensors, const
     if (!contiguous(l) || (int64_t)len != ne) {
       // The reference reads the whole data block first (an I/O error if the
       // file is short), then copy_from_slice asserts (tensor.rs:817-826).
+      // The earlier tensors' last copies still read the staging buffers: let
+      // them finish before buffer 0 takes the discarded block, so those
+      // tensors end fully loaded, as the reference leaves them.
+      CK_TRY(st.wait(0));
+      CK_TRY(st.wait(1));
       for (uint64_t left = (uint64_t)len * 4; left > 0;) {
         const size_t step = left < kChunk ? (size_t)left : kChunk;
         if (std::fread(st.buf[0], 1, step, f.f) != step) {

@@ -67,6 +67,13 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
   }
   // Every load issued before the max chain starts consuming them.
   __builtin_amdgcn_sched_barrier(0);
+  const int32_t t = xent_target(a, row);
+  // MODE 2 reads the target logit here, before the team barriers below: the
+  // row's gradient stores come after them, so dlogits may alias logits.
+  float lt = 0.0f;
+  if constexpr (MODE == 2) {
+    if (threadIdx.x == 0 && t >= 0) lt = lr[t];
+  }
 #pragma unroll
   for (int k = 0; k < NV; ++k)
     if (v[k] > m) m = v[k];
@@ -79,7 +86,6 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
     s += e;
   }
   s = team_sum<XE_TEAM>(s, red);
-  const int32_t t = xent_target(a, row);
   if constexpr (MODE == 0) {
     if (threadIdx.x == 0) a.out[row] = t >= 0 ? lr[t] - m - logf(s) : 0.0f;
   }
@@ -103,7 +109,7 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
     }
   }
   if constexpr (MODE == 2) {  // after the row's registers are free
-    if (threadIdx.x == 0) a.row_loss[row] = t >= 0 ? lr[t] - m - logf(s) : 0.0f;
+    if (threadIdx.x == 0) a.row_loss[row] = t >= 0 ? lt - m - logf(s) : 0.0f;
   }
 }
 

@@ -20,6 +20,7 @@
 
 #include "../../include/vearo_hip.h"
 #include "vh_kargs.h"
+#include "arena.h"
 #include "rt_internal.h"
 
 extern "C" const unsigned char vh_code_object_start[];
@@ -100,75 +101,72 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ------------------------------------------------------------------ arena --
-// Exact-size free lists keyed by a rounded size (512 B granularity below 1 MiB,
-// 2 MiB above), 256-byte aligned blocks straight from hipMalloc. Freed blocks are
-// reused in stream order on the runtime stream.
+// The caching arena: free-list bookkeeping and reuse rules in arena.h, device
+// calls here. A freed block is reused at once on the stream its last user
+// queued work on, and on any other stream only after that stream waits for an
+// event marking the work (hipStreamWaitEvent: the device waits, the host does
+// not). Events come from a small pool.
+struct HipArenaDev {
+  using Stream = hipStream_t;
+  using Event = hipEvent_t;
+  std::vector<hipEvent_t> pool;
+  int dev_malloc(void** p, size_t r) {
+    if (hipMalloc(p, r) == hipSuccess) return 0;
+    (void)hipGetLastError();
+    return 1;
+  }
+  int dev_free(void* p) { return hipFree(p) == hipSuccess ? 0 : 1; }
+  Event record(Stream s) {
+    hipEvent_t e = nullptr;
+    if (!pool.empty()) {
+      e = pool.back();
+      pool.pop_back();
+    } else if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+      return nullptr;
+    }
+    if (hipEventRecord(e, s) != hipSuccess) {
+      (void)hipEventDestroy(e);
+      return nullptr;
+    }
+    return e;
+  }
+  int stream_wait(Stream s, Event e) { return hipStreamWaitEvent(s, e, 0) == hipSuccess ? 0 : 1; }
+  void release(Event e) { pool.push_back(e); }
+  bool persistent(Stream s) { return s == g_rt.stream; }
+  void destroy_pool() {
+    for (hipEvent_t e : pool) (void)hipEventDestroy(e);
+    pool.clear();
+  }
+};
+
 struct Arena {
   std::mutex mu;
-  std::map<size_t, std::vector<void*>> free_lists;
-  std::unordered_map<void*, size_t> live;
-  size_t live_bytes = 0, cached_bytes = 0, peak_bytes = 0, hip_bytes = 0;
+  ArenaCore<HipArenaDev> core;
 
-  static size_t rounded(size_t b) {
-    if (b == 0) b = 1;
-    if (b <= (1u << 20)) return (b + 511) & ~size_t(511);
-    const size_t g = size_t(2) << 20;
-    return (b + g - 1) / g * g;
-  }
+  static size_t rounded(size_t b) { return ArenaCore<HipArenaDev>::rounded(b); }
 
-  int release_all_cached() {
-    for (auto& kv : free_lists)
-      for (void* p : kv.second) {
-        hipError_t e = hipFree(p);
-        if (e != hipSuccess) return fail(VH_ERR_HIP, std::string("hipFree: ") + hipGetErrorString(e));
-        hip_bytes -= kv.first;
-      }
-    free_lists.clear();
-    cached_bytes = 0;
+  // A block of at least `bytes` for work queued on stream s.
+  int alloc(size_t bytes, hipStream_t s, void** out) {
+    std::lock_guard<std::mutex> lk(mu);
+    const int rc = core.alloc(bytes, s, out);
+    if (rc == 1) return fail(VH_ERR_HIP, "arena: a device call failed while allocating " + std::to_string(bytes) +
+                                             " bytes");
+    if (rc == 2)
+      return fail(VH_ERR_OOM, "hipMalloc of " + std::to_string(rounded(bytes)) + " bytes failed");
     return VH_OK;
   }
 
-  int alloc(size_t bytes, void** out) {
-    const size_t r = rounded(bytes);
+  // Returns p, last used by work queued on stream s.
+  int free(void* p, hipStream_t s) {
     std::lock_guard<std::mutex> lk(mu);
-    auto it = free_lists.find(r);
-    void* p = nullptr;
-    if (it != free_lists.end() && !it->second.empty()) {
-      p = it->second.back();
-      it->second.pop_back();
-      cached_bytes -= r;
-    } else {
-      hipError_t e = hipMalloc(&p, r);
-      if (e != hipSuccess) {
-        (void)hipGetLastError();
-        // Give the cache back to the driver and retry once.
-        int rc = release_all_cached();
-        if (rc != VH_OK) return rc;
-        e = hipMalloc(&p, r);
-        if (e != hipSuccess) {
-          (void)hipGetLastError();
-          return fail(VH_ERR_OOM, "hipMalloc of " + std::to_string(r) + " bytes failed: " +
-                                      hipGetErrorString(e));
-        }
-      }
-      hip_bytes += r;
-    }
-    live.emplace(p, r);
-    live_bytes += r;
-    peak_bytes = std::max(peak_bytes, live_bytes);
-    *out = p;
+    const int rc = core.free(p, s);
+    if (rc < 0) return fail(VH_ERR_INVALID, "vh_free: pointer not allocated by vh_alloc");
+    if (rc > 0) return fail(VH_ERR_HIP, "arena: could not record the freeing stream's event");
     return VH_OK;
   }
 
-  int free(void* p) {
-    std::lock_guard<std::mutex> lk(mu);
-    auto it = live.find(p);
-    if (it == live.end()) return fail(VH_ERR_INVALID, "vh_free: pointer not allocated by vh_alloc");
-    const size_t r = it->second;
-    live.erase(it);
-    live_bytes -= r;
-    free_lists[r].push_back(p);
-    cached_bytes += r;
+  int release_all_cached() {  // caller holds mu
+    if (core.release_all_cached() != 0) return fail(VH_ERR_HIP, "hipFree of a cached block failed");
     return VH_OK;
   }
 };
@@ -176,14 +174,17 @@ struct Arena {
 Arena g_arena;
 
 // Scratch buffer for one call: the caller's, or a block from the arena that is
-// returned (stream-ordered) when the call's launches are queued.
+// returned when the call's launches are queued (reused in stream order on the
+// call's stream, after an event wait on any other).
 struct Scratch {
   void* p = nullptr;
+  hipStream_t s = nullptr;
   bool owned = false;
   ~Scratch() {
-    if (owned && p) g_arena.free(p);
+    if (owned && p) g_arena.free(p, s);
   }
-  int get(void* user, size_t user_bytes, size_t need) {
+  int get(hipStream_t stream, void* user, size_t user_bytes, size_t need) {
+    s = stream;
     if (need == 0) return VH_OK;
     if (user) {
       if (user_bytes < need)
@@ -193,7 +194,7 @@ struct Scratch {
       p = user;
       return VH_OK;
     }
-    VH_TRY(g_arena.alloc(need, &p));
+    VH_TRY(g_arena.alloc(need, s, &p));
     owned = true;
     return VH_OK;
   }
@@ -420,10 +421,11 @@ int vh_shutdown(void) {
   {
     std::lock_guard<std::mutex> al(g_arena.mu);
     VH_TRY(g_arena.release_all_cached());
-    for (auto& kv : g_arena.live) (void)hipFree(kv.first);
-    g_arena.live.clear();
-    g_arena.live_bytes = 0;
-    g_arena.hip_bytes = 0;
+    for (auto& kv : g_arena.core.live) (void)hipFree(kv.first);
+    g_arena.core.live.clear();
+    g_arena.core.live_bytes = 0;
+    g_arena.core.dev_bytes = 0;
+    g_arena.core.dev.destroy_pool();
   }
   VH_HIP(hipFree(g_rt.err));
   VH_HIP(hipModuleUnload(g_rt.module));
@@ -453,7 +455,9 @@ int vh_check_device_error(void) {
 int vh_alloc(size_t bytes, int zero, void** out) {
   VH_TRY(require_init());
   if (!out) return fail(VH_ERR_INVALID, "vh_alloc: null out");
-  VH_TRY(g_arena.alloc(bytes, out));
+  // Blocks handed to callers belong to the runtime stream: vh_h2d / vh_d2h /
+  // vh_fill_f32 and every entry given stream = NULL queue on it.
+  VH_TRY(g_arena.alloc(bytes, g_rt.stream, out));
   if (zero) VH_TRY(fill(*out, 0.0f, (int64_t)(Arena::rounded(bytes) / 4), g_rt.stream));
   return VH_OK;
 }
@@ -461,7 +465,7 @@ int vh_alloc(size_t bytes, int zero, void** out) {
 int vh_free(void* ptr) {
   if (!ptr) return VH_OK;
   VH_TRY(require_init());
-  return g_arena.free(ptr);
+  return g_arena.free(ptr, g_rt.stream);
 }
 
 int vh_h2d(void* dst, const void* src, size_t bytes) {
@@ -507,10 +511,10 @@ int vh_fill_f32(float* out, float value, int64_t n, void* stream) {
 int vh_mem_stats_get(vh_mem_stats* out) {
   if (!out) return fail(VH_ERR_INVALID, "vh_mem_stats_get: null out");
   std::lock_guard<std::mutex> lk(g_arena.mu);
-  out->live_bytes = g_arena.live_bytes;
-  out->cached_bytes = g_arena.cached_bytes;
-  out->peak_bytes = g_arena.peak_bytes;
-  out->hip_bytes = g_arena.hip_bytes;
+  out->live_bytes = g_arena.core.live_bytes;
+  out->cached_bytes = g_arena.core.cached_bytes;
+  out->peak_bytes = g_arena.core.peak_bytes;
+  out->hip_bytes = g_arena.core.dev_bytes;
   return VH_OK;
 }
 
@@ -626,7 +630,7 @@ int vh_layernorm_bwd(const float* x, const float* w, const float* dy, float* dx,
   LnBwdPlan p;
   VH_TRY(ln_bwd_plan(rows, C, vec, &p));
   Scratch sc;
-  VH_TRY(sc.get(scratch, scratch_bytes, p.need));
+  VH_TRY(sc.get(S(stream), scratch, scratch_bytes, p.need));
   return ln_bwd_launch(p, x, w, dy, dx, dw, db, rows, C, eps, static_cast<float*>(sc.p), s);
 }
 
@@ -723,7 +727,7 @@ int vh_gelu_bias_bwd(const float* x, const float* bias, const float* dy, float* 
   const int64_t rpb = cdiv(rows, G0);
   const int64_t G = cdiv(rows, rpb);
   Scratch sc;
-  VH_TRY(sc.get(scratch, scratch_bytes, align256((size_t)G0 * (size_t)C * sizeof(float))));
+  VH_TRY(sc.get(S(stream), scratch, scratch_bytes, align256((size_t)G0 * (size_t)C * sizeof(float))));
   GeluBiasBwdArgs a{x, bias, dy, dx, static_cast<float*>(sc.p), rows, rpb, (int32_t)C};
   // Grid: 64-unit column tiles by row blocks. At [16384, 3072] 101 us against
   // 122 us for one workgroup walking each row block (measured on MI355X).
@@ -848,7 +852,7 @@ int vh_embedding_bwd(const float* ids, const float* dy, float* dW, int64_t n, in
     return fail(VH_ERR_UNSUPPORTED, "vh_embedding_bwd: size exceeds int32");
   const EmbScratchLayout L = emb_layout(n, V, D);
   Scratch sc;
-  VH_TRY(sc.get(scratch, scratch_bytes, L.total));
+  VH_TRY(sc.get(S(stream), scratch, scratch_bytes, L.total));
   char* base = static_cast<char*>(sc.p);
   auto I = [&](size_t off) { return reinterpret_cast<int32_t*>(base + off); };
   // counts, cursor and the counters are contiguous: one fill of zeros
@@ -913,7 +917,7 @@ int vh_cross_entropy_fwd_ld(const float* logits, int64_t ld, const float* target
   if (V > INT32_MAX || B > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_cross_entropy_fwd: size exceeds int32");
   hipStream_t s = S(stream);
   Scratch sc;
-  VH_TRY(sc.get(scratch, scratch_bytes, vh_cross_entropy_fwd_scratch_bytes(B)));
+  VH_TRY(sc.get(S(stream), scratch, scratch_bytes, vh_cross_entropy_fwd_scratch_bytes(B)));
   XentArgs a{logits, targets, nullptr, static_cast<float*>(sc.p), nullptr, g_rt.err, B, ld, (int32_t)V};
   VH_TRY(launch(xent_kernel("fwd", V), (unsigned)B, 1, xent_threads(xent_kernel("fwd", V)), 0, s, a));
   XentReduceArgs r{static_cast<float*>(sc.p), loss, B};
@@ -956,7 +960,7 @@ int vh_cross_entropy_fwd_bwd_ld(const float* logits, int64_t ld, const float* ta
   }
   hipStream_t s = S(stream);
   Scratch sc;
-  VH_TRY(sc.get(scratch, scratch_bytes, vh_cross_entropy_fwd_scratch_bytes(B)));
+  VH_TRY(sc.get(S(stream), scratch, scratch_bytes, vh_cross_entropy_fwd_scratch_bytes(B)));
   float* rows = static_cast<float*>(sc.p);
   XentArgs a{logits, targets, grad_out, dlogits, rows, g_rt.err, B, ld, (int32_t)V};
   VH_TRY(launch(xent_kernel("fb", V), (unsigned)B, 1, xent_threads(xent_kernel("fb", V)), 0, s, a));
@@ -1078,7 +1082,7 @@ int vh_sum_rows(const float* x, int64_t rows, int64_t C, float* out, void* scrat
   const int64_t rpb = cdiv(rows, G0);
   const int64_t G = cdiv(rows, rpb);
   Scratch sc;
-  VH_TRY(sc.get(scratch, scratch_bytes, align256((size_t)G0 * (size_t)C * sizeof(float))));
+  VH_TRY(sc.get(S(stream), scratch, scratch_bytes, align256((size_t)G0 * (size_t)C * sizeof(float))));
   float* part = static_cast<float*>(sc.p);
   ColPartialArgs a{x, part, rows, rpb, (int32_t)C};
   VH_TRY(launch("vh_col_partial", (unsigned)G, (unsigned)cdiv(C, 256), 256, 0, s, a));
@@ -1222,7 +1226,7 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
     const int64_t ks = plan.ksplit, kchunk = plan.kchunk;
     if (ks > 1) {
       void* ws = nullptr;
-      VH_TRY(g_arena.alloc((size_t)(ks * M * N) * sizeof(float), &ws));
+      VH_TRY(g_arena.alloc((size_t)(ks * M * N) * sizeof(float), s, &ws));
       // Raw partials: the reduce applies alpha, the addend and accumulation.
       GemmArgs g = gemm_args(d, lda, ldb, tiles_m, tiles_n);
       g.E = nullptr;
@@ -1237,7 +1241,7 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
         const int64_t blocks = std::min<int64_t>(cdiv(M * N, 256), 8192);
         rc = launch("vh_gemm_reduce", (unsigned)blocks, 1, 256, 0, s, r);
       }
-      g_arena.free(ws);  // stream-ordered reuse
+      g_arena.free(ws, s);
       return rc;
     }
   }
@@ -1273,8 +1277,9 @@ namespace {
 // stride (the reference makes every matmul operand contiguous, cpu:307-308).
 struct Contig {
   void* p = nullptr;
+  hipStream_t s = nullptr;
   ~Contig() {
-    if (p) g_arena.free(p);
+    if (p) g_arena.free(p, s);
   }
 };
 
@@ -1287,7 +1292,8 @@ int matmul_operand(const float* x, const vh_layout* l, Contig* tmp, const float*
                   l->dims[r - 2] == 1;
   if (ok) return VH_OK;
   const int64_t n = numel(l);
-  VH_TRY(g_arena.alloc((size_t)n * sizeof(float), &tmp->p));
+  tmp->s = s;
+  VH_TRY(g_arena.alloc((size_t)n * sizeof(float), s, &tmp->p));
   VH_TRY(vh_strided_copy(x, l, static_cast<float*>(tmp->p), s));
   int64_t acc = 1;
   for (int i = r - 1; i >= 0; --i) {
@@ -1560,7 +1566,7 @@ int vh_fused_attention_fwd(const float* q, const vh_layout* ql, const float* k, 
   if (sh.S > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_fused_attention_fwd: S too large");
   hipStream_t s = S(stream);
   Scratch sc;
-  VH_TRY(sc.get(scratch, scratch_bytes, vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 0)));
+  VH_TRY(sc.get(S(stream), scratch, scratch_bytes, vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 0)));
   float* P = static_cast<float*>(sc.p);
   VH_TRY(attn_probs(q, ql, k, kl, mask, mst, causal, sh, P, s));
   vh_gemm_desc d{};  // out = P v
@@ -1610,7 +1616,7 @@ int vh_fused_attention_bwd(const float* q, const vh_layout* ql, const float* k, 
   if (sh.S > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_fused_attention_bwd: S too large");
   hipStream_t s = S(stream);
   Scratch sc;
-  VH_TRY(sc.get(scratch, scratch_bytes, vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 1)));
+  VH_TRY(sc.get(S(stream), scratch, scratch_bytes, vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 1)));
   float* P = static_cast<float*>(sc.p);
   float* G = P + vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 0) / sizeof(float);
   // P, recomputed from q and k as the reference does (cpu:2520-2569).
@@ -1638,7 +1644,7 @@ int vh_fused_attention_bwd_probs(const float* P, const float* q, const vh_layout
   if (sh.S > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_fused_attention_bwd_probs: S too large");
   hipStream_t s = S(stream);
   Scratch sc;
-  VH_TRY(sc.get(scratch, scratch_bytes, vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 0)));
+  VH_TRY(sc.get(S(stream), scratch, scratch_bytes, vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 0)));
   return attn_bwd_from_probs(P, static_cast<float*>(sc.p), q, ql, k, kl, v, vl, causal, dout, dol, dq, dql, dk,
                              dkl, dv, dvl, sh, s);
 }
