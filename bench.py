@@ -7,27 +7,31 @@ over one synthetic batch at GPT-2-small shape,
   causal softmax bwd   from the saved input x and dy, as the autograd arm does
   layernorm backward   (x, w, dy -> dx, dgamma, dbeta)
 issued in that order on the runtime stream, as a training step meets them
-(forward, then backward in reverse). Other configs of BASELINE.json are
-available with --workload (gelu_bias, embedding_uniform, embedding_zipf,
-cross_entropy, layernorm_cfg0, gpt2_block); each prints its own line.
-gpt2_block is config[4]'s training step (token+position embedding, one pre-LN
-transformer block, final layernorm, lm_head, cross-entropy, backward, AdamW);
-its value is milliseconds per step and its roofline is the f32 matrix cores.
+(forward, then backward in reverse). After it, the default run measures the
+other configs of BASELINE.json the same way and reports them in the same JSON
+line under "configs" (gpt2_block -- config[4]'s training step, whose ms per
+step is also the top-level "gpt2_block_ms" -- gelu_bias, embedding_uniform,
+embedding_zipf, cross_entropy, softmax_dense -- the dense form the BackendOps
+slot runs -- and layernorm_cfg0); --no-extra skips them, --workload NAME
+prints one config's own line.
 
 Inputs are resident in HBM before timing. Buffers that would otherwise stay in
 the 256 MB MALL between uses alternate between two sets (or are flushed by the
 step's own multi-GB traffic), so every kernel reads cold data.
 
-value = algorithmic bytes per step / wall time per step (GB/s); algorithmic
-bytes count each necessary HBM transfer once (the live causal triangle only for
-softmax reads, distinct rows only for embedding gathers). The timed steps are
-issued back to back with nothing between the ops; per-kernel durations come
-from a second pass of the same steps with HIP events on the runtime stream
-around each launch; `roofline`
-reports the longest kernel, with `traffic` from the committed rocprofv3
-FETCH_SIZE / WRITE_SIZE passes when present. cpu_baseline times the CPU oracle
-(the C restatement of the reference's CPU backend, one thread) on a bounded
-sample of the same workload, counting the same algorithmic bytes.
+value = algorithmic bytes per step / wall time per step (GB/s), over exactly
+--steps steps issued back to back; algorithmic bytes count each necessary HBM
+transfer once (the live causal triangle only for causal softmax reads, distinct
+rows only for embedding gathers). Per kernel, "avg_us" is the op run alone
+--steps times back to back between two HIP events on the runtime stream (its
+average launch duration, the figure a kernel trace reports) and "in_step_us"
+the HIP events around it inside a second pass of the steps (each event's own
+cost included). `roofline` reports the longest kernel by avg_us, with
+`traffic` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes when
+present. cpu_baseline times the CPU oracle (the C restatement of the
+reference's CPU backend, one thread, as the reference's kernels are) on the
+whole headline step at its own shapes, and on bounded samples for the other
+configs; "host" records the CPU model, core count and glibc.
 
 Warmup is at least --warmup steps and at least --min-warmup-ms of them: after
 the second or so of host-side input generation the GPU has lowered its clocks,
@@ -36,7 +40,8 @@ backward runs 262 us back to back, 270-336 us for the first ~10 ms after a 1 s
 idle). The JSON's "warmup" is the number of warmup steps run; the timed region
 is exactly --steps steps either way.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--min-warmup-ms 500] [--workload NAME] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--min-warmup-ms 1000] [--workload NAME]
+                       [--no-cpu] [--no-extra]
 """
 import argparse
 import ctypes
@@ -167,19 +172,25 @@ def wl_ln_softmax(vh):
     keep = (W, Bi, sets, LNS, S, G, P, DS)
 
     def cpu(budget):
+        # The oracle on the headline shapes themselves: one whole step (LN
+        # fwd+bwd [16384,768], causal softmax fwd + the autograd arm's composite
+        # backward [16,12,1024,1024]), repeated while the budget lasts.
         import oracle
         rc = np.random.default_rng(SEED)
-        ln_rows, heads = 4096, 2
-        x = rc.standard_normal(size=(ln_rows, LN_C), dtype=np.float32)
-        dy = rc.standard_normal(size=(ln_rows, LN_C), dtype=np.float32)
-        s = causal_scores(rc, 1, heads, SM_T)
+        x = rc.standard_normal(size=(LN_ROWS, LN_C), dtype=np.float32)
+        dy = rc.standard_normal(size=(LN_ROWS, LN_C), dtype=np.float32)
+        s = causal_scores(rc, SM_B, SM_H, SM_T)
         g = rc.standard_normal(size=s.shape, dtype=np.float32)
-        t, reps = time_cpu(lambda: (oracle.layernorm(x, w, b, 1e-5), oracle.softmax(s, 3),
-                                    oracle.softmax_backward_composite(s, g, 3),
-                                    oracle.layernorm_backward(x, w, b, dy, 1e-5)), budget)
-        nb = sum(ln_bytes(ln_rows, LN_C)) + sum(sm_bytes(1, heads, SM_T))
-        return nb * reps / t, (f"layernorm fwd+bwd [{ln_rows},{LN_C}] + causal softmax fwd + composite bwd "
-                               f"[1,{heads},{SM_T},{SM_T}], {reps} reps in {t:.1f} s, single thread")
+
+        def step():
+            oracle.layernorm(x, w, b, 1e-5)
+            oracle.softmax(s, 3)
+            oracle.softmax_backward_composite(s, g, 3)
+            oracle.layernorm_backward(x, w, b, dy, 1e-5)
+        t, reps = time_cpu(step, budget)
+        return (lf + lb + sf + sb) * reps / t, (f"the whole headline step at its own shapes (LN [{LN_ROWS},{LN_C}], "
+                                                f"softmax [{SM_B},{SM_H},{SM_T},{SM_T}]), {reps} step(s) in {t:.1f} s, "
+                                                f"single thread (the reference's CPU kernels spawn none)")
 
     info = {"workload": "layernorm fwd+bwd [16384,768] + causal softmax fwd+bwd [16,12,1024,1024]",
             "ln_shape": [LN_ROWS, LN_C], "softmax_shape": [SM_B, SM_H, SM_T, SM_T]}
@@ -300,6 +311,33 @@ def wl_cross_entropy(vh):
 
     return ops, {"workload": "cross-entropy fwd+bwd over logits [16384,50257] (cfg[4] lm_head output)"}, cpu, \
         (L, T, GO, LOSS, DL, SC), None
+
+
+def wl_softmax_dense(vh):
+    """The softmax the BackendOps slot runs: vearo's attention adds the causal
+    mask to the scores (scores.add(mask).softmax(3)), so the slot sees a plain
+    [rows, T] softmax and reads every entry (causal = 0). Same scores (-inf
+    above the diagonal), dense accounting: fwd R x + W y, bwd R x + R dy + W dx."""
+    B, H, T = 16, 12, 1024
+    rs = np.random.default_rng(SEED + 2)
+    S = vh.DeviceBuffer.from_array(causal_scores(rs, B, H, T))
+    G = vh.DeviceBuffer.from_array(rs.standard_normal(size=(B, H, T, T), dtype=np.float32))
+    n = B * H * T * T
+    P, DS = vh.DeviceBuffer(4 * n), vh.DeviceBuffer(4 * n)
+    rows = B * H * T
+    ops = [("softmax_dense_fwd", 8 * n, lambda i: vh.lib.vh_softmax_fwd(S.ptr, P.ptr, rows, T, 0, None)),
+           ("softmax_dense_bwd", 12 * n, lambda i: vh.lib.vh_softmax_bwd(S.ptr, G.ptr, DS.ptr, rows, T, 1, 0, None))]
+
+    def cpu(budget):
+        import oracle
+        rc = np.random.default_rng(SEED + 2)
+        s = causal_scores(rc, 1, 2, T)
+        g = rc.standard_normal(size=s.shape, dtype=np.float32)
+        t, reps = time_cpu(lambda: (oracle.softmax(s, 3), oracle.softmax_backward_composite(s, g, 3)), budget)
+        return 20 * s.size * reps / t, f"softmax fwd + composite bwd on [1,2,{T},{T}], {reps} reps, single thread"
+
+    return ops, {"workload": "softmax fwd+bwd [16,12,1024,1024], dense (the BackendOps slot form)"}, cpu, \
+        (S, G, P, DS), None
 
 
 def gpt_fwd_flops(B, S, D, H, F, V):
@@ -445,15 +483,100 @@ def run_checkpoint(args, vh):
     print(json.dumps(res), flush=True)
 
 
-WORKLOADS = {"ln_softmax": wl_ln_softmax, "gpt2_block": wl_gpt2_block, "layernorm_cfg0": wl_layernorm_cfg0, "gelu_bias": wl_gelu_bias,
-             "embedding_uniform": wl_embedding_uniform, "embedding_zipf": wl_embedding_zipf,
-             "cross_entropy": wl_cross_entropy, "checkpoint": run_checkpoint}
+WORKLOADS = {"ln_softmax": wl_ln_softmax, "gpt2_block": wl_gpt2_block, "layernorm_cfg0": wl_layernorm_cfg0,
+             "gelu_bias": wl_gelu_bias, "embedding_uniform": wl_embedding_uniform,
+             "embedding_zipf": wl_embedding_zipf, "cross_entropy": wl_cross_entropy,
+             "softmax_dense": wl_softmax_dense, "checkpoint": run_checkpoint}
+# Run by default after the headline, each reported under "configs" in the one line.
+EXTRA = ["gpt2_block", "gelu_bias", "embedding_uniform", "embedding_zipf", "cross_entropy", "softmax_dense",
+         "layernorm_cfg0"]
 
 
-def report_step_ms(args, vh, hip, stream, ops, info, cpu, per, wall, K):
-    """The bench line of a training-step workload: value = ms per step."""
+def host_info():
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    try:
+        glibc = os.confstr("CS_GNU_LIBC_VERSION")
+    except (ValueError, OSError):
+        glibc = None
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "glibc": glibc}
+
+
+def measure(vh, hip, stream, ops, K, warmup, min_warmup_ms):
+    """Warm up (at least `warmup` steps and `min_warmup_ms`), time exactly K
+    steps back to back (wall clock around them, synchronised on both sides),
+    then per-op times two ways: HIP events between the ops of a second pass of
+    K steps ("in_step": includes each event's own cost), and each op alone K
+    times back to back between two events ("avg": the op's average launch
+    duration, what a kernel trace reports plus the gap between launches)."""
+    vh.sync()
+    warm = 0
+    t_w = time.perf_counter()
+    while warm < warmup or time.perf_counter() - t_w < min_warmup_ms / 1e3:
+        for _, _, call in ops:
+            vh.check(call(warm))
+        warm += 1
+        if warm % 8 == 0:
+            vh.sync()  # wall time then tracks the GPU's, not the launch queue's
+    vh.sync()
+    t0 = time.perf_counter()
+    for i in range(K):
+        for _, _, call in ops:
+            vh.check(call(i))
+    hip.sync(stream)
+    wall = time.perf_counter() - t0
+    vh.sync()
+    ev = [[hip.event() for _ in range(len(ops) + 1)] for _ in range(K)]
+    for i in range(K):
+        e = ev[i]
+        hip.record(e[0], stream)
+        for j, (_, _, call) in enumerate(ops):
+            vh.check(call(i))
+            hip.record(e[j + 1], stream)
+    hip.sync(stream)
+    vh.sync()
+    in_step = {n: sum(hip.elapsed_ms(ev[i][j], ev[i][j + 1]) for i in range(K)) / K
+               for j, (n, _, _) in enumerate(ops)}
+    avg = {}
+    for n, _, call in ops:
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0, stream)
+        for i in range(K):
+            vh.check(call(i))
+        hip.record(e1, stream)
+        hip.sync(stream)
+        avg[n] = hip.elapsed_ms(e0, e1) / K
+    vh.sync()
+    return {"warmup": warm, "wall": wall, "in_step_ms": in_step, "avg_ms": avg}
+
+
+def summarize_bytes(ops, m, K, traffic_file=None):
+    kernels = {}
+    for n, nb, _ in ops:
+        a_s, s_s = m["avg_ms"][n] / 1e3, m["in_step_ms"][n] / 1e3
+        kernels[n] = {"avg_us": round(a_s * 1e6, 2), "in_step_us": round(s_s * 1e6, 2), "bytes": nb,
+                      "gbps": round(nb / a_s / 1e9, 1), "frac": round(nb / a_s / 1e9 / PEAK_GBPS, 4)}
+    tpath = os.path.join(ROOT, "profiles", traffic_file) if traffic_file else None
+    if tpath and os.path.exists(tpath):
+        with open(tpath) as f:
+            tk = json.load(f).get("kernels", {})
+        for n in kernels:
+            if n in tk:
+                kernels[n]["traffic_bytes"] = tk[n]["traffic_bytes"]
+    step_bytes = sum(o[1] for o in ops)
+    ms = m["wall"] / K * 1e3
+    return {"ms_per_step": round(ms, 4), "bytes_per_step": step_bytes,
+            "gbps": round(step_bytes / (ms / 1e3) / 1e9, 1),
+            "frac": round(step_bytes / (ms / 1e3) / 1e9 / PEAK_GBPS, 4), "kernels": kernels}
+
+
+def lm_head_probe(vh, hip, stream, info):
     pname, pflops, pcall = info.pop("_probe")
-    info.pop("_mode")
     reps = 10
     vh.check(pcall(0))
     e0, e1 = hip.event(), hip.event()
@@ -464,29 +587,41 @@ def report_step_ms(args, vh, hip, stream, ops, info, cpu, per, wall, K):
     hip.sync(stream)
     p_s = hip.elapsed_ms(e0, e1) / reps / 1e3
     achieved = pflops / p_s / 1e12
-    name, flops, _ = ops[0]
-    step_s = per[name] / K / 1e3
-    kernels = {name: {"avg_ms": round(step_s * 1e3, 3), "flops": flops,
-                      "tflops": round(flops / step_s / 1e12, 2)},
-               pname: {"avg_us": round(p_s * 1e6, 1), "flops": pflops, "tflops": round(achieved, 2)}}
-    roofline = {"bound": "mfma", "kernel": pname, "impl": "hipBLASLt f32 (vh_gemm, plain product)",
-                "achieved": round(achieved, 2), "peak": PEAK_F32_MFMA_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK_F32_MFMA_TFLOPS, 4), "traffic": None}
-    cpu_res = None
-    if not args.no_cpu:
-        ms, threads, sample = cpu(args.cpu_seconds)
-        cpu_res = {"value": round(ms, 1), "unit": "ms per step", "cores": threads, "kind": "port",
-                   "sample": sample}
-    res = {
-        "metric": "GPT block step ms (config[4]: fwd + bwd + AdamW)", "value": round(wall / K * 1e3, 3),
-        "unit": "ms", "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": round(wall / K * 1e3, 3),
-        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (random ids/targets, weights ~N(0,0.02))", "config": info,
-        "tflops_per_s": round(info["flops_per_step"] / (wall / K) / 1e12, 2),
-        "frac_of_peak": round(info["flops_per_step"] / (wall / K) / 1e12 / PEAK_F32_MFMA_TFLOPS, 4),
-        "kernels": kernels, "roofline": roofline, "cpu_baseline": cpu_res,
-    }
-    print(json.dumps(res), flush=True)
+    return pname, {"avg_us": round(p_s * 1e6, 1), "flops": pflops, "tflops": round(achieved, 2),
+                   "frac": round(achieved / PEAK_F32_MFMA_TFLOPS, 4)}
+
+
+def run_one(name, vh, hip, stream, args, cpu_budget):
+    """Set up one workload, measure it, time its CPU baseline; returns a summary."""
+    ops, info, cpu, keep, traffic_file = WORKLOADS[name](vh)
+    m = measure(vh, hip, stream, ops, args.steps, args.warmup, args.min_warmup_ms)
+    K = args.steps
+    if info.get("_mode") == "step_ms":
+        info.pop("_mode")
+        pname, probe = lm_head_probe(vh, hip, stream, info)
+        step_s = m["wall"] / K
+        flops = info["flops_per_step"]
+        res = {"ms_per_step": round(step_s * 1e3, 3), "tflops": round(flops / step_s / 1e12, 2),
+               "frac_of_f32_mfma_peak": round(flops / step_s / 1e12 / PEAK_F32_MFMA_TFLOPS, 4),
+               "kernels": {pname: probe}, "config": info,
+               "roofline": {"bound": "mfma", "kernel": pname, "achieved": probe["tflops"],
+                            "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": probe["frac"], "traffic": None}}
+        if cpu_budget is not None:
+            ms, threads, sample = cpu(cpu_budget)
+            res["cpu_baseline"] = {"value": round(ms, 1), "unit": "ms per step", "cores": threads, "kind": "port",
+                                   "sample": sample, "host": host_info()}
+    else:
+        res = summarize_bytes(ops, m, K, traffic_file)
+        res["config"] = info
+        if cpu_budget is not None:
+            rate, sample = cpu(cpu_budget)
+            res["cpu_baseline"] = {"value": round(rate / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                                   "sample": sample + "; GB/s counts the same algorithmic bytes as the GPU figure"}
+    res["warmup_steps"] = m["warmup"]
+    del keep, ops
+    vh.sync()
+    vh.check(vh.lib.vh_empty_cache())
+    return res
 
 
 def main():
@@ -494,11 +629,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--min-warmup-ms", type=float, default=500.0,
+    ap.add_argument("--min-warmup-ms", type=float, default=1000.0,
                     help="keep warming up until this much wall time has passed (GPU clocks recover "
                          "from the idle of input generation)")
     ap.add_argument("--workload", default="ln_softmax", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="headline only (no other configs in the line)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 4 device-to-device copies of 1 GiB (a copy kernel of known "
@@ -530,94 +666,60 @@ def main():
         print(json.dumps({"calibrate_copy_bytes": nb, "copies": 4,
                           "copy_gbps": round(4 * 2 * nb / (ms / 1e3) / 1e9, 1)}), flush=True)
         return
-
     if args.workload == "checkpoint":
         run_checkpoint(args, vh)
         return
-    ops, info, cpu, keep, traffic_file = WORKLOADS[args.workload](vh)
-    vh.sync()
-    names = [o[0] for o in ops]
-    warm = 0
-    t_w = time.perf_counter()
-    while warm < args.warmup or time.perf_counter() - t_w < args.min_warmup_ms / 1e3:
-        for _, _, call in ops:
-            vh.check(call(warm))
-        warm += 1
-        if warm % 8 == 0:
-            vh.sync()  # wall time then tracks the GPU's, not the launch queue's
-    vh.sync()
-    args.warmup = warm
 
+    cpu_budget = None if args.no_cpu else args.cpu_seconds
+    head = run_one(args.workload, vh, hip, stream, args, cpu_budget)
     K = args.steps
-    # The timed steps carry no instrumentation between the ops: the value is
-    # the wall time of exactly K steps issued back to back.
-    vh.sync()
-    t0 = time.perf_counter()
-    for i in range(K):
-        for _, _, call in ops:
-            vh.check(call(i))
-    hip.sync(stream)
-    wall = time.perf_counter() - t0
-    vh.sync()
-    # Per-op times from a second pass of K steps with a HIP event between ops
-    # (the events themselves cost a little; that pass is not the value).
-    ev = [[hip.event() for _ in range(len(ops) + 1)] for _ in range(K)]
-    for i in range(K):
-        e = ev[i]
-        hip.record(e[0], stream)
-        for j, (_, _, call) in enumerate(ops):
-            vh.check(call(i))
-            hip.record(e[j + 1], stream)
-    hip.sync(stream)
-    vh.sync()
-
-    per = {n: 0.0 for n in names}
-    for i in range(K):
-        for j, n in enumerate(names):
-            per[n] += hip.elapsed_ms(ev[i][j], ev[i][j + 1])
-    kernels = {}
-    for n, nb, _ in ops:
-        avg_s = per[n] / K / 1e3
-        gbps = nb / avg_s / 1e9
-        kernels[n] = {"avg_us": round(avg_s * 1e6, 2), "bytes": nb, "gbps": round(gbps, 1),
-                      "frac": round(gbps / PEAK_GBPS, 4)}
-    if info.get("_mode") == "step_ms":
-        report_step_ms(args, vh, hip, stream, ops, info, cpu, per, wall, K)
-        del keep
+    common = {"n_gpus": 1, "steps": K, "warmup": head.pop("warmup_steps"), "scaling": "weak",
+              "vs_baseline": None, "dtype": "f32"}
+    if args.workload == "gpt2_block":
+        res = {"metric": "GPT block step ms (config[4]: fwd + bwd + AdamW)", "value": head["ms_per_step"],
+               "unit": "ms", **common, "ms_per_step": head["ms_per_step"], "higher_is_better": False,
+               "data": "synthetic (random ids/targets, weights ~N(0,0.02))", **head}
+        print(json.dumps(res), flush=True)
         return
-    step_bytes = sum(o[1] for o in ops)
-    value = step_bytes / (wall / K) / 1e9
-    dom = max(names, key=lambda n: per[n])
-    # HBM traffic per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-    # passes over this same workload, scaled by the counters' reading of a copy of
-    # known size (profiles/<file>.json); null when absent.
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", traffic_file) if traffic_file else None
-    if tpath and os.path.exists(tpath):
-        with open(tpath) as f:
-            tk = json.load(f).get("kernels", {})
-        for n in names:
-            if n in tk:
-                kernels[n]["traffic_bytes"] = tk[n]["traffic_bytes"]
-        traffic = tk.get(dom, {}).get("traffic_bytes")
-    roofline = {"bound": "hbm", "kernel": dom, "achieved": kernels[dom]["gbps"], "peak": PEAK_GBPS,
-                "unit": "GB/s", "frac": kernels[dom]["frac"], "traffic": traffic}
-    cpu_res = None
-    if not args.no_cpu:
-        rate, sample = cpu(args.cpu_seconds)
-        cpu_res = {"value": round(rate / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-                   "sample": sample + "; GB/s counts the same algorithmic bytes as the GPU figure"}
-    info["bytes_per_step"] = step_bytes
-    res = {
-        "metric": METRIC if args.workload == "ln_softmax" else f"{args.workload} fwd+bwd HBM GB/s",
-        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K,
-        "warmup": args.warmup, "ms_per_step": round(wall / K * 1e3, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": info, "frac_of_peak": round(value / PEAK_GBPS, 4), "kernels": kernels,
-        "roofline": roofline, "cpu_baseline": cpu_res,
-    }
+    kernels = head["kernels"]
+    dom = max(kernels, key=lambda n: kernels[n]["avg_us"])
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": kernels[dom]["gbps"], "peak": PEAK_GBPS, "unit": "GB/s",
+                "frac": kernels[dom]["frac"], "traffic": kernels[dom].get("traffic_bytes")}
+    info = head["config"]
+    info["bytes_per_step"] = head["bytes_per_step"]
+    res = {"metric": METRIC if args.workload == "ln_softmax" else f"{args.workload} fwd+bwd HBM GB/s",
+           "value": head["gbps"], "unit": "GB/s", **common, "ms_per_step": head["ms_per_step"],
+           "higher_is_better": True, "data": "synthetic", "config": info, "frac_of_peak": head["frac"],
+           "kernels": kernels, "roofline": roofline, "cpu_baseline": head.get("cpu_baseline")}
+    if res["cpu_baseline"] is not None:
+        res["cpu_baseline"]["host"] = host_info()
+    if args.workload == "ln_softmax":
+        lnk = [kernels["layernorm_fwd"], kernels["layernorm_bwd"]]
+        ln_us = sum(k["avg_us"] for k in lnk)
+        ln_b = sum(k["bytes"] for k in lnk)
+        res["layernorm_fwd_bwd"] = {"avg_us": round(ln_us, 2), "bytes": ln_b, "gbps": round(ln_b / ln_us / 1e3, 1),
+                                    "frac": round(ln_b / ln_us / 1e3 / PEAK_GBPS, 4)}
+        smk = [kernels["softmax_fwd"], kernels["softmax_bwd"]]
+        sm_us = sum(k["avg_us"] for k in smk)
+        sm_b = sum(k["bytes"] for k in smk)
+        res["softmax_fwd_bwd"] = {"avg_us": round(sm_us, 2), "bytes": sm_b, "gbps": round(sm_b / sm_us / 1e3, 1),
+                                  "frac": round(sm_b / sm_us / 1e3 / PEAK_GBPS, 4)}
+    if args.workload == "ln_softmax" and not args.no_extra:
+        # The other configs of BASELINE.json, each measured the same way; their
+        # CPU baselines are bounded samples (a few seconds each).
+        configs = {}
+        ebudget = None if args.no_cpu else min(3.0, args.cpu_seconds)
+        for name in EXTRA:
+            t0 = time.perf_counter()
+            configs[name] = run_one(name, vh, hip, stream, args, ebudget)
+            configs[name]["wall_s"] = round(time.perf_counter() - t0, 1)
+            print(f"# {name} done ({configs[name]['wall_s']} s)", file=sys.stderr, flush=True)
+        g = configs["gpt2_block"]
+        res["gpt2_block_ms"] = g["ms_per_step"]
+        res["gpt2_block_tflops"] = g["tflops"]
+        res["gpt2_block_frac_of_f32_mfma_peak"] = g["frac_of_f32_mfma_peak"]
+        res["configs"] = configs
     print(json.dumps(res), flush=True)
-    del keep
 
 
 if __name__ == "__main__":
