@@ -227,6 +227,25 @@ def test_embedding_shapes(vh, n, V, D):
     check_embedding_grad(fetch(vh, DW, (V, D)), ids, dy, V)
 
 
+def test_embedding_sorted_and_general_paths_agree(vh):
+    """The same Zipf ids through the sorted path (V = 50257) and the general
+    one (V = 70000 > 65534, the rows past 50257 unused): the same bits in the
+    shared rows -- the same light-row order, 32-hit tasks and final grouping --
+    and zeros past them."""
+    r = rng(31)
+    n, D = 16384, 768
+    ids = zipf_ids(r, n, 50257)
+    dy = r.normal(size=(n, D)).astype(np.float32)
+    I, DY = dev(vh, ids), dev(vh, dy)
+    A, B = out(vh, (50257, D)), out(vh, (70000, D))
+    vh.check(vh.lib.vh_embedding_bwd(I.ptr, DY.ptr, A.ptr, n, 50257, D, None, 0, None))
+    vh.check(vh.lib.vh_embedding_bwd(I.ptr, DY.ptr, B.ptr, n, 70000, D, None, 0, None))
+    a, b = fetch(vh, A, (50257, D)), fetch(vh, B, (70000, D))
+    np.testing.assert_array_equal(a, b[:50257])
+    assert not b[50257:].any()
+    check_embedding_grad(a, ids, dy, 50257)
+
+
 def test_embedding_heavy_token_clustered(vh):
     # A heavy token whose hits all sit at the end of the positions: the chunks
     # before them hold nothing, the last chunks hold everything.

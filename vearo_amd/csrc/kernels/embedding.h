@@ -6,7 +6,26 @@
 // loads/stores when D % 4 == 0. ids are f32 as in the reference API.
 //
 // Backward (lib.rs:920-980): dW = zeros[V, D]; dW[tok_i] += dy[i] for i ascending.
-// No float atomics; dW is written exactly once (dense, 4*V*D bytes), dy read once.
+// No float atomics; dy is read once.
+// Sorted path (n <= 16384, V < 65535 -- every BASELINE config), three launches:
+//   1. emb_sort    : workgroup 0 sorts the n keys (token << 14 | position) by
+//                    token in LDS -- a stable LSD radix sort, two 8-bit passes,
+//                    each key's rank among equal digits taken from eight wave
+//                    ballots (no atomics) -- so positions stay ascending within
+//                    a token; then it cuts the sorted array into one segment
+//                    per distinct token and numbers the heavy tokens (more than
+//                    EMB_LIGHT hits) and their 32-hit tasks with block-wide
+//                    prefix sums. Meanwhile workgroups 1.. write dW's zeros
+//                    (the sort, ~10 us on one CU, hides under that 154 MB
+//                    write at GPT-2 size); the rows with hits are rewritten by
+//                    launches 2 and 3.
+//   2. emb_sum     : one wave per light segment adds its dy rows in ascending
+//                    position order from 0.0 -- the CPU loop's exact f32 order,
+//                    so those rows are bit-exact -- and writes the row; one
+//                    wave per (heavy task, 64-unit column slice) adds its 32
+//                    hits' rows in order into a partial row.
+//   3. emb_heavy_final (below).
+// General path (larger n or V), six launches and integer atomics on counters:
 //   1. emb_tokens : validate/round ids; integer histogram of tokens, with the
 //                   duplicates inside each wave merged first (one atomic per
 //                   distinct token per wave, so hot tokens do not serialise)
@@ -18,13 +37,13 @@
 //   4. emb_rows   : the leading workgroups run heavy tasks while the rest stream
 //                   the vocabulary rows, one wave per row: zeros for an unused
 //                   row; for a light row, its <= 16 positions sorted in registers
-//                   and the dy rows added in ascending position order from 0.0 --
-//                   the CPU loop's exact f32 order, so those rows are bit-exact.
+//                   and the dy rows added in ascending position order from 0.0.
 //                   A heavy task gathers the positions of its 32 ranks (visiting
 //                   only blocks that hold them) and sums their rows in order into
 //                   a partial row, as one wave per 64-unit column slice (one unit
 //                   per lane, 16 rows in flight).
-//   5. emb_heavy_final: one wave per (heavy row, column slice) adds the row's
+// Both paths end with
+//   emb_heavy_final: one wave per (heavy row, column slice) adds the row's
 //                   partials: each group of 8 in task order, then the group sums
 //                   in group order, into dW (a fixed grouping of the same sum:
 //                   deterministic, within f32 rounding of the CPU's order). A
@@ -32,6 +51,8 @@
 //                   device-scope fences, and on this GPU each one writes back
 //                   and invalidates an XCD's whole L2 (measured: they made the
 //                   Zipf case 1.8x slower once the tasks were split in slices).
+// The two paths give the same bits: the same light-row order, the same 32-hit
+// tasks and the same final grouping.
 #pragma once
 #include "common.h"
 
@@ -412,6 +433,389 @@ VH_DEV void emb_heavy_final_impl(const EmbFinalArgs& a) {
       }
 #pragma unroll
       for (int q = 0; q < EMB_FINAL_GROUPS; ++q) {
+        const int32_t g = g0 + q;
+        if (g < ngrp) {
+          const int32_t gsize = min(EMB_GROUP, nch - g * EMB_GROUP);
+          Unit<VW> gs = zero_unit<VW>();
+#pragma unroll
+          for (int r = 0; r < EMB_GROUP; ++r) {
+            if (r < gsize) {
+#pragma unroll
+              for (int j = 0; j < VW; ++j) gs.v[j] += d[q][r].v[j];
+            }
+          }
+          if (ngrp == 1) {
+            total = gs;
+          } else {
+#pragma unroll
+            for (int j = 0; j < VW; ++j) total.v[j] += gs.v[j];
+          }
+        }
+      }
+    }
+    if (u < U) store_stream<VW>(a.dW + (int64_t)tok * a.D + u * VW, total);
+  }
+}
+
+// ------------------------------------------------------------- sorted path --
+#define EMB_SORT_N 16384   // keys a range workgroup holds (n <= this)
+#define EMB_CNT_STRIDE 17  // words per digit row of the [digit][wave] counts (odd: no bank conflicts)
+#define EMB_LT_BITS 6      // bits per pass over the 12-bit range-local token
+
+// Inclusive prefix sum over the 64 lanes of a wave (DPP row shifts within
+// rows of 16, then the row_bcast steps across rows; lanes a step does not
+// write keep 0 to add).
+VH_DEV uint32_t wave_incl_scan(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
+  return v;
+}
+
+// Exclusive prefix over the 16 waves of the workgroup of one wave-uniform
+// value per wave: returns the sum over lower waves, *total the sum over all.
+// Every thread must call (two barriers).
+VH_DEV uint32_t waves_excl_scan(uint32_t v, uint32_t* wsum, uint32_t* total) {
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) wsum[w] = v;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t t = wsum[i];
+    before += i < w ? t : 0u;
+    all += t;
+  }
+  __syncthreads();
+  *total = all;
+  return before;
+}
+
+// Count of the lanes below this one in mask m.
+VH_DEV uint32_t lanes_below(unsigned long long m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Launch 1 of the sorted path, 1024-thread workgroups. Workgroup k <
+// EMB_RANGES owns the tokens t with t % EMB_RANGES == k (so a distribution's
+// hot tokens spread over the workgroups): it reads every id, keeps its
+// positions in position order, sorts them by t / EMB_RANGES (a stable LSD
+// radix sort of two 6-bit passes; each key's rank among the earlier keys of
+// its wave with the same digit comes from six wave ballots -- a lane keeps a
+// ballot where its bit is 1 and its complement where it is 0 -- no atomics)
+// into its own spos region, then cuts them into one segment per token and
+// numbers the heavy tokens (> EMB_LIGHT hits) and their 32-hit tasks, in token
+// order, with prefix sums. The other workgroups write dW's zeros (154 MB at
+// GPT-2 size, long enough to hide the sorts); rows with hits are rewritten by
+// launches 2 and 3.
+VH_DEV void emb_sort_impl(const EmbSortArgs& a) {
+  if ((int)blockIdx.x >= EMB_RANGES) {
+    const int64_t stride = (int64_t)(gridDim.x - EMB_RANGES) * blockDim.x;
+    for (int64_t u = (int64_t)(blockIdx.x - EMB_RANGES) * blockDim.x + threadIdx.x; u < a.fill_n; u += stride) {
+      if (a.vec)
+        store_stream<4>(a.dW + u * 4, zero_unit<4>());
+      else
+        store_stream<1>(a.dW + u, zero_unit<1>());
+    }
+    return;
+  }
+  __shared__ uint32_t kb[2][EMB_SORT_N];
+  __shared__ uint32_t cnt[2][64 * EMB_CNT_STRIDE];
+  __shared__ uint32_t wsum[2][16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int rk = blockIdx.x;
+  for (int e = tid; e < 2 * 64 * EMB_CNT_STRIDE; e += 1024) (&cnt[0][0])[e] = 0;
+
+  // 1. Lane l of wave w holds position w*1024 + r*64 + l in slot r. Range 0
+  // reports invalid ids. Each wave keeps its range's keys (local token << 14
+  // | position) in position order in its own LDS region kb[0][1024 w ...).
+  uint32_t mw = 0;  // keys in this wave's region
+  {
+    float tv[16];  // all 16 loads in flight before the checks
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = w * 1024 + r * 64 + lane;
+      tv[r] = i < a.n ? a.ids[i] : 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = w * 1024 + r * 64 + lane;
+      const int32_t t = i < a.n ? checked_index(tv[r], a.V) : -1;
+      if (rk == 0 && i < a.n && t < 0) {
+        atomicMin(&a.err->token, err_pack(i, tv[r]));  // the panic report, not the sum
+        a.err->token_bound = (unsigned)a.V;
+      }
+      const bool in = t >= 0 && (t % EMB_RANGES) == rk;
+      const unsigned long long mk = __ballot(in);
+      if (in) kb[0][w * 1024 + mw + lanes_below(mk)] = ((uint32_t)(t / EMB_RANGES) << 14) | (uint32_t)i;
+      mw += (uint32_t)__popcll(mk);
+    }
+  }
+  uint32_t m;
+  (void)waves_excl_scan(mw, wsum[0], &m);
+  // 2. Stable LSD sort by the local token. Pass 0 reads the waves' regions,
+  // pass 1 the dense result [0, m) in chunks of `per` per wave; either way
+  // (wave, round, lane) order is the input order.
+  const uint32_t per = ((m + 1023) / 1024) * 64;
+  uint32_t k[16], rank[16];
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const uint32_t* src = kb[pass];
+    uint32_t* dst = kb[pass ^ 1];
+    uint32_t* cn = cnt[pass];
+    const int shift = 14 + EMB_LT_BITS * pass;
+    const uint32_t jb = pass == 0 ? (uint32_t)w * 1024 : (uint32_t)w * per;
+    const uint32_t jn = pass == 0 ? mw : (m > (uint32_t)w * per ? min(per, m - (uint32_t)w * per) : 0u);
+    const int rounds = (int)((jn + 63) / 64);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if (r < rounds) {
+        const uint32_t j = (uint32_t)(r * 64 + lane);
+        const bool act = j < jn;
+        k[r] = act ? src[jb + j] : 0u;
+        const unsigned long long am = __ballot(act);
+        uint32_t plo = (uint32_t)am, phi = (uint32_t)(am >> 32);
+#pragma unroll
+        for (int b = 0; b < EMB_LT_BITS; ++b) {
+          const uint32_t rep = (uint32_t)__builtin_amdgcn_sbfe((int)k[r], shift + b, 1);  // 0 or ~0
+          const unsigned long long bal = __ballot(rep != 0u);
+          plo &= ~((uint32_t)bal ^ rep);
+          phi &= ~((uint32_t)(bal >> 32) ^ rep);
+        }
+        if (act) {
+          const unsigned long long peers = ((unsigned long long)phi << 32) | plo;
+          const uint32_t lt = lanes_below(peers);
+          const uint32_t at = ((k[r] >> shift) & 63u) * EMB_CNT_STRIDE + (uint32_t)w;
+          const uint32_t base = cn[at];
+          rank[r] = base + lt;
+          if (lt == 0) cn[at] = base + (uint32_t)__popcll(peers);
+        }
+      }
+    }
+    __syncthreads();
+    // Offsets: exclusive prefix over (digit, wave) in that order (64 x 16 =
+    // 1024 entries, one per thread), so keys land by digit, then wave, round, lane.
+    {
+      const uint32_t at = (uint32_t)(tid >> 4) * EMB_CNT_STRIDE + (uint32_t)(tid & 15);
+      const uint32_t c = cn[at];
+      const uint32_t inc = wave_incl_scan(c);
+      uint32_t all;
+      const uint32_t before = waves_excl_scan(__shfl(inc, 63, 64), wsum[pass], &all);
+      cn[at] = before + inc - c;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if (r < rounds && (uint32_t)(r * 64 + lane) < jn)
+        dst[cn[((k[r] >> shift) & 63u) * EMB_CNT_STRIDE + (uint32_t)w] + rank[r]] = k[r];
+    }
+    __syncthreads();
+  }
+  const uint32_t* sorted = kb[0];
+  int32_t* sposk = a.spos + (size_t)rk * a.n;
+  for (uint32_t j = tid; j < m; j += 1024) sposk[j] = (int32_t)(sorted[j] & 0x3FFFu);
+  // 3. Segments: heads (a local token differing from the previous key's),
+  // numbered by the count of heads before them.
+  const uint32_t jw = (uint32_t)w * per;
+  const int rounds = (int)(per / 64);
+  auto head_mask = [&](int r) {
+    const uint32_t j = jw + (uint32_t)(r * 64 + lane);
+    const bool head = j < m && (j == 0 || (sorted[j] >> 14) != (sorted[j - 1] >> 14));
+    return __ballot(head);
+  };
+  uint32_t nh = 0;
+  for (int r = 0; r < rounds; ++r) nh += (uint32_t)__popcll(head_mask(r));
+  uint32_t nseg;
+  uint32_t s0 = waves_excl_scan(nh, wsum[0], &nseg);
+  uint32_t* start = kb[1];  // segment s covers sorted[start[s], start[s + 1]) (the last ends at m)
+  for (int r = 0; r < rounds; ++r) {
+    const unsigned long long hm = head_mask(r);
+    if ((hm >> lane) & 1ull) start[s0 + lanes_below(hm)] = jw + (uint32_t)(r * 64 + lane);
+    s0 += (uint32_t)__popcll(hm);
+  }
+  __syncthreads();
+  // 4. Per segment (wave w takes [w pers, (w+1) pers) in rounds of 64): hits,
+  // and for heavy ones their entry and first task, numbered in token order.
+  const uint32_t pers = ((nseg + 1023) / 1024) * 64;
+  const int srounds = (int)(pers / 64);
+  const uint32_t sw = (uint32_t)w * pers;
+  auto seg_hits = [&](int r) -> uint32_t {
+    const uint32_t sg = sw + (uint32_t)(r * 64 + lane);
+    return sg < nseg ? (sg + 1 < nseg ? start[sg + 1] : m) - start[sg] : 0u;
+  };
+  auto tasks_of = [](uint32_t h) -> uint32_t {
+    return h > EMB_LIGHT ? (h + EMB_CHUNK_HITS - 1) / EMB_CHUNK_HITS : 0u;
+  };
+  uint32_t tot_t = 0, tot_h = 0;
+  for (int r = 0; r < srounds; ++r) {
+    const uint32_t h = seg_hits(r);
+    const unsigned long long hv = __ballot(h > EMB_LIGHT);
+    if (hv) tot_t += __shfl(wave_incl_scan(tasks_of(h)), 63, 64);
+    tot_h += (uint32_t)__popcll(hv);
+  }
+  uint32_t ntask, nheavy;
+  uint32_t tb = waves_excl_scan(tot_t, wsum[0], &ntask);
+  uint32_t hb = waves_excl_scan(tot_h, wsum[1], &nheavy);
+  int32_t* segk = a.seg + (size_t)rk * a.n * EMB_REC;
+  int32_t* heavyk = a.heavy + (size_t)rk * a.hmax * 4;
+  int32_t* hstk = a.heavy_start + (size_t)rk * a.hmax;
+  int32_t* tmapk = a.taskmap + (size_t)rk * a.tmax;
+  for (int r = 0; r < srounds; ++r) {
+    const uint32_t sg = sw + (uint32_t)(r * 64 + lane);
+    const uint32_t h = seg_hits(r), nt = tasks_of(h);
+    const unsigned long long hv = __ballot(h > EMB_LIGHT);
+    const uint32_t tinc = hv ? wave_incl_scan(nt) : 0u;
+    if (sg < nseg) {
+      const uint32_t st = start[sg];
+      const int32_t tok = (int32_t)(sorted[st] >> 14) * EMB_RANGES + rk;
+      int32_t* rec = segk + (size_t)EMB_REC * sg;
+      *reinterpret_cast<int4*>(rec) = make_int4(tok, (int32_t)st, (int32_t)h, 0);
+      if (h <= EMB_LIGHT) {
+        for (uint32_t q = 0; q < h; ++q) rec[4 + q] = (int32_t)(sorted[st + q] & 0x3FFFu);
+      } else {
+        const uint32_t e = hb + lanes_below(hv);
+        const uint32_t t0 = tb + tinc - nt;
+        *reinterpret_cast<int4*>(heavyk + 4 * e) = make_int4(tok, (int32_t)t0, (int32_t)nt, (int32_t)h);
+        hstk[e] = (int32_t)st;
+        for (uint32_t c = 0; c < nt; ++c) tmapk[t0 + c] = (int32_t)e;
+      }
+    }
+    if (hv) tb += __shfl(tinc, 63, 64);
+    hb += (uint32_t)__popcll(hv);
+  }
+  if (tid == 0) {
+    a.counts[rk] = (int32_t)nseg;
+    a.counts[EMB_RANGES + rk] = (int32_t)ntask;
+    a.counts[2 * EMB_RANGES + rk] = (int32_t)nheavy;
+  }
+}
+
+// The 16 ranges' counts of kind `kind` (0 segments, 1 tasks, 2 heavy
+// entries): lane l < 16 gets range l's inclusive prefix; *total the sum.
+VH_DEV uint32_t range_prefix(const int32_t* counts, int kind, uint32_t* total) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t c = lane < EMB_RANGES ? (uint32_t)counts[kind * EMB_RANGES + lane] : 0u;
+  const uint32_t inc = wave_incl_scan(c);
+  *total = __shfl(inc, EMB_RANGES - 1, 64);
+  return inc;
+}
+// The range holding global item x (0 <= x < total) and x's index within it.
+VH_DEV int range_of(uint32_t inc, uint32_t x, uint32_t* local) {
+  const int lane = threadIdx.x & 63;
+  const int k = __popcll(__ballot(lane < EMB_RANGES && inc <= x));
+  const uint32_t before = k > 0 ? __shfl(inc, k - 1, 64) : 0u;
+  *local = x - before;
+  return k;
+}
+
+// Launch 2 of the sorted path: 256-thread workgroups, waves striding over the
+// items [0, segments) (light segments; heavy ones are skipped) and then
+// (heavy task, column slice) pairs; tasks are numbered range by range.
+template <int VW>
+VH_DEV void emb_sum_impl(const EmbSumArgs& a) {
+  const int lane = threadIdx.x & 63;
+  const int U = a.D / VW;
+  uint32_t nseg, ntask;
+  const uint32_t seg_inc = range_prefix(a.counts, 0, &nseg);
+  const uint32_t task_inc = range_prefix(a.counts, 1, &ntask);
+  const int64_t nitems = (int64_t)nseg + (int64_t)ntask * a.slices;
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  for (int64_t it = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); it < nitems; it += nw) {
+    if (it < nseg) {
+      uint32_t s;
+      const int k = range_of(seg_inc, (uint32_t)it, &s);
+      // One load of the record: lanes 0-3 the header, 4 .. 4+hits the positions.
+      const int32_t* rec = a.seg + ((size_t)k * a.n + s) * EMB_REC;
+      const int32_t rv = lane < EMB_REC ? rec[lane] : 0;
+      const int32_t tok = __shfl(rv, 0, 64), m = __shfl(rv, 2, 64);
+      if (m > EMB_LIGHT) continue;
+      const int32_t mypos = __shfl(rv, 4 + (lane < EMB_LIGHT ? lane : 0), 64);  // ascending
+      float* o = a.dW + (int64_t)tok * a.D;
+      for (int u0 = 0; u0 < U; u0 += 64 * EMB_Q) {
+        Unit<VW> acc[EMB_Q];
+#pragma unroll
+        for (int q = 0; q < EMB_Q; ++q) acc[q] = zero_unit<VW>();
+        for (int32_t kk = 0; kk < m; kk += 4) {
+          const float* src[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) src[r] = a.dy + (int64_t)__shfl(mypos, kk + r < m ? kk + r : kk, 64) * a.D;
+          emb_add_rows<VW, true>(acc, src, m - kk < 4 ? m - kk : 4, u0, lane, U);
+        }
+#pragma unroll
+        for (int q = 0; q < EMB_Q; ++q) {
+          const int u = u0 + lane + q * 64;
+          if (u < U) store_stream<VW>(o + u * VW, acc[q]);
+        }
+      }
+    } else {
+      const int64_t item = it - nseg;
+      const uint32_t t = (uint32_t)(item / a.slices);  // global task index
+      const int u = (int)(item % a.slices) * 64 + lane;
+      uint32_t lt;
+      const int k = range_of(task_inc, t, &lt);
+      const int32_t e = a.taskmap[(size_t)k * a.tmax + lt];
+      const int4 hv = *reinterpret_cast<const int4*>(a.heavy + ((size_t)k * a.hmax + e) * 4);
+      const int32_t r0 = ((int32_t)lt - hv.y) * EMB_CHUNK_HITS;
+      const int32_t got = min(r0 + EMB_CHUNK_HITS, hv.w) - r0;
+      const int32_t mypos = lane < got ? a.spos[(size_t)k * a.n + a.heavy_start[(size_t)k * a.hmax + e] + r0 + lane] : 0;
+      Unit<VW> acc = zero_unit<VW>();
+      for (int jj = 0; jj < got; jj += EMB_BATCH) {  // ascending positions, 16 rows per batch
+        const float* src[EMB_BATCH];
+#pragma unroll
+        for (int r = 0; r < EMB_BATCH; ++r)
+          src[r] = a.dy + (int64_t)__shfl(mypos, jj + r < got ? jj + r : jj, 64) * a.D;
+        emb_add_slice<VW, true, EMB_BATCH>(acc, src, got - jj < EMB_BATCH ? got - jj : EMB_BATCH, u, U);
+      }
+      if (u < U) store_unit<VW>(a.partial + (int64_t)t * a.D + u * VW, acc);
+    }
+  }
+}
+
+// Launch 3 of the sorted path: one wave per (heavy entry, column slice of 64
+// units), striding over the entries of all ranges: dW[token] at the slice's
+// units = the sum over groups (in order, from 0.0) of the group's partials
+// summed in task order from 0.0 (groups of EMB_GROUP tasks; a row with one
+// group takes that group's sum as it is) -- the grouping of emb_heavy_final,
+// with 4 groups' partials (32 rows) in flight per batch.
+#define EMB_FINAL_GROUPS_S 4
+template <int VW>
+VH_DEV void emb_final_sorted_impl(const EmbSumArgs& a) {
+  const int lane = threadIdx.x & 63;
+  const int U = a.D / VW;
+  uint32_t nheavy, ntask;
+  const uint32_t heavy_inc = range_prefix(a.counts, 2, &nheavy);
+  const uint32_t task_inc = range_prefix(a.counts, 1, &ntask);
+  const int64_t nitems = (int64_t)nheavy * a.slices;
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  for (int64_t it = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); it < nitems; it += nw) {
+    uint32_t e;
+    const int k = range_of(heavy_inc, (uint32_t)(it / a.slices), &e);
+    const int u = (int)(it % a.slices) * 64 + lane;
+    const int4 hv = *reinterpret_cast<const int4*>(a.heavy + ((size_t)k * a.hmax + e) * 4);
+    const int32_t tok = hv.x, nch = hv.z;
+    const int64_t tb = (int64_t)(k > 0 ? __shfl(task_inc, k - 1, 64) : 0u) + hv.y;  // global first task
+    const int32_t ngrp = (nch + EMB_GROUP - 1) / EMB_GROUP;
+    Unit<VW> total = zero_unit<VW>();
+    for (int32_t g0 = 0; g0 < ngrp; g0 += EMB_FINAL_GROUPS_S) {
+      Unit<VW> d[EMB_FINAL_GROUPS_S][EMB_GROUP];
+#pragma unroll
+      for (int q = 0; q < EMB_FINAL_GROUPS_S; ++q) {
+        const int32_t g = g0 + q;
+        const int32_t gsize = g < ngrp ? min(EMB_GROUP, nch - g * EMB_GROUP) : 0;
+#pragma unroll
+        for (int r = 0; r < EMB_GROUP; ++r) {
+          if (r < gsize && u < U)
+            d[q][r] = load_unit<VW>(a.partial + (tb + g * EMB_GROUP + r) * a.D + u * VW);
+          else
+            d[q][r] = zero_unit<VW>();
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < EMB_FINAL_GROUPS_S; ++q) {
         const int32_t g = g0 + q;
         if (g < ngrp) {
           const int32_t gsize = min(EMB_GROUP, nch - g * EMB_GROUP);

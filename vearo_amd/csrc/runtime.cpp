@@ -833,12 +833,75 @@ EmbScratchLayout emb_layout(int64_t n, int64_t V, int64_t D) {
   L.total = o;
   return L;
 }
+
+// The sorted path: each of EMB_RANGES workgroups sorts the keys of the tokens
+// t % EMB_RANGES == k in LDS ((t / EMB_RANGES) << 14 | position: n <= 16384,
+// t / EMB_RANGES < 4096).
+constexpr int64_t kEmbSortMaxN = 16384;
+constexpr int64_t kEmbSortMaxV = 65534;
+bool emb_sorted_path(int64_t n, int64_t V, int64_t D) {
+  return n > 0 && n <= kEmbSortMaxN && V > 0 && V <= kEmbSortMaxV && D > 0;
+}
+struct EmbSortLayout {
+  size_t spos, seg, heavy, heavy_start, taskmap, counts, partial, total;
+  int64_t hmax, tmax;
+};
+EmbSortLayout emb_sort_layout(int64_t n, int64_t D) {
+  EmbSortLayout L;
+  L.hmax = n / (kEmbLight + 1) + 1;              // heavy tokens have > 16 hits
+  L.tmax = n / kEmbChunkHits + L.hmax + 1;       // ceil(hits / 32) tasks each
+  size_t o = 0;
+  auto take = [&](size_t elems) {
+    size_t at = o;
+    o += align256(elems * 4);
+    return at;
+  };
+  L.spos = take((size_t)EMB_RANGES * n);
+  L.seg = take((size_t)EMB_RANGES * n * EMB_REC);
+  L.heavy = take((size_t)EMB_RANGES * L.hmax * 4);
+  L.heavy_start = take((size_t)EMB_RANGES * L.hmax);
+  L.taskmap = take((size_t)EMB_RANGES * L.tmax);
+  L.counts = take(3 * EMB_RANGES);
+  L.partial = take((size_t)L.tmax * (size_t)D);
+  L.total = o;
+  return L;
+}
 }  // namespace
 
 size_t vh_embedding_bwd_scratch_bytes(int64_t n, int64_t V, int64_t D) {
   if (n <= 0 || V < 0 || D < 0) return 0;
+  if (emb_sorted_path(n, V, D)) return emb_sort_layout(n, D).total;
   return emb_layout(n, V, D).total;
 }
+
+namespace {
+// Sorted path: range sorts + zero fill, segment sums and heavy partials, heavy rows.
+int emb_bwd_sorted(const float* ids, const float* dy, float* dW, int64_t n, int64_t V, int64_t D, void* base_p,
+                   hipStream_t s) {
+  const EmbSortLayout L = emb_sort_layout(n, D);
+  char* base = static_cast<char*>(base_p);
+  auto I = [&](size_t off) { return reinterpret_cast<int32_t*>(base + off); };
+  const bool vec = D % 4 == 0 && aligned16(dy) && aligned16(dW);
+  const int64_t fill_n = V * D / (vec ? 4 : 1);
+  // One workgroup per CU (the sort's LDS): the range sorts plus fills on the rest.
+  const int64_t fill_blocks =
+      std::max<int64_t>(1, std::min<int64_t>(std::max(g_rt.cu_count, EMB_RANGES + 1) - EMB_RANGES,
+                                             cdiv(fill_n, 8192)));
+  EmbSortArgs k1{ids, dW, I(L.spos), I(L.seg), I(L.heavy), I(L.heavy_start), I(L.taskmap), I(L.counts),
+                 g_rt.err, fill_n, (int32_t)n, (int32_t)V, (int32_t)L.hmax,
+                 (int32_t)L.tmax, vec ? 1 : 0};
+  VH_TRY(launch("vh_emb_sort", (unsigned)(EMB_RANGES + fill_blocks), 1, 1024, 0, s, k1));
+  const int32_t slices = (int32_t)cdiv(D / (vec ? 4 : 1), 64);
+  EmbSumArgs k2{I(L.spos), I(L.seg), I(L.heavy), I(L.heavy_start), I(L.taskmap), I(L.counts),
+                reinterpret_cast<float*>(base + L.partial), dy, dW, (int32_t)n, (int32_t)L.hmax, (int32_t)L.tmax,
+                (int32_t)D, slices};
+  // A wave per item (segments, then heavy tasks' slices) up to 16384 waves.
+  VH_TRY(launch(vec ? "vh_emb_sum_v4" : "vh_emb_sum_v1",
+                (unsigned)std::min<int64_t>(4096, cdiv(n + L.tmax * slices, 4)), 1, 256, 0, s, k2));
+  return launch(vec ? "vh_emb_final_sorted_v4" : "vh_emb_final_sorted_v1",
+                (unsigned)std::min<int64_t>(256, cdiv(L.hmax * slices, 4)), 1, 256, 0, s, k2);
+}
+}  // namespace
 
 int vh_embedding_bwd(const float* ids, const float* dy, float* dW, int64_t n, int64_t V, int64_t D,
                      void* scratch, size_t scratch_bytes, void* stream) {
@@ -850,6 +913,11 @@ int vh_embedding_bwd(const float* ids, const float* dy, float* dW, int64_t n, in
   if (!ids || (D > 0 && !dy)) return fail(VH_ERR_INVALID, "vh_embedding_bwd: null pointer");
   if (V >= INT32_MAX || D > INT32_MAX || n >= INT32_MAX / 2)
     return fail(VH_ERR_UNSUPPORTED, "vh_embedding_bwd: size exceeds int32");
+  if (emb_sorted_path(n, V, D)) {
+    Scratch sc;
+    VH_TRY(sc.get(S(stream), scratch, scratch_bytes, emb_sort_layout(n, D).total));
+    return emb_bwd_sorted(ids, dy, dW, n, V, D, sc.p, s);
+  }
   const EmbScratchLayout L = emb_layout(n, V, D);
   Scratch sc;
   VH_TRY(sc.get(S(stream), scratch, scratch_bytes, L.total));

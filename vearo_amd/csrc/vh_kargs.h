@@ -205,6 +205,49 @@ struct EmbSegArgs {
   int32_t slices;        // column slices per heavy task (64 units of VW floats each)
 };
 
+// Embedding backward, sorted path (n <= 16384, V <= 65534). Launch 1:
+// workgroup k < EMB_RANGES sorts the keys of the tokens t % EMB_RANGES == k
+// and writes that range's lists (below); the others write dW's zeros. Launches 2
+// (segment sums, heavy partial rows) and 3 (heavy rows) walk the lists, each
+// wave taking the 16 ranges' counts and their prefix sums itself.
+#define EMB_RANGES 16
+#define EMB_REC 20  // ints per segment record: token, start, hits, 0, then a light token's positions
+struct EmbSortArgs {
+  const float* ids;
+  float* dW;             // zeroed by workgroups EMB_RANGES.. (fill_n units of 4 floats if vec, else 1)
+  int32_t* spos;         // [EMB_RANGES][n]: each range's positions sorted by token, ascending within a token
+  int32_t* seg;          // [EMB_RANGES][n][20]: token, start in the range's spos, hits, 0, then the positions
+                         // of a light token (<= 16 hits) -- one record per token
+  int32_t* heavy;        // [EMB_RANGES][hmax][4]: token, range-local first task, task count, hits
+  int32_t* heavy_start;  // [EMB_RANGES][hmax]: start in the range's spos of each heavy token's hits
+  int32_t* taskmap;      // [EMB_RANGES][tmax]: range-local heavy entry of each task
+  int32_t* counts;       // [3][EMB_RANGES]: segments, tasks, heavy entries of each range
+  VhErrRecord* err;
+  int64_t fill_n;
+  int32_t n;
+  int32_t V;
+  int32_t hmax;
+  int32_t tmax;
+  int32_t vec;
+};
+
+struct EmbSumArgs {
+  const int32_t* spos;
+  const int32_t* seg;
+  const int32_t* heavy;
+  const int32_t* heavy_start;
+  const int32_t* taskmap;
+  const int32_t* counts;
+  float* partial;  // [tasks][D], tasks numbered range by range
+  const float* dy;
+  float* dW;
+  int32_t n;
+  int32_t hmax;
+  int32_t tmax;
+  int32_t D;
+  int32_t slices;  // column slices per heavy task / heavy row (64 units of VW floats each)
+};
+
 // Heavy rows' final sums: one wave per (heavy entry, column slice).
 struct EmbFinalArgs {
   const int32_t* heavy;   // [4 * max] token, first task, task count, hits
