@@ -32,3 +32,17 @@ def vh():
 
     _abi.init(0)
     return _abi
+
+
+def pytest_sessionfinish(session, exitstatus):
+    """Writes the parity statistics of every assert_parity call (tests/parity.py)
+    to the file VH_PARITY_REPORT names, if set."""
+    path = os.environ.get("VH_PARITY_REPORT")
+    if not path:
+        return
+    import json
+
+    import parity
+
+    with open(path, "w") as f:
+        json.dump(parity.REPORT, f, indent=1)

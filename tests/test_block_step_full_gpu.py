@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+from parity import assert_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -60,6 +61,8 @@ def test_block_step_full_size_matches_oracle(vh):
         err = np.abs(grads[i] - ograds[i]).max()
         print(f"  grad {name:6s} max|cpu| {scale:.3e} max|gpu-cpu| {err:.3e}", flush=True)
         assert err <= 1e-4 * scale, (name, err, scale)
+        # Elementwise, the north-star bar |gpu - cpu| <= 1e-5 + 1e-4 |cpu| on every element.
+        assert_parity(grads[i], ograds[i], name=f"full-size block-step grad {name}")
     for p, gr in zip(params, ograds):
         O.adamw_step(p, gr, np.zeros_like(p), np.zeros_like(p), 1, *ADAM)
     t0 = time.perf_counter()
