@@ -267,6 +267,17 @@ size_t vh_sum_rows_scratch_bytes(int64_t rows, int64_t C);
 #define VH_GEMM_K_LE_M 2     /* A[m, k] == 0 for k > m (M == K) */
 #define VH_GEMM_K_GE_M 3     /* A[m, k] == 0 for k < m (M == K) */
 
+/* vh_gemm_desc.engine: which kernels carry the product. The default is this
+ * library's own matrix-core kernels, chosen by shape (large dense unbatched
+ * products: the persistent 256-row-tile kernel; everything else: the tiled
+ * kernel, split along K where the output alone cannot fill the chip). TILED
+ * forces the tiled kernel (tests of its split-K path); LIBRARY hands the
+ * dense unbatched products hipBLASLt supports to it (an A/B reference for
+ * benchmarks) and runs the rest as DEFAULT. No counterpart in the reference. */
+#define VH_GEMM_ENGINE_DEFAULT 0
+#define VH_GEMM_ENGINE_TILED 1
+#define VH_GEMM_ENGINE_LIBRARY 2
+
 /* C[m, n] = (C[m, n] +) alpha * sum_k A[m, k] B[k, n] (+ E[m, n]) over two batch
  * dims, on the f32 matrix cores. The epilogue order is v = acc*alpha;
  * v = v + E; v = C + v, i.e. the separate scale / mask / bias-add / gradient
@@ -287,8 +298,20 @@ typedef struct vh_gemm_desc {
   float alpha;
   int32_t accumulate; /* 1: add into C */
   int32_t causal;     /* VH_GEMM_* */
+  int32_t engine;     /* VH_GEMM_ENGINE_* (0 in a zero-initialised descriptor) */
 } vh_gemm_desc;
 int vh_gemm(const vh_gemm_desc* d, void* stream);
+/* Which kernels carried the calling thread's last successful vh_gemm (the main
+ * product; a ragged K tail of the persistent kernel runs on the tiled one):
+ * VH_GEMM_PATH_* (0 before any call, or for an empty product). A diagnostic
+ * for tests and benchmarks, no counterpart in the reference. */
+#define VH_GEMM_PATH_NONE 0
+#define VH_GEMM_PATH_TILED 1       /* 128-row tiles, one pass over K */
+#define VH_GEMM_PATH_SPLIT_K 2     /* 128-row tiles over K ranges + fixed-order reduce */
+#define VH_GEMM_PATH_PERSISTENT 3  /* persistent 256 x 192 tiles, stream-K last round */
+#define VH_GEMM_PATH_LIBRARY 4     /* hipBLASLt */
+#define VH_GEMM_PATH_BATCHED 5     /* persistent walk over batched short-K products */
+int vh_gemm_last_path(void);
 
 /* out = lhs @ rhs with broadcast batch dims; any strides (operands with no
  * unit stride in their last two dims are copied first, as the reference makes

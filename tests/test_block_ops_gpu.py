@@ -135,6 +135,7 @@ def gemm_desc(vh, M, N, K, a, a_sm, a_sk, b, b_sk, b_sn, c, c_sm, **kw):
     d.causal = kw.get("causal", 0)
     if "e" in kw:
         d.e, d.e_sm, d.e_sn = kw["e"], kw["e_sm"], kw["e_sn"]
+    d.engine = kw.get("engine", vh.GEMM_ENGINE_DEFAULT)
     return d
 
 
@@ -359,10 +360,12 @@ def test_sum_rows(vh, rows, C):
     assert_parity(fetch(vh, OUT, (C,)), O.reduce_to(x, (C,)), x.astype(np.float64).sum(axis=0), name="sum_rows")
 
 
-@pytest.mark.parametrize("M,N,K", [(200, 150, 8192), (768, 768, 16384), (3072, 768, 4096), (200, 64, 8192)])
+@pytest.mark.parametrize("M,N,K", [(64, 64, 8192), (200, 64, 4096), (200, 150, 8192), (768, 768, 16384)])
 def test_gemm_split_k(vh, M, N, K):
-    """Few C tiles over a long K (the weight gradients) take the split-K path:
-    partials summed in a fixed order, then the epilogue."""
+    """Few C tiles over a long K (weight-gradient shapes) on the tiled kernel's
+    split-K path, forced with the TILED engine and checked through
+    vh_gemm_last_path: the K-range partials summed in a fixed order by
+    vh_gemm_reduce, then alpha, a column bias and accumulation into C."""
     print("split-k", M, N, K, flush=True)
     r = np.random.default_rng(M + N + K)
     # dW = dy^T x as the block step issues it: A m-contiguous (dy [K, M]), B = x [K, N].
@@ -373,22 +376,117 @@ def test_gemm_split_k(vh, M, N, K):
     DY, X, BI = dev(vh, dy), dev(vh, x), dev(vh, bias)
     ref = O.matmul(np.ascontiguousarray(dy.T), x)
     ref64 = dy.T.astype(np.float64) @ x.astype(np.float64)
+    tiled = vh.GEMM_ENGINE_TILED
     C = out(vh, (M, N))
-    d = gemm_desc(vh, M, N, K, DY.ptr, 1, M, X.ptr, N, 1, C.ptr, N)
+    d = gemm_desc(vh, M, N, K, DY.ptr, 1, M, X.ptr, N, 1, C.ptr, N, engine=tiled)
     vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+    assert vh.lib.vh_gemm_last_path() == vh.GEMM_PATH_SPLIT_K
     got = fetch(vh, C, (M, N))
     assert_parity(got, ref, ref64, name="split-k plain")
     C2 = dev(vh, c0)
     d = gemm_desc(vh, M, N, K, DY.ptr, 1, M, X.ptr, N, 1, C2.ptr, N, alpha=0.5, accumulate=1,
-                  e=BI.ptr, e_sm=0, e_sn=1)
+                  e=BI.ptr, e_sm=0, e_sn=1, engine=tiled)
     vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+    assert vh.lib.vh_gemm_last_path() == vh.GEMM_PATH_SPLIT_K
     assert_parity(fetch(vh, C2, (M, N)), c0 + (ref * np.float32(0.5) + bias),
                   c0.astype(np.float64) + (ref64 * 0.5 + bias), name="split-k epilogue")
     # Deterministic: the same call gives the same bits.
     C3 = out(vh, (M, N))
-    d = gemm_desc(vh, M, N, K, DY.ptr, 1, M, X.ptr, N, 1, C3.ptr, N)
+    d = gemm_desc(vh, M, N, K, DY.ptr, 1, M, X.ptr, N, 1, C3.ptr, N, engine=tiled)
     vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
     np.testing.assert_array_equal(fetch(vh, C3, (M, N)), got)
+
+
+# The persistent 256 x 192-tile kernel at the block step's shapes (fewer rows
+# where the full product would keep the oracle busy): every layout pair, tile
+# edges in M and N, a stream-K last round (tiles mod CUs != 0), a ragged K
+# (50260 = 1570 x 32 + 20: the tiled kernel adds the tail), and the Linear
+# epilogues (bias, bias + residual accumulation, alpha). A is N(0,1) times
+# a_scale: lm_head dx's A is dlogits, whose entries are ~1e-4 (softmax over
+# 50257 classes, divided by the row count), so a 50260-term row sum of it
+# stays far from cancellation; the plain cases also meet the f32 error bound
+# of a K-term sum in any order, which holds for any data.
+#   name, M, N, K, A k-contiguous, B k-contiguous, epilogue, a_scale
+PERSISTENT_CASES = [
+    ("lm_head fwd", 1024, 50257, 768, True, True, "", 1.0),
+    ("lm_head dx", 512, 768, 50260, True, False, "", 1e-3),
+    ("lm_head dW", 50260, 768, 512, False, False, "", 1.0),
+    ("qkv fwd + bias", 2048, 2304, 768, True, True, "bias", 1.0),
+    ("fc2 fwd + bias + residual", 2048, 768, 3072, True, True, "bias_acc", 1.0),
+    ("fc1 dW", 3072, 768, 2048, False, False, "", 1.0),
+    ("m-contiguous A, k-contiguous B", 1000, 777, 1536, False, True, "alpha", 1.0),
+    ("edges", 1000, 1001, 2052, True, True, "alpha_acc", 1.0),
+]
+
+
+@pytest.mark.parametrize("case", PERSISTENT_CASES, ids=[c[0] for c in PERSISTENT_CASES])
+def test_gemm_persistent_block_shapes(vh, case):
+    name, M, N, K, akc, bkc, epi, a_scale = case
+    print("persistent", case, flush=True)
+    r = np.random.default_rng(M * 7 + N * 3 + K)
+    a = (r.standard_normal((M, K)) * a_scale).astype(np.float32)
+    b = (r.standard_normal((K, N)) * 0.05).astype(np.float32)
+    # Operands stored as the block step stores them: k-contiguous A is a [M, K]
+    # row-major array; m-contiguous A is stored transposed ([K, M]); likewise B.
+    A = dev(vh, a if akc else np.ascontiguousarray(a.T))
+    B = dev(vh, np.ascontiguousarray(b.T) if bkc else b)
+    a_sm, a_sk = (K, 1) if akc else (1, M)
+    b_sk, b_sn = (1, K) if bkc else (N, 1)
+    ref = O.matmul(a, b)
+    ref64 = a.astype(np.float64) @ b.astype(np.float64)
+    kw = {}
+    c0 = np.zeros((M, N), np.float32)
+    want, want64 = ref, ref64
+    alpha = np.float32(0.75) if "alpha" in epi else np.float32(1.0)
+    if "alpha" in epi:
+        kw["alpha"] = float(alpha)
+        want, want64 = ref * alpha, ref64 * float(alpha)
+    if "bias" in epi:
+        bias = (r.standard_normal(N) * 0.1).astype(np.float32)
+        BI = dev(vh, bias)
+        kw.update(e=BI.ptr, e_sm=0, e_sn=1)
+        want, want64 = want + bias, want64 + bias.astype(np.float64)
+    if "acc" in epi:
+        c0 = r.standard_normal((M, N), dtype=np.float32)
+        kw["accumulate"] = 1
+        want, want64 = c0 + want, c0.astype(np.float64) + want64
+    C = dev(vh, c0)
+    d = gemm_desc(vh, M, N, K, A.ptr, a_sm, a_sk, B.ptr, b_sk, b_sn, C.ptr, N, **kw)
+    vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+    assert vh.lib.vh_gemm_last_path() == vh.GEMM_PATH_PERSISTENT, name
+    got = fetch(vh, C, (M, N))
+    assert_parity(got, want, want64, name=f"persistent {name}")
+    if not epi:
+        u = 2.0 ** -24
+        bound = (K * u / (1 - K * u)) * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
+        assert np.all(np.abs(got - ref64) <= bound), f"persistent {name}: f32 error bound"
+    if not kw.get("accumulate"):
+        # Deterministic (fixed stream-K split and fix-up order): same bits again.
+        C2 = out(vh, (M, N))
+        d = gemm_desc(vh, M, N, K, A.ptr, a_sm, a_sk, B.ptr, b_sk, b_sn, C2.ptr, N, **kw)
+        vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+        np.testing.assert_array_equal(fetch(vh, C2, (M, N)), got)
+
+
+def test_gemm_library_engine_is_an_ab_only(vh):
+    """The LIBRARY engine hands a large dense product to hipBLASLt (when it has
+    an algorithm) and gives the same results to the parity bar; the default
+    engine never does."""
+    M, N, K = 1024, 1536, 768
+    r = np.random.default_rng(5)
+    a = r.standard_normal((M, K), dtype=np.float32)
+    w = (r.standard_normal((N, K)) * 0.05).astype(np.float32)
+    A, W, C = dev(vh, a), dev(vh, w), out(vh, (M, N))
+    ref = O.matmul(a, np.ascontiguousarray(w.T))
+    ref64 = a.astype(np.float64) @ w.T.astype(np.float64)
+    d = gemm_desc(vh, M, N, K, A.ptr, K, 1, W.ptr, 1, K, C.ptr, N)
+    vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+    assert vh.lib.vh_gemm_last_path() == vh.GEMM_PATH_PERSISTENT
+    assert_parity(fetch(vh, C, (M, N)), ref, ref64, name="default engine")
+    d = gemm_desc(vh, M, N, K, A.ptr, K, 1, W.ptr, 1, K, C.ptr, N, engine=vh.GEMM_ENGINE_LIBRARY)
+    vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+    assert vh.lib.vh_gemm_last_path() in (vh.GEMM_PATH_LIBRARY, vh.GEMM_PATH_PERSISTENT)
+    assert_parity(fetch(vh, C, (M, N)), ref, ref64, name="library engine")
 
 
 def test_cross_entropy_row_stride(vh):
@@ -438,14 +536,21 @@ def test_cross_entropy_fwd_bwd_in_place(vh, B, V):
     assert_parity(fetch(vh, LOSS, (1,)), O.cross_entropy(logits, tg), name="loss")
 
 
+ENGINES = [("default", 0), ("library", 2)]
+
+
+@pytest.mark.parametrize("engine", ENGINES, ids=[e[0] for e in ENGINES])
 @pytest.mark.parametrize("akc,bkc", [(True, True), (True, False), (False, False), (False, True)])
-def test_plain_gemm_library_path(vh, akc, bkc):
+def test_plain_gemm_large(vh, akc, bkc, engine):
     """Large plain products (no batch, causal range, addend or accumulation)
-    run through hipBLASLt: the oracle's matmul within the parity bar at model
-    scale, the f32 error bound against float64 with N(0,1) operands, and the
-    same bits from a second call (determinism), for every operand layout."""
+    on the default engine (the persistent kernel) and on the LIBRARY engine
+    (hipBLASLt, the benchmarks' A/B reference): the oracle's matmul within the
+    parity bar at model scale, the f32 error bound against float64 with N(0,1)
+    operands, and the same bits from a second call (determinism), for every
+    operand layout."""
     M, N, K = 1024, 3000, 768
-    print("plain gemm", akc, bkc, flush=True)
+    eng = engine[1]
+    print("plain gemm", akc, bkc, engine[0], flush=True)
     r = np.random.default_rng(int(akc) * 2 + int(bkc))
     a = r.standard_normal((M, K), dtype=np.float32)
     b = (r.standard_normal((K, N)) * 0.02).astype(np.float32)
@@ -457,26 +562,29 @@ def test_plain_gemm_library_path(vh, akc, bkc):
         B = dev(vh, np.ascontiguousarray(bb.T) if bkc else bb)
         b_sk, b_sn = (1, K) if bkc else (N, 1)
         C, C2 = out(vh, (M, N)), out(vh, (M, N))
-        d = gemm_desc(vh, M, N, K, A.ptr, a_sm, a_sk, B.ptr, b_sk, b_sn, C.ptr, N)
+        d = gemm_desc(vh, M, N, K, A.ptr, a_sm, a_sk, B.ptr, b_sk, b_sn, C.ptr, N, engine=eng)
         vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
-        d2 = gemm_desc(vh, M, N, K, A.ptr, a_sm, a_sk, B.ptr, b_sk, b_sn, C2.ptr, N)
+        if eng == vh.GEMM_ENGINE_DEFAULT:
+            assert vh.lib.vh_gemm_last_path() == vh.GEMM_PATH_PERSISTENT
+        d2 = gemm_desc(vh, M, N, K, A.ptr, a_sm, a_sk, B.ptr, b_sk, b_sn, C2.ptr, N, engine=eng)
         vh.check(vh.lib.vh_gemm(ctypes.byref(d2), None))
         got = fetch(vh, C, (M, N))
         np.testing.assert_array_equal(got, fetch(vh, C2, (M, N)))
         exact = a.astype(np.float64) @ bb.astype(np.float64)
         if bb is b:
-            assert_parity(got, O.matmul(a, bb), exact, name=f"plain {akc} {bkc}")
+            assert_parity(got, O.matmul(a, bb), exact, name=f"plain {akc} {bkc} {engine[0]}")
         else:
             u = 2.0 ** -24
             bound = (K * u / (1 - K * u)) * (np.abs(a).astype(np.float64) @ np.abs(bb).astype(np.float64))
             assert np.all(np.abs(got - exact) <= bound), f"plain {akc} {bkc}: f32 error bound"
 
 
+@pytest.mark.parametrize("engine", ENGINES, ids=[e[0] for e in ENGINES])
 @pytest.mark.parametrize("accumulate", [0, 1])
-def test_linear_library_path_bias_and_residual(vh, accumulate):
-    """A Linear forward large enough for the library path: y = x W^T + b, and
-    with accumulation h = h0 + (x W^T + b) (the residual form the block step
-    uses), against the oracle's matmul then add; determinism on a repeat."""
+def test_linear_bias_and_residual(vh, accumulate, engine):
+    """A large Linear forward: y = x W^T + b, and with accumulation
+    h = h0 + (x W^T + b) (the residual form the block step uses), on both
+    engines, against the oracle's matmul then add; determinism on a repeat."""
     M, K, N = 2048, 3072, 768
     r = np.random.default_rng(40 + accumulate)
     x = r.standard_normal((M, K), dtype=np.float32)
@@ -488,7 +596,7 @@ def test_linear_library_path_bias_and_residual(vh, accumulate):
     for _ in range(2):
         C = dev(vh, h0 if accumulate else np.zeros((M, N), np.float32))
         d = gemm_desc(vh, M, N, K, X.ptr, K, 1, W.ptr, 1, K, C.ptr, N, e=BI.ptr, e_sm=0, e_sn=1,
-                      accumulate=accumulate)
+                      accumulate=accumulate, engine=engine[1])
         vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
         outs.append(fetch(vh, C, (M, N)))
     np.testing.assert_array_equal(outs[0], outs[1])
@@ -496,4 +604,4 @@ def test_linear_library_path_bias_and_residual(vh, accumulate):
     lin64 = x.astype(np.float64) @ w.T.astype(np.float64) + bias
     ref = (h0 + lin) if accumulate else lin
     ref64 = (h0.astype(np.float64) + lin64) if accumulate else lin64
-    assert_parity(outs[0], ref, ref64, name=f"linear library path acc={accumulate}")
+    assert_parity(outs[0], ref, ref64, name=f"linear {engine[0]} acc={accumulate}")

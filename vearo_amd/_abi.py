@@ -54,11 +54,13 @@ class VhGemmDesc(ctypes.Structure):
         ("c", c_void_p), ("c_sm", c_int64),
         ("batch", c_int64 * 2), ("a_sb", c_int64 * 2), ("b_sb", c_int64 * 2), ("c_sb", c_int64 * 2),
         ("e", c_void_p), ("e_sm", c_int64), ("e_sn", c_int64), ("e_sb", c_int64 * 2),
-        ("alpha", c_float), ("accumulate", c_int32), ("causal", c_int32),
+        ("alpha", c_float), ("accumulate", c_int32), ("causal", c_int32), ("engine", c_int32),
     ]
 
 
 GEMM_DENSE, GEMM_SKIP_UPPER, GEMM_K_LE_M, GEMM_K_GE_M = 0, 1, 2, 3
+GEMM_ENGINE_DEFAULT, GEMM_ENGINE_TILED, GEMM_ENGINE_LIBRARY = 0, 1, 2
+GEMM_PATH_NONE, GEMM_PATH_TILED, GEMM_PATH_SPLIT_K, GEMM_PATH_PERSISTENT, GEMM_PATH_LIBRARY, GEMM_PATH_BATCHED = range(6)
 
 
 class VhError(RuntimeError):
@@ -82,6 +84,7 @@ SIGNATURES = {
     "vh_shutdown": (c_int, []),
     "vh_last_error": (ctypes.c_char_p, []),
     "vh_stream": (c_void_p, []),
+    "vh_gemm_last_path": (c_int, []),
     "vh_device_cu_count": (c_int, []),
     "vh_sync": (c_int, []),
     "vh_check_device_error": (c_int, []),

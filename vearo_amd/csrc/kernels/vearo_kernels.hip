@@ -9,6 +9,7 @@
 #include "embedding.h"
 #include "gelu.h"
 #include "gemm.h"
+#include "gemm_big.h"
 #include "generic.h"
 #include "layernorm.h"
 #include "optim.h"
@@ -210,6 +211,16 @@ K_GEMMP(false, true, vh_gemmp_m4_k4)
 K_GEMMP(false, false, vh_gemmp_m4_n4)
 
 extern "C" __global__ void __launch_bounds__(256) vh_gemm_reduce(GemmReduceArgs a) { gemm_reduce_impl(a); }
+
+// Large dense products: vh_gemmb_<A><B>_192, persistent 256 x 192 tiles (one
+// workgroup per CU), and the fix-up of its stream-K round.
+#define K_GEMMB(AK, BK, NAME) \
+  extern "C" __global__ void __launch_bounds__(256, 1) NAME(GemmArgs a) { gemm_big_impl<AK, BK, 192>(a); }
+K_GEMMB(true, true, vh_gemmb_kk_192)
+K_GEMMB(true, false, vh_gemmb_kn_192)
+K_GEMMB(false, true, vh_gemmb_mk_192)
+K_GEMMB(false, false, vh_gemmb_mn_192)
+extern "C" __global__ void __launch_bounds__(256) vh_gemmb_fix_192(GemmArgs a) { gemm_big_fix_impl<192>(a); }
 
 // AdamW
 extern "C" __global__ void __launch_bounds__(256) vh_adamw_v1(AdamArgs a) { adamw_impl<1>(a); }

@@ -1247,7 +1247,68 @@ GemmArgs gemm_args(const vh_gemm_desc* d, int64_t lda, int64_t ldb, int64_t tile
 }
 }  // namespace
 
+namespace {
+thread_local int g_gemm_path = VH_GEMM_PATH_NONE;
+
+// The persistent 256 x 192-tile kernel (kernels/gemm_big.h) for a large dense
+// unbatched product, when its conditions hold; *taken reports whether it ran.
+// Conditions: 16-byte aligned operands with leading dimensions % 4 == 0 and
+// 128-bit pieces wholly inside or outside the operand (K % 4 == 0 for a
+// k-contiguous operand, M or N % 4 == 0 for a row-contiguous one); a tile's
+// reads within 2^32 bytes of its origin (leading dimensions < 2^22); k tile
+// and tile counts below 2^31 (K < 2^26). A k-contiguous operand with
+// K % 32 != 0 splits K: the kernel takes the whole 32-wide k tiles and the
+// tiled kernel adds the rest (alpha times the tail product) into C.
+int gemm_big(const vh_gemm_desc* d, bool akc, bool bkc, int64_t lda, int64_t ldb, hipStream_t s, bool* taken) {
+  *taken = false;
+  const int64_t M = d->M, N = d->N, K = d->K;
+  if (d->batch[0] * d->batch[1] != 1 || d->causal != VH_GEMM_DENSE || K <= 0) return VH_OK;
+  if (M < VH_GEMMB_TM || N < VH_GEMMB_TN || (double)M * (double)N * (double)K < 67108864.0) return VH_OK;
+  if (!aligned16(d->a) || !aligned16(d->b) || lda % 4 != 0 || ldb % 4 != 0) return VH_OK;
+  if ((akc ? K : M) % 4 != 0 || (bkc ? K : N) % 4 != 0) return VH_OK;
+  if (lda >= (int64_t(1) << 22) || ldb >= (int64_t(1) << 22) || K >= (int64_t(1) << 26)) return VH_OK;
+  const int G = std::max(8, g_rt.cu_count / 8 * 8);
+  const int64_t K32 = (akc || bkc) ? K / 32 * 32 : K;
+  if (K32 == 0) return VH_OK;
+  const int64_t tiles_m = cdiv(M, VH_GEMMB_TM), tiles_n = cdiv(N, VH_GEMMB_TN);
+  if (tiles_m * tiles_n >= INT32_MAX) return VH_OK;
+  const int64_t tiles = tiles_m * tiles_n, rem = tiles % G;
+  GemmArgs g = gemm_args(d, lda, ldb, tiles_m, tiles_n);
+  g.K = K32;
+  void* ws = nullptr;
+  if (rem > 0) {
+    VH_TRY(g_arena.alloc((size_t)G * VH_GEMMB_SLOTS * VH_GEMMB_TM * VH_GEMMB_TN * sizeof(float), s, &ws));
+    g.ws = static_cast<float*>(ws);
+  }
+  const std::string name = std::string("vh_gemmb_") + (akc ? "k" : "m") + (bkc ? "k" : "n") + "_192";
+  int rc = launch(name, (unsigned)G, 1, 256, 0, s, g);
+  if (rc == VH_OK && rem > 0) {
+    GemmArgs f = g;
+    f.ksplit = G;
+    rc = launch("vh_gemmb_fix_192", (unsigned)(rem * (VH_GEMMB_TM / 16)), 1, 256, 0, s, f);
+  }
+  if (ws) g_arena.free(ws, s);
+  VH_TRY(rc);
+  *taken = true;
+  if (K32 < K) {
+    vh_gemm_desc t = *d;
+    t.K = K - K32;
+    t.a = d->a + K32 * d->a_sk;
+    t.b = d->b + K32 * d->b_sk;
+    t.e = nullptr;
+    t.accumulate = 1;
+    t.engine = VH_GEMM_ENGINE_TILED;
+    VH_TRY(vh_gemm(&t, s));
+  }
+  g_gemm_path = VH_GEMM_PATH_PERSISTENT;
+  return VH_OK;
+}
+}  // namespace
+
+int vh_gemm_last_path(void) { return g_gemm_path; }
+
 int vh_gemm(const vh_gemm_desc* d, void* stream) {
+  g_gemm_path = VH_GEMM_PATH_NONE;
   VH_TRY(require_init());
   if (!d) return fail(VH_ERR_INVALID, "vh_gemm: null descriptor");
   const int64_t M = d->M, N = d->N, K = d->K;
@@ -1272,13 +1333,23 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
     return fail(VH_ERR_UNSUPPORTED, "vh_gemm: B needs a unit stride along k or n");
   const int64_t lda = akc ? (M == 1 ? 0 : d->a_sm) : d->a_sk;
   const int64_t ldb = bkc ? (N == 1 ? 0 : d->b_sn) : d->b_sk;
-  // Large unbatched dense products, with no addend or a bias over the output
-  // columns, go to hipBLASLt (faster on them, measured); the kernel below
-  // covers every product, and runs these when the library has no algorithm.
-  if (d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE && (!d->e || (d->e_sm == 0 && d->e_sn == 1)) &&
-      K > 0 && (double)M * (double)N * (double)K >= 67108864.0) {
+  if (d->engine < VH_GEMM_ENGINE_DEFAULT || d->engine > VH_GEMM_ENGINE_LIBRARY)
+    return fail(VH_ERR_INVALID, "vh_gemm: unknown engine");
+  // LIBRARY: large unbatched dense products, with no addend or a bias over
+  // the output columns, go to hipBLASLt when it has an algorithm (the A/B
+  // reference); everything else as DEFAULT.
+  if (d->engine == VH_GEMM_ENGINE_LIBRARY && d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE &&
+      (!d->e || (d->e_sm == 0 && d->e_sn == 1)) && K > 0 && (double)M * (double)N * (double)K >= 67108864.0) {
     bool taken = false;
     VH_TRY(vh_rt::blaslt_gemm(d, akc, bkc, stream, &taken));
+    if (taken) {
+      g_gemm_path = VH_GEMM_PATH_LIBRARY;
+      return VH_OK;
+    }
+  }
+  if (d->engine != VH_GEMM_ENGINE_TILED) {
+    bool taken = false;
+    VH_TRY(gemm_big(d, akc, bkc, lda, ldb, S(stream), &taken));
     if (taken) return VH_OK;
   }
   const bool avec = K > 0 && gemm_vec_ok(d->a, lda, akc ? K : M, d->a_sb);
@@ -1310,6 +1381,7 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
         rc = launch("vh_gemm_reduce", (unsigned)blocks, 1, 256, 0, s, r);
       }
       g_arena.free(ws, s);
+      if (rc == VH_OK) g_gemm_path = VH_GEMM_PATH_SPLIT_K;
       return rc;
     }
   }
@@ -1327,7 +1399,9 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
     const int64_t slots = 8 * std::max<int64_t>(1, 2 * std::max(g_rt.cu_count, 1) / 8);
     const int64_t grid = std::min<int64_t>(slots, 8 * cdiv(live * nbat, 8));
     const std::string pname = std::string("vh_gemmp_") + (akc ? "k4" : "m4") + "_" + (bkc ? "k4" : "n4");
-    return launch(pname, (unsigned)grid, 1, 256, 0, s, g);
+    VH_TRY(launch(pname, (unsigned)grid, 1, 256, 0, s, g));
+    g_gemm_path = VH_GEMM_PATH_BATCHED;
+    return VH_OK;
   }
   // Grid y covers both batch dims; runs of the outer one keep it under 65535.
   const int64_t outer_chunk = std::max<int64_t>(1, 65535 / d->batch[1]);
@@ -1337,6 +1411,7 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
     const GemmArgs g = gemm_args(d, lda, ldb, tiles_m, tiles_n, b0);
     VH_TRY(launch(name, (unsigned)(tiles_m * tiles_n), (unsigned)(nb * d->batch[1]), 256, 0, s, g));
   }
+  g_gemm_path = VH_GEMM_PATH_TILED;
   return VH_OK;
 }
 

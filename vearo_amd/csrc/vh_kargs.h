@@ -76,6 +76,11 @@ struct SoftmaxArgs {
 // C tile of one GEMM workgroup (host and device agree on the grid).
 #define VH_GEMM_TILE_M 128
 #define VH_GEMM_TILE_N 128
+// The persistent kernel for large dense products (kernels/gemm_big.h): C tile
+// rows x columns, and the workspace slots per workgroup of its stream-K round.
+#define VH_GEMMB_TM 256
+#define VH_GEMMB_TN 192
+#define VH_GEMMB_SLOTS 2
 
 struct GemmArgs {
   const float* A;
