@@ -373,8 +373,8 @@ def wl_gpt2_block(vh):
     ops = [("train_step", flops, lambda i: _block.lib.vb_gpt_train_step(g.h, 0.02, 0.9, 0.95, 1e-8, 0.01))]
     # The dominant kernel, timed on its own after the timed loop: the lm_head
     # forward GEMM logits[16384, 50257] = lnf[16384, 768] W^T, through the same
-    # vh_gemm path the step uses (a plain product: vh_gemm hands it to
-    # hipBLASLt), on scratch buffers of the same shapes.
+    # vh_gemm path the step uses (this library's persistent kernel), on scratch
+    # buffers of the same shapes.
     A = vh.DeviceBuffer.from_array(r.standard_normal((B * S, D), dtype=np.float32))
     W = vh.DeviceBuffer.from_array(params[20])
     C = vh.DeviceBuffer(4 * B * S * V)
@@ -386,6 +386,32 @@ def wl_gpt2_block(vh):
     d.batch[0] = d.batch[1] = 1
     d.alpha = 1.0
     probe = ("lm_head_gemm", 2 * B * S * D * V, lambda i: vh.lib.vh_gemm(ctypes.byref(d), None))
+    # A/B reference: the same step and lm_head product with the dense products
+    # on hipBLASLt (the LIBRARY engine), timed after the headline.
+    dl = vh.VhGemmDesc.from_buffer_copy(d)
+    dl.engine = vh.GEMM_ENGINE_LIBRARY
+
+    def ab(hip, stream, steps):
+        out = {}
+        lp = lm_head_time(vh, hip, stream, lambda i: vh.lib.vh_gemm(ctypes.byref(dl), None), 2 * B * S * D * V)
+        lp["path"] = {vh.GEMM_PATH_LIBRARY: "hipBLASLt"}.get(vh.lib.vh_gemm_last_path(), "fell back to own kernel")
+        out["lm_head_gemm_library"] = lp
+        g.set_gemm_engine(vh.GEMM_ENGINE_LIBRARY)
+        try:
+            step = lambda: vh.check(_block.lib.vb_gpt_train_step(g.h, 0.02, 0.9, 0.95, 1e-8, 0.01))
+            for _ in range(2):
+                step()
+            vh.sync()
+            e0, e1 = hip.event(), hip.event()
+            hip.record(e0, stream)
+            for _ in range(steps):
+                step()
+            hip.record(e1, stream)
+            hip.sync(stream)
+            out["gpt2_block_ms_library"] = round(hip.elapsed_ms(e0, e1) / steps, 3)
+        finally:
+            g.set_gemm_engine(vh.GEMM_ENGINE_DEFAULT)
+        return out
 
     def cpu(budget):
         import oracle
@@ -404,8 +430,8 @@ def wl_gpt2_block(vh):
 
     info = {"workload": "cfg[4] GPT-2-small block training step: B=16, T=1024, C=768, H=12, MLP 3072, "
                         "V=50257, one block; fwd + backward + AdamW",
-            "flops_per_step": flops, "_mode": "step_ms", "_probe": probe}
-    return ops, info, cpu, (g, A, W, C, d), None
+            "flops_per_step": flops, "_mode": "step_ms", "_probe": probe, "_ab": ab}
+    return ops, info, cpu, (g, A, W, C, d, dl), None
 
 
 PEAK_PCIE_GBPS = 64.0  # MI355X host link, PCIe 5.0 x16, one direction
@@ -575,9 +601,7 @@ def summarize_bytes(ops, m, K, traffic_file=None):
             "frac": round(step_bytes / (ms / 1e3) / 1e9 / PEAK_GBPS, 4), "kernels": kernels}
 
 
-def lm_head_probe(vh, hip, stream, info):
-    pname, pflops, pcall = info.pop("_probe")
-    reps = 10
+def lm_head_time(vh, hip, stream, pcall, pflops, reps=10):
     vh.check(pcall(0))
     e0, e1 = hip.event(), hip.event()
     hip.record(e0, stream)
@@ -587,8 +611,16 @@ def lm_head_probe(vh, hip, stream, info):
     hip.sync(stream)
     p_s = hip.elapsed_ms(e0, e1) / reps / 1e3
     achieved = pflops / p_s / 1e12
-    return pname, {"avg_us": round(p_s * 1e6, 1), "flops": pflops, "tflops": round(achieved, 2),
-                   "frac": round(achieved / PEAK_F32_MFMA_TFLOPS, 4)}
+    return {"avg_us": round(p_s * 1e6, 1), "flops": pflops, "tflops": round(achieved, 2),
+            "frac": round(achieved / PEAK_F32_MFMA_TFLOPS, 4)}
+
+
+def lm_head_probe(vh, hip, stream, info):
+    pname, pflops, pcall = info.pop("_probe")
+    res = lm_head_time(vh, hip, stream, pcall, pflops)
+    res["path"] = {vh.GEMM_PATH_PERSISTENT: "own persistent kernel", vh.GEMM_PATH_LIBRARY: "hipBLASLt"}.get(
+        vh.lib.vh_gemm_last_path(), "own tiled kernel")
+    return pname, res
 
 
 def run_one(name, vh, hip, stream, args, cpu_budget):
@@ -599,6 +631,7 @@ def run_one(name, vh, hip, stream, args, cpu_budget):
     if info.get("_mode") == "step_ms":
         info.pop("_mode")
         pname, probe = lm_head_probe(vh, hip, stream, info)
+        ab = info.pop("_ab", None)
         step_s = m["wall"] / K
         flops = info["flops_per_step"]
         res = {"ms_per_step": round(step_s * 1e3, 3), "tflops": round(flops / step_s / 1e12, 2),
@@ -606,6 +639,8 @@ def run_one(name, vh, hip, stream, args, cpu_budget):
                "kernels": {pname: probe}, "config": info,
                "roofline": {"bound": "mfma", "kernel": pname, "achieved": probe["tflops"],
                             "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": probe["frac"], "traffic": None}}
+        if ab is not None:
+            res["ab_library"] = ab(hip, stream, max(3, min(K, 10)))
         if cpu_budget is not None:
             ms, threads, sample = cpu(cpu_budget)
             res["cpu_baseline"] = {"value": round(ms, 1), "unit": "ms per step", "cores": threads, "kind": "port",
@@ -718,6 +753,7 @@ def main():
         res["gpt2_block_ms"] = g["ms_per_step"]
         res["gpt2_block_tflops"] = g["tflops"]
         res["gpt2_block_frac_of_f32_mfma_peak"] = g["frac_of_f32_mfma_peak"]
+        res["gpt2_block_ms_hipblaslt_ab"] = g.get("ab_library", {}).get("gpt2_block_ms_library")
         res["configs"] = configs
     print(json.dumps(res), flush=True)
 

@@ -78,6 +78,12 @@ const char* vb_last_error(void);
 int vb_gpt_save(vb_gpt* g, const char* path);
 int vb_gpt_load(vb_gpt* g, const char* path);
 
+/* The vh_gemm engine (VH_GEMM_ENGINE_*) of the step's dense products (the
+ * Linear layers and lm_head; attention's batched products always run on this
+ * library's kernels): DEFAULT, or LIBRARY for the benchmarks' hipBLASLt A/B.
+ * No counterpart in the reference. */
+int vb_gpt_set_gemm_engine(vb_gpt* g, int engine);
+
 /* The config[4] training step: forward + backward + AdamW. */
 int vb_gpt_train_step(vb_gpt* g, float lr, float beta1, float beta2, float eps, float weight_decay);
 

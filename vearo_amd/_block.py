@@ -45,6 +45,7 @@ def _load():
         "vb_last_error": (ctypes.c_char_p, []),
         "vb_gpt_save": (c_int, [H, ctypes.c_char_p]),
         "vb_gpt_load": (c_int, [H, ctypes.c_char_p]),
+        "vb_gpt_set_gemm_engine": (c_int, [H, c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -104,6 +105,11 @@ class Gpt:
         assert ids.size == self.cfg.B * self.cfg.S and targets.size == ids.size
         _abi.check(_abi.lib.vh_h2d(i.value, ids.ctypes.data, ids.nbytes))
         _abi.check(_abi.lib.vh_h2d(t.value, targets.ctypes.data, targets.nbytes))
+
+    def set_gemm_engine(self, engine: int) -> None:
+        """vh_gemm engine of the dense products: 0 (this library's kernels) or
+        2 (hipBLASLt, an A/B reference)."""
+        check(lib.vb_gpt_set_gemm_engine(self.h, engine))
 
     def forward_backward(self, backward: bool = True) -> None:
         check(lib.vb_gpt_forward_backward(self.h, 1 if backward else 0))

@@ -70,6 +70,7 @@ struct vb_gpt {
   size_t block_floats = 0;
   float *P = nullptr, *G = nullptr, *M = nullptr, *Vm = nullptr;  // params, grads, AdamW m and v
   int t = 0;
+  int engine = VH_GEMM_ENGINE_DEFAULT;  // vh_gemm engine of the dense products
   // forward activations
   float *ids, *tg, *pos, *tok, *pe, *h0, *ln1, *qkv, *att, *h1, *ln2, *y1, *g, *h2, *lnf, *logits;
   float *loss, *one;
@@ -114,6 +115,7 @@ struct vb_gpt {
     d.e_sn = 1;
     d.alpha = 1.0f;
     d.accumulate = accumulate;
+    d.engine = engine;
     VB(vh_gemm(&d, nullptr));
     return VH_OK;
   }
@@ -135,6 +137,7 @@ struct vb_gpt {
     d.batch[0] = d.batch[1] = 1;
     d.alpha = 1.0f;
     d.accumulate = accumulate;
+    d.engine = engine;
     VB(vh_gemm(&d, nullptr));
     return VH_OK;
   }
@@ -156,6 +159,7 @@ struct vb_gpt {
     d.c_sm = Din;
     d.batch[0] = d.batch[1] = 1;
     d.alpha = 1.0f;
+    d.engine = engine;
     VB(vh_gemm(&d, nullptr));
     return VH_OK;
   }
@@ -345,6 +349,14 @@ int vb_gpt_inputs(vb_gpt* g, float** ids, float** targets) {
 }
 
 float* vb_gpt_loss_ptr(vb_gpt* g) { return g ? g->loss : nullptr; }
+
+int vb_gpt_set_gemm_engine(vb_gpt* g, int engine) {
+  if (!g) return vb_fail(VH_ERR_INVALID, "vb_gpt_set_gemm_engine: null handle");
+  if (engine != VH_GEMM_ENGINE_DEFAULT && engine != VH_GEMM_ENGINE_LIBRARY)
+    return vb_fail(VH_ERR_INVALID, "vb_gpt_set_gemm_engine: engine must be DEFAULT or LIBRARY");
+  g->engine = engine;
+  return VH_OK;
+}
 
 int vb_gpt_forward_backward(vb_gpt* g, int backward) {
   if (!g) return vb_fail(VH_ERR_INVALID, "vb_gpt_forward_backward: null handle");
