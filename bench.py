@@ -413,6 +413,36 @@ def wl_gpt2_block(vh):
             g.set_gemm_engine(vh.GEMM_ENGINE_DEFAULT)
         return out
 
+    def dropin(hip, stream, steps):
+        # The same step issued op by op through the BackendOps mirror, in the
+        # reference's own order (forward tape, backward_impl arms, AdamW::step):
+        # what an unchanged vearo program gets. Timed like the headline, then
+        # one step with an event after every op for the per-phase breakdown.
+        d = _block.DropIn(_block.GptConfig(*cfg))
+        try:
+            d.set_params(params)
+            d.set_inputs(ids, tg)
+            step = lambda: d.step(backward=True, adamw=True, want_loss=False)
+            for _ in range(2):
+                step()
+            vh.sync()
+            e0, e1 = hip.event(), hip.event()
+            hip.record(e0, stream)
+            for _ in range(steps):
+                step()
+            hip.record(e1, stream)
+            hip.sync(stream)
+            ms = hip.elapsed_ms(e0, e1) / steps
+            d.step(backward=True, adamw=True, want_loss=False, timing=True)
+            ph = d.phase_ms()
+            loss = d.step(backward=False)
+        finally:
+            d.close()
+        return {"ms_per_step": round(ms, 3), "tflops": round(flops / ms / 1e9, 2), "steps": steps,
+                "loss_after": round(loss, 6),
+                "phases_ms": {k: round(v, 3) for k, v in ph.items()},
+                "phases_sum_ms": round(sum(ph.values()), 3)}
+
     def cpu(budget):
         import oracle
         t0 = time.perf_counter()
@@ -430,7 +460,7 @@ def wl_gpt2_block(vh):
 
     info = {"workload": "cfg[4] GPT-2-small block training step: B=16, T=1024, C=768, H=12, MLP 3072, "
                         "V=50257, one block; fwd + backward + AdamW",
-            "flops_per_step": flops, "_mode": "step_ms", "_probe": probe, "_ab": ab}
+            "flops_per_step": flops, "_mode": "step_ms", "_probe": probe, "_ab": ab, "_dropin": dropin}
     return ops, info, cpu, (g, A, W, C, d, dl), None
 
 
@@ -632,6 +662,7 @@ def run_one(name, vh, hip, stream, args, cpu_budget):
         info.pop("_mode")
         pname, probe = lm_head_probe(vh, hip, stream, info)
         ab = info.pop("_ab", None)
+        dropin = info.pop("_dropin", None)
         step_s = m["wall"] / K
         flops = info["flops_per_step"]
         res = {"ms_per_step": round(step_s * 1e3, 3), "tflops": round(flops / step_s / 1e12, 2),
@@ -641,6 +672,8 @@ def run_one(name, vh, hip, stream, args, cpu_budget):
                             "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": probe["frac"], "traffic": None}}
         if ab is not None:
             res["ab_library"] = ab(hip, stream, max(3, min(K, 10)))
+        if dropin is not None:
+            res["dropin"] = dropin(hip, stream, max(3, min(K, 10)))
         if cpu_budget is not None:
             ms, threads, sample = cpu(cpu_budget)
             res["cpu_baseline"] = {"value": round(ms, 1), "unit": "ms per step", "cores": threads, "kind": "port",
@@ -754,6 +787,7 @@ def main():
         res["gpt2_block_tflops"] = g["tflops"]
         res["gpt2_block_frac_of_f32_mfma_peak"] = g["frac_of_f32_mfma_peak"]
         res["gpt2_block_ms_hipblaslt_ab"] = g.get("ab_library", {}).get("gpt2_block_ms_library")
+        res["gpt2_block_dropin_ms"] = g.get("dropin", {}).get("ms_per_step")
         res["configs"] = configs
     print(json.dumps(res), flush=True)
 

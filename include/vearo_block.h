@@ -87,6 +87,45 @@ int vb_gpt_set_gemm_engine(vb_gpt* g, int engine);
 /* The config[4] training step: forward + backward + AdamW. */
 int vb_gpt_train_step(vb_gpt* g, float lr, float beta1, float beta2, float eps, float weight_decay);
 
+/* ---------------------------------------------------------------------------
+ * The same model and step issued op by op through the HIP BackendOps table
+ * (the C++ mirror of tensor.rs:1108-1196), in the order the reference's own
+ * code issues them: SimpleGPT::forward's Tensor ops recording a tape
+ * (nn:584-621, 666-675, 745-791; autograd lib.rs:150-188), loss.backward()
+ * walking it in reverse through the backward_impl arms (autograd
+ * lib.rs:429-792), then AdamW::step (optim:105-123). This is what an unchanged
+ * vearo program gets from this backend, op for op; vb_gpt above fuses the same
+ * chain. reduce_to, the Gelu arm's mask and adamw_step, host loops in the
+ * reference, run on the device (sum slot, vh_gelu_grad_mul, vh_adamw_step).
+ * Parameters are numbered as for vb_gpt; the model starts like vb_gpt_create's.
+ * Every call is synchronous except vb_dropin_step with loss == NULL and
+ * timing == 0. No counterpart entry point in the reference: the drop-in
+ * step's measurement and parity harness.
+ * ------------------------------------------------------------------------- */
+#define VB_DROPIN_NPHASES 19
+
+typedef struct vb_dropin vb_dropin;
+
+int vb_dropin_create(const vb_gpt_config* cfg, vb_dropin** out);
+void vb_dropin_destroy(vb_dropin* d);
+/* Host copies of parameter i (numel must match) and of its last gradient
+ * (after a step with backward != 0). */
+int vb_dropin_set_param(vb_dropin* d, int i, const float* host, int64_t numel);
+int vb_dropin_get_param(vb_dropin* d, int i, float* host, int64_t numel);
+int vb_dropin_get_grad(vb_dropin* d, int i, float* host, int64_t numel);
+/* Token ids and targets, host [B, S] f32. */
+int vb_dropin_set_inputs(vb_dropin* d, const float* ids, const float* targets);
+/* One forward, with backward != 0 the autograd backward, with adamw != 0 (needs
+ * backward) one AdamW step. timing != 0 records an event after every op and
+ * waits for the step, for vb_dropin_phase_ms. loss != NULL waits and stores
+ * the loss. */
+int vb_dropin_step(vb_dropin* d, int backward, int adamw, float lr, float beta1, float beta2, float eps,
+                   float weight_decay, int timing, float* loss);
+/* Milliseconds per phase of the last timed step (n >= VB_DROPIN_NPHASES), and
+ * the phases' names ("fwd.matmul", "bwd.reduce_to", "adamw.update", ...). */
+int vb_dropin_phase_ms(vb_dropin* d, double* ms, int n);
+const char* vb_dropin_phase_name(int i);
+
 #ifdef __cplusplus
 }
 #endif

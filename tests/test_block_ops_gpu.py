@@ -107,6 +107,25 @@ def test_matmul_batched_broadcast(vh):
     assert_parity(run_matmul(vh, a5, b5), O.matmul(a5, b5), name="rank5")
 
 
+def test_matmul_folds_shared_weight_batches(vh):
+    """A [B, S, K] input times a weight shared by every batch (Linear::forward's
+    input.matmul(weight.transpose(0, 1)), crates/vearo-nn/src/lib.rs:121-122)
+    runs as one product over B*S rows, on the large-product kernel at this
+    size; a left operand whose batches are not evenly spaced rows (its
+    transposed view) stays a batched product. Same results either way."""
+    r = np.random.default_rng(12)
+    a = r.standard_normal((4, 1024, 768), dtype=np.float32)
+    w = (r.standard_normal((2304, 768)) * 0.02).astype(np.float32)
+    ref = O.matmul(a, np.ascontiguousarray(w.T))
+    ref64 = a.astype(np.float64) @ w.T.astype(np.float64)
+    got = run_matmul(vh, a, w.T, b_view="T")
+    assert vh.lib.vh_gemm_last_path() == vh.GEMM_PATH_PERSISTENT
+    assert_parity(got, ref, ref64, name="folded batches")
+    got_t = run_matmul(vh, a, w.T, a_view="T", b_view="T")
+    assert vh.lib.vh_gemm_last_path() in (vh.GEMM_PATH_TILED, vh.GEMM_PATH_BATCHED)
+    assert_parity(got_t, ref, ref64, name="batched")
+
+
 def test_matmul_zero_k_and_errors(vh):
     a = np.zeros((3, 0), np.float32)
     b = np.zeros((0, 4), np.float32)

@@ -1,7 +1,8 @@
 """Config[4] at its real size (B=16, T=1024, C=768, H=12, MLP 3072, V=50257):
 the device step against the CPU oracle's SimpleGPT step on identical inputs --
-the step-0 loss, every parameter gradient, and the loss after one AdamW step
-(north_star: "the full config[4] block step runs end to end with loss matching
+the step-0 loss, every parameter gradient, and the loss after one AdamW step,
+for the fused driver (vb_gpt) and for the same step issued op by op through the
+BackendOps mirror (vb_dropin) (north_star: "the full config[4] block step runs end to end with loss matching
 the CPU backend"; loss within 1e-4 relative).
 
 The oracle needs about 6 TFLOP here; it runs threaded (its results do not
@@ -63,9 +64,26 @@ def test_block_step_full_size_matches_oracle(vh):
         assert err <= 1e-4 * scale, (name, err, scale)
         # Elementwise, the north-star bar |gpu - cpu| <= 1e-5 + 1e-4 |cpu| on every element.
         assert_parity(grads[i], ograds[i], name=f"full-size block-step grad {name}")
+    # The same step issued op by op through the BackendOps mirror (vb_dropin),
+    # the reference's own op order: loss, gradients, then AdamW.
+    d = _block.DropIn(_block.GptConfig(*CFG))
+    d.set_params(params)
+    d.set_inputs(ids, tg)
+    dloss0 = d.step(backward=True, adamw=True, lr=ADAM[0], beta1=ADAM[1], beta2=ADAM[2], eps=ADAM[3], wd=ADAM[4])
+    print(f"drop-in: loss0 {dloss0:.7f}", flush=True)
+    assert abs(dloss0 - oloss0) <= 1e-4 * abs(oloss0), (dloss0, oloss0)
+    for i, dg in enumerate(d.grads()):
+        if O.GPT_PARAM_NAMES[i] == "k_b":
+            assert np.abs(dg).max() < 1e-6
+            continue
+        assert_parity(dg, ograds[i], name=f"full-size drop-in grad {O.GPT_PARAM_NAMES[i]}")
+    dloss1 = d.step(backward=False)
+    d.close()
+    print(f"drop-in: loss1 {dloss1:.7f}", flush=True)
     for p, gr in zip(params, ograds):
         O.adamw_step(p, gr, np.zeros_like(p), np.zeros_like(p), 1, *ADAM)
     t0 = time.perf_counter()
     oloss1, _ = O.gpt_step(O.GptConfig(*CFG), params, ids, tg, grads=False)
     print(f"oracle forward after AdamW {time.perf_counter() - t0:.1f} s: loss1 {oloss1:.7f}", flush=True)
     assert abs(loss1 - oloss1) <= 1e-4 * abs(oloss1), (loss1, oloss1)
+    assert abs(dloss1 - oloss1) <= 1e-4 * abs(oloss1), (dloss1, oloss1)

@@ -1,0 +1,158 @@
+"""The config[4] step issued op by op through the BackendOps mirror
+(vb_dropin_*, include/vearo_block.h): the tape SimpleGPT::forward records
+(crates/vearo-nn/src/lib.rs:584-621, 666-675, 745-791), walked in reverse
+through backward_impl's arms (crates/vearo-autograd/src/lib.rs:429-792), then
+AdamW::step (crates/vearo-optim/src/lib.rs:105-123). Against the oracle's
+SimpleGPT step and the golden float64 torch model: the loss, every parameter
+gradient and the loss after one AdamW step; against the fused vb_gpt driver on
+the same model; and the reference's GPT overfitting run
+(crates/vearo/tests/verification_harness.rs:184-237) through the drop-in path.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from parity import assert_parity
+from test_block_step_gpu import check_grads, random_model
+
+pytestmark = pytest.mark.gpu
+GOLD = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden.npz"))
+
+
+def dropin(cfg_tuple):
+    from vearo_amd import _block
+    return _block.DropIn(_block.GptConfig(*cfg_tuple))
+
+
+def adam_ref(params, grads, t=1, ms=None, vs=None):
+    ps = [p.copy() for p in params]
+    ms = ms or [np.zeros_like(p) for p in ps]
+    vs = vs or [np.zeros_like(p) for p in ps]
+    for p, gr, m, v in zip(ps, grads, ms, vs):
+        O.adamw_step(p, gr, m, v, t, 0.02, 0.9, 0.95, 1e-8, 0.01)
+    return ps
+
+
+def test_dropin_golden_model(vh):
+    cfg = tuple(int(x) for x in GOLD["gpt_cfg"])
+    d = dropin(cfg)
+    params = [GOLD[f"gpt_p{i}"] for i in range(21)]
+    ids, tg = GOLD["gpt_ids"], GOLD["gpt_targets"]
+    d.set_params(params)
+    d.set_inputs(ids, tg)
+    loss = d.step(backward=True)
+    oloss, ograds = O.gpt_step(O.GptConfig(*cfg), params, ids, tg)
+    assert abs(loss - oloss) <= 1e-5 + 1e-4 * abs(oloss), (loss, oloss)
+    assert abs(loss - GOLD["gpt_loss"]) <= 1e-4 * GOLD["gpt_loss"]
+    check_grads(d.grads(), ograds, [GOLD[f"gpt_g{i}"] for i in range(21)], "dropin golden")
+    # Forward + backward + AdamW in one call, then the step-1 loss.
+    d.set_params(params)
+    d.step(backward=True, adamw=True)
+    loss1 = d.step(backward=False)
+    assert abs(loss1 - GOLD["gpt_loss1"]) <= 1e-4 * GOLD["gpt_loss1"], (loss1, GOLD["gpt_loss1"])
+    ps = adam_ref(params, ograds)
+    oloss1, _ = O.gpt_step(O.GptConfig(*cfg), ps, ids, tg, grads=False)
+    assert abs(loss1 - oloss1) <= 1e-5 + 1e-4 * abs(oloss1), (loss1, oloss1)
+    assert_parity(d.params()[20], ps[20], name="dropin lm_w after AdamW")
+    d.close()
+
+
+def test_dropin_medium_model_matches_oracle_and_fused_driver(vh):
+    from vearo_amd import _block
+    cfg = (2, 128, 128, 4, 512, 1000, 128)
+    print("dropin medium", flush=True)
+    params, ids, tg = random_model(cfg, 11)
+    d = dropin(cfg)
+    d.set_params(params)
+    d.set_inputs(ids, tg)
+    loss = d.step(backward=True, timing=True)
+    ph = d.phase_ms()
+    assert len(ph) == 19 and all(v >= 0 for v in ph.values()) and ph["fwd.matmul"] > 0
+    assert ph["bwd.reduce_to"] > 0 and ph["bwd.grad_accumulate"] > 0, ph
+    grads = d.grads()
+    oloss, ograds = O.gpt_step(O.GptConfig(*cfg), params, ids, tg)
+    assert abs(loss - oloss) <= 1e-5 + 1e-4 * abs(oloss), (loss, oloss)
+    check_grads(grads, ograds, tag="dropin medium")
+    # The fused driver on the same model: same loss and gradients to the same bar.
+    g = _block.Gpt(_block.GptConfig(*cfg))
+    g.set_params(params)
+    g.set_inputs(ids, tg)
+    g.forward_backward(True)
+    assert abs(g.loss() - loss) <= 1e-5 + 1e-4 * abs(oloss)
+    for i, (a, b) in enumerate(zip(g.grads(), grads)):
+        if O.GPT_PARAM_NAMES[i] != "k_b":
+            assert_parity(b, a, ograds[i].astype(np.float64), name=f"dropin vs fused {O.GPT_PARAM_NAMES[i]}")
+    g.close()
+    # Two AdamW steps against the oracle's.
+    ms = [np.zeros_like(p) for p in params]
+    vs = [np.zeros_like(p) for p in params]
+    ps = [p.copy() for p in params]
+    for t in (1, 2):
+        d.step(backward=True, adamw=True, want_loss=False)
+        _, og = O.gpt_step(O.GptConfig(*cfg), ps, ids, tg)
+        for p, gr, m, v in zip(ps, og, ms, vs):
+            O.adamw_step(p, gr, m, v, t, 0.02, 0.9, 0.95, 1e-8, 0.01)
+    loss2 = d.step(backward=False)
+    oloss2, _ = O.gpt_step(O.GptConfig(*cfg), ps, ids, tg, grads=False)
+    assert abs(loss2 - oloss2) <= 1e-5 + 1e-4 * abs(oloss2), (loss2, oloss2)
+    d.close()
+
+
+def test_dropin_errors(vh):
+    from vearo_amd import _block
+    cfg = (1, 4, 8, 2, 16, 8, 4)
+    d = dropin(cfg)
+    with pytest.raises(vh.VhError, match="no gradient"):
+        d.grads()
+    with pytest.raises(vh.VhError, match="AdamW needs"):
+        d.step(backward=False, adamw=True)
+    with pytest.raises(vh.VhError, match="element count"):
+        _block.check(_block.lib.vb_dropin_set_param(d.h, 0, np.zeros(3, np.float32).ctypes.data, 3))
+    # A target outside the vocabulary: the cross-entropy slot's panic (cpu:1000-1006).
+    d.set_inputs(np.zeros((1, 4), np.float32), np.full((1, 4), 9.0, np.float32))
+    with pytest.raises(vh.VhError, match="Target class 9 out of vocab bounds 8"):
+        d.step(backward=False)
+    vh.sync()  # the panic was reported once and cleared
+    d.close()
+    with pytest.raises(vh.VhError, match="divisible"):
+        dropin((1, 4, 9, 2, 16, 8, 4))
+
+
+def test_dropin_overfits_like_the_reference_test(vh):
+    """verification_harness.rs:184-237 through the drop-in path, which issues
+    the reference's own op sequence: 150 AdamW steps bring the loss under 0.05,
+    and the first ten losses follow the oracle's."""
+    cfg = (2, 4, 8, 2, 16, 8, 4)
+    ocfg = O.GptConfig(*cfg)
+    r = np.random.default_rng(42)
+    params = []
+    for name, sh in zip(O.GPT_PARAM_NAMES, O.gpt_param_shapes(ocfg)):
+        if name.startswith("ln") and name.endswith("_w"):
+            params.append(np.ones(sh, np.float32))
+        elif name.startswith("ln"):
+            params.append(np.zeros(sh, np.float32))
+        else:
+            fan = sh[1] if len(sh) == 2 else (cfg[2] if name != "fc2_b" else cfg[4])
+            bound = 1.0 / math.sqrt(fan)
+            params.append(r.uniform(-bound, bound, size=sh).astype(np.float32))
+    ids = np.array([[0, 1, 2, 3], [1, 2, 3, 0]], np.float32)
+    tg = np.array([[1, 2, 3, 0], [2, 3, 0, 1]], np.float32)
+    d = dropin(cfg)
+    d.set_params(params)
+    d.set_inputs(ids, tg)
+    ps = [p.copy() for p in params]
+    ms = [np.zeros_like(p) for p in ps]
+    vs = [np.zeros_like(p) for p in ps]
+    for t in range(1, 151):
+        loss = d.step(backward=True, adamw=True)
+        if t <= 10:
+            oloss, ograds = O.gpt_step(ocfg, ps, ids, tg)
+            for p, gr, m, v in zip(ps, ograds, ms, vs):
+                O.adamw_step(p, gr, m, v, t, 0.02, 0.9, 0.95, 1e-8, 0.01)
+            assert abs(loss - oloss) <= 1e-4 * max(1.0, abs(oloss)), (t, loss, oloss)
+    loss = d.step(backward=False)
+    assert loss < 0.05, loss
+    d.close()

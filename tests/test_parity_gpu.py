@@ -350,6 +350,15 @@ def test_reduce_and_strided_copy(vh):
             vh.check(vh.lib.vh_reduce(mean, X.ptr, vh.layout(x.shape), dim, OUT.ptr, None))
             assert_parity(fetch(vh, OUT, shape), O.reduce(x, dim, mean=bool(mean)),
                           x.astype(np.float64).mean(dim) if mean else x.astype(np.float64).sum(dim))
+    # Column sums of a tall matrix (a bias gradient's reduce_to): the two-pass
+    # row-group path, and the same sum with a leading 1 dim.
+    y = r.normal(size=(3000, 70)).astype(np.float32)
+    Y = dev(vh, y)
+    for lay in ((3000, 70), (1, 3000, 70)):
+        OUT = out(vh, (70,))
+        dim = len(lay) - 2
+        vh.check(vh.lib.vh_reduce(0, Y.ptr, vh.layout(lay), dim, OUT.ptr, None))
+        assert_parity(fetch(vh, OUT, (70,)), O.reduce(y, 0), y.astype(np.float64).sum(0), name=f"col sum {lay}")
     # A transposed view [300, 6, 4] of the same buffer.
     dims, strides = (300, 6, 4), (1, 300, 1800)
     xt = np.transpose(x, (2, 1, 0))

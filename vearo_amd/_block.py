@@ -46,6 +46,16 @@ def _load():
         "vb_gpt_save": (c_int, [H, ctypes.c_char_p]),
         "vb_gpt_load": (c_int, [H, ctypes.c_char_p]),
         "vb_gpt_set_gemm_engine": (c_int, [H, c_int]),
+        "vb_dropin_create": (c_int, [POINTER(GptConfig), POINTER(c_void_p)]),
+        "vb_dropin_destroy": (None, [H]),
+        "vb_dropin_set_param": (c_int, [H, c_int, c_void_p, c_int64]),
+        "vb_dropin_get_param": (c_int, [H, c_int, c_void_p, c_int64]),
+        "vb_dropin_get_grad": (c_int, [H, c_int, c_void_p, c_int64]),
+        "vb_dropin_set_inputs": (c_int, [H, c_void_p, c_void_p]),
+        "vb_dropin_step": (c_int, [H, c_int, c_int, c_float, c_float, c_float, c_float, c_float, c_int,
+                                   POINTER(c_float)]),
+        "vb_dropin_phase_ms": (c_int, [H, POINTER(ctypes.c_double), c_int]),
+        "vb_dropin_phase_name": (ctypes.c_char_p, [c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -137,6 +147,71 @@ class Gpt:
     def close(self) -> None:
         if self.h is not None:
             lib.vb_gpt_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+DROPIN_NPHASES = 19
+
+
+class DropIn:
+    """The same model and step issued op by op through the HIP BackendOps
+    table in the reference's own order (SimpleGPT::forward's tape, then
+    backward_impl's arms, then AdamW::step): include/vearo_block.h vb_dropin_*."""
+
+    def __init__(self, cfg: GptConfig):
+        self.cfg = cfg
+        h = c_void_p()
+        check(lib.vb_dropin_create(ctypes.byref(cfg), ctypes.byref(h)))
+        self.h = h
+        self.shapes = param_shapes(cfg)
+
+    def set_params(self, params) -> None:
+        for i, a in enumerate(params):
+            a = np.ascontiguousarray(a, np.float32)
+            assert a.shape == self.shapes[i], (i, a.shape, self.shapes[i])
+            check(lib.vb_dropin_set_param(self.h, i, a.ctypes.data, a.size))
+
+    def _get(self, fn, i):
+        out = np.empty(self.shapes[i], np.float32)
+        check(fn(self.h, i, out.ctypes.data, out.size))
+        return out
+
+    def params(self):
+        return [self._get(lib.vb_dropin_get_param, i) for i in range(NPARAMS)]
+
+    def grads(self):
+        return [self._get(lib.vb_dropin_get_grad, i) for i in range(NPARAMS)]
+
+    def set_inputs(self, ids, targets) -> None:
+        ids = np.ascontiguousarray(ids, np.float32).reshape(-1)
+        targets = np.ascontiguousarray(targets, np.float32).reshape(-1)
+        assert ids.size == self.cfg.B * self.cfg.S and targets.size == ids.size
+        check(lib.vb_dropin_set_inputs(self.h, ids.ctypes.data, targets.ctypes.data))
+
+    def step(self, backward=True, adamw=False, lr=0.02, beta1=0.9, beta2=0.95, eps=1e-8, wd=0.01,
+             timing=False, want_loss=True):
+        """One step; returns the loss (or None with want_loss=False, which
+        leaves the step queued)."""
+        loss = c_float()
+        check(lib.vb_dropin_step(self.h, int(backward), int(adamw), lr, beta1, beta2, eps, wd, int(timing),
+                                 ctypes.byref(loss) if want_loss else None))
+        return float(loss.value) if want_loss else None
+
+    def phase_ms(self) -> dict:
+        """Per-phase milliseconds of the last step run with timing=True."""
+        ms = (ctypes.c_double * DROPIN_NPHASES)()
+        check(lib.vb_dropin_phase_ms(self.h, ms, DROPIN_NPHASES))
+        return {lib.vb_dropin_phase_name(i).decode(): ms[i] for i in range(DROPIN_NPHASES)}
+
+    def close(self) -> None:
+        if self.h is not None:
+            lib.vb_dropin_destroy(self.h)
             self.h = None
 
     def __del__(self):

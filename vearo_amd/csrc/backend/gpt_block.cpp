@@ -30,15 +30,18 @@
 
 #include "../../../include/vearo_block.h"
 #include "../../../include/vearo_hip.h"
+#include "vb_internal.h"
 
 namespace {
-
 thread_local std::string g_err;
+}  // namespace
 
 int vb_fail(int code, const std::string& msg) {
   g_err = msg;
   return code;
 }
+
+namespace {
 
 #define VB(expr)                                                  \
   do {                                                            \

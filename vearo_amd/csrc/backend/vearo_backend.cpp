@@ -332,11 +332,14 @@ Tensor layernorm(const Tensor& x, const Tensor& w, const Tensor& b, float eps) {
 
 std::tuple<Tensor, Tensor, Tensor> layernorm_backward(const Tensor& x, const Tensor& w, const Tensor& b,
                                                       const Tensor& g, float eps) {
-  Tensor gx = Tensor::zeros(x.shape(), x.device());
-  Tensor gw = Tensor::zeros(w.shape(), w.device());
-  Tensor gb = Tensor::zeros(b.shape(), b.device());
-  if (x.shape().numel() == 0) return {gx, gw, gb};
+  if (x.shape().numel() == 0)
+    return {Tensor::zeros(x.shape(), x.device()), Tensor::zeros(w.shape(), w.device()),
+            Tensor::zeros(b.shape(), b.device())};
   ln_checks(x, w, b);
+  // vh_layernorm_bwd writes every element of the three gradients.
+  Tensor gx = Tensor::empty(x.shape(), x.device());
+  Tensor gw = Tensor::empty(w.shape(), w.device());
+  Tensor gb = Tensor::empty(b.shape(), b.device());
   const int64_t C = x.shape()[x.shape().rank - 1];
   const Tensor xc = x.contiguous(), wc = w.contiguous(), gc = g.contiguous();
   check(vh_layernorm_bwd(xc.data(), wc.data(), gc.data(), gx.data(), gw.data(), gb.data(),
@@ -416,8 +419,11 @@ Tensor matmul(const Tensor& l, const Tensor& r) {
   }
   od.push_back(M);
   od.push_back(N);
-  Tensor out = Tensor::zeros(Shape(od), l.device());
-  if (out.shape().numel() == 0) return out;
+  // vh_matmul writes every output element (K == 0 gives zeros); an empty
+  // product returns the zeros tensor the reference returns.
+  const Shape os(od);
+  if (os.numel() == 0) return Tensor::zeros(os, l.device());
+  Tensor out = Tensor::empty(os, l.device());
   const vh_layout ll = layout_of(l), rl = layout_of(r);
   check(vh_matmul(l.data(), &ll, r.data(), &rl, out.data(), nullptr));
   return out;
@@ -465,8 +471,8 @@ static void attention_checks(const Tensor& q, const Tensor& k, const Tensor& v) 
 Tensor fused_attention(const Tensor& q0, const Tensor& k0, const Tensor& v0, const Tensor* mask) {
   attention_checks(q0, k0, v0);
   const Tensor q = unit_last(q0), k = unit_last(k0), v = unit_last(v0);
-  Tensor out = Tensor::zeros(q.shape(), q.device());
-  if (q.shape().numel() == 0) return out;
+  if (q.shape().numel() == 0) return Tensor::zeros(q.shape(), q.device());
+  Tensor out = Tensor::empty(q.shape(), q.device());  // the P v product writes all of it
   const vh_layout ql = layout_of(q), kl = layout_of(k), vl = layout_of(v), ol = layout_of(out);
   vh_layout ml{};
   if (mask) ml = layout_of(*mask);
@@ -482,9 +488,12 @@ std::tuple<Tensor, Tensor, Tensor> fused_attention_backward(const Tensor& q0, co
   attention_checks(q0, k0, v0);
   panic_if(g0.shape() != q0.shape(), "grad_out must have the attention output's shape");
   const Tensor q = unit_last(q0), k = unit_last(k0), v = unit_last(v0), g = unit_last(g0);
-  Tensor dq = Tensor::zeros(q.shape(), q.device()), dk = Tensor::zeros(q.shape(), q.device()),
-         dv = Tensor::zeros(q.shape(), q.device());
-  if (q.shape().numel() == 0) return {dq, dk, dv};
+  if (q.shape().numel() == 0)
+    return {Tensor::zeros(q.shape(), q.device()), Tensor::zeros(q.shape(), q.device()),
+            Tensor::zeros(q.shape(), q.device())};
+  // Each gradient is one product that writes all of it.
+  Tensor dq = Tensor::empty(q.shape(), q.device()), dk = Tensor::empty(q.shape(), q.device()),
+         dv = Tensor::empty(q.shape(), q.device());
   const vh_layout ql = layout_of(q), kl = layout_of(k), vl = layout_of(v), gl = layout_of(g),
                   dl = layout_of(dq);
   vh_layout ml{};

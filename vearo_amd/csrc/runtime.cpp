@@ -1101,6 +1101,14 @@ int vh_reduce(int mean, const float* x, const vh_layout* xl, int dim, float* out
   if (!x || !out) return fail(VH_ERR_INVALID, "vh_reduce: null pointer");
   const int64_t red_len = xl->dims[dim];
   const int64_t red_stride = xl->strides[dim];
+  // A sum over the outermost dim of a contiguous tensor is the column sum of a
+  // [red_len, n_out] matrix (a bias gradient's reduce_to): two passes over row
+  // groups instead of one thread walking each column.
+  if (!mean && red_len >= 64 && is_contig(xl) && n_out <= INT32_MAX) {
+    bool outer = true;
+    for (int i = 0; i < dim; ++i) outer = outer && xl->dims[i] == 1;
+    if (outer) return vh_sum_rows(x, red_len, n_out, out, nullptr, 0, stream);
+  }
   ReduceArgs a{x, out, ol, n_out, red_len, red_stride, mean ? 1 : 0};
   hipStream_t s = S(stream);
   if ((red_stride == 1 || red_len == 1) && red_len >= 128)
@@ -1486,7 +1494,34 @@ int vh_matmul(const float* lhs, const vh_layout* ll, const float* rhs, const vh_
     cs[i] = acc;
     acc *= odims[i];
   }
+  // A right operand shared by every batch (a Linear weight applied to [B, S, K]
+  // input) whose left batches are evenly spaced rows folds into one product of
+  // batch * M rows: the same multiply-adds in the same order per element, one
+  // launch of the large-product kernel instead of a batched one.
+  bool fold = ob > 0;
+  int64_t rows = M;
+  for (int i = ob - 1; i >= 0 && fold; --i) {
+    if (odims[i] == 1) continue;
+    fold = bs[i] == 0 && as[i] == rows * al.strides[lr - 2];
+    rows *= odims[i];
+  }
   vh_gemm_desc d{};
+  if (fold) {
+    d.M = rows;
+    d.N = N;
+    d.K = K;
+    d.a = A;
+    d.a_sm = al.strides[lr - 2];
+    d.a_sk = al.strides[lr - 1];
+    d.b = B;
+    d.b_sk = bl.strides[rr - 2];
+    d.b_sn = bl.strides[rr - 1];
+    d.c = out;
+    d.c_sm = N;
+    d.alpha = 1.0f;
+    d.batch[0] = d.batch[1] = 1;
+    return vh_gemm(&d, stream);
+  }
   d.M = M;
   d.N = N;
   d.K = K;
