@@ -435,20 +435,33 @@ PERSISTENT_CASES = [
     ("fc1 dW", 3072, 768, 2048, False, False, "", 1.0),
     ("m-contiguous A, k-contiguous B", 1000, 777, 1536, False, True, "alpha", 1.0),
     ("edges", 1000, 1001, 2052, True, True, "alpha_acc", 1.0),
+    # Operands only 4-byte aligned (32-bit loads): the drop-in step's logits
+    # gradient has rows of V = 50257 floats; bases one float off 16 bytes.
+    ("lm_head dx, odd V", 512, 768, 50257, True, False, "", 1e-3, 0),
+    ("lm_head dW^T, odd V", 768, 50257, 512, False, False, "", 1.0, 0),
+    ("m-contiguous A, odd M", 1001, 777, 1536, False, True, "", 1.0, 0),
+    ("edges, bases one float off", 1000, 1001, 2052, True, True, "alpha_acc", 1.0, 1),
 ]
 
 
 @pytest.mark.parametrize("case", PERSISTENT_CASES, ids=[c[0] for c in PERSISTENT_CASES])
 def test_gemm_persistent_block_shapes(vh, case):
-    name, M, N, K, akc, bkc, epi, a_scale = case
+    name, M, N, K, akc, bkc, epi, a_scale = case[:8]
+    off = case[8] if len(case) > 8 else 0  # floats before each operand's first element
     print("persistent", case, flush=True)
     r = np.random.default_rng(M * 7 + N * 3 + K)
     a = (r.standard_normal((M, K)) * a_scale).astype(np.float32)
     b = (r.standard_normal((K, N)) * 0.05).astype(np.float32)
     # Operands stored as the block step stores them: k-contiguous A is a [M, K]
     # row-major array; m-contiguous A is stored transposed ([K, M]); likewise B.
-    A = dev(vh, a if akc else np.ascontiguousarray(a.T))
-    B = dev(vh, np.ascontiguousarray(b.T) if bkc else b)
+    pad = np.zeros(off, np.float32)
+    Abuf = dev(vh, np.concatenate([pad, (a if akc else a.T).reshape(-1)]))
+    Bbuf = dev(vh, np.concatenate([pad, (b.T if bkc else b).reshape(-1)]))
+
+    class _At:  # device address `off` floats into the buffer
+        def __init__(self, buf):
+            self.ptr = buf.ptr + 4 * off
+    A, B = _At(Abuf), _At(Bbuf)
     a_sm, a_sk = (K, 1) if akc else (1, M)
     b_sk, b_sn = (1, K) if bkc else (N, 1)
     ref = O.matmul(a, b)

@@ -48,6 +48,8 @@
 //   row-contiguous: [k][row], padded to NR + 8 floats so the two lane halves'
 //     32-bit fragment reads (4 k apart) sit 32 banks apart.
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 #include "gemm.h"
 
@@ -131,7 +133,12 @@ struct GbSeg {
 };
 #define GB_SLOTS VH_GEMMB_SLOTS  // workspace slots per workgroup: stream-K first / last piece
 
-template <bool A_KC, bool B_KC, int BN>
+// A_U / B_U: the operand is only 4-byte aligned (a leading dimension or base
+// not a multiple of 16 bytes, or a row-contiguous extent not a multiple of 4):
+// its pieces load as four 32-bit reads, each bounds-checked on its own, so a
+// piece that straddles a row end or the operand's end reads exactly what lies
+// in range.
+template <bool A_KC, bool B_KC, int BN, bool A_U = false, bool B_U = false>
 VH_DEV void gemm_big_impl(const GemmArgs& a) {
   static_assert(BN == 256 || BN == 192, "tile width");
   constexpr int NB = BN / 64;  // 32-wide n tiles per wave
@@ -208,13 +215,23 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
   };
   // Staging registers: one k tile's pieces of A and B.
   vh_f4 ga[OA::PER], gb[OB::PER];
+  auto piece = [](__amdgpu_buffer_rsrc_t r, uint32_t off, auto unaligned) -> vh_f4 {
+    if constexpr (decltype(unaligned)::value) {
+      vh_f4 v;
+      v.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+      v.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 4, 0, 0));
+      v.z = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 8, 0, 0));
+      v.w = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 12, 0, 0));
+      return v;
+    } else {
+      return __builtin_bit_cast(vh_f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    }
+  };
   auto gload = [&](__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb) {
 #pragma unroll
-    for (int i = 0; i < OA::PER; ++i)
-      ga[i] = __builtin_bit_cast(vh_f4, __builtin_amdgcn_raw_buffer_load_b128(ra, goa[i], 0, 0));
+    for (int i = 0; i < OA::PER; ++i) ga[i] = piece(ra, goa[i], std::integral_constant<bool, A_U>{});
 #pragma unroll
-    for (int i = 0; i < OB::PER; ++i)
-      gb[i] = __builtin_bit_cast(vh_f4, __builtin_amdgcn_raw_buffer_load_b128(rb, gob[i], 0, 0));
+    for (int i = 0; i < OB::PER; ++i) gb[i] = piece(rb, gob[i], std::integral_constant<bool, B_U>{});
   };
   auto swrite = [&](float* SA, float* SB) {
 #pragma unroll
@@ -308,10 +325,14 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
   //   B: after the barrier, quarter 0 of the other stage is read during the
   //      second half of quarter 3, so the next step starts on fragments
   //      already in registers.
-  constexpr int VM = OA::PER + OB::PER;                  // loads (and LDS writes) per step
+  constexpr int VM = OA::PER + OB::PER;                  // LDS writes per step
+  constexpr int VL = (A_U ? 4 : 1) * OA::PER + (B_U ? 4 : 1) * OB::PER;  // load instructions
+  constexpr int LPM = (A_U || B_U) ? 2 : 1;              // loads placed per product
+  static_assert(VL % LPM == 0, "loads pair up");
+  constexpr int SP = VM + VL / LPM;                      // quarter-0 products that carry the staging
   constexpr int MQ = 16 * NB;                            // products per quarter
   constexpr int RA = A_KC ? 1 : 4, RB = B_KC ? 1 : 4;    // LDS read instructions per fragment
-  static_assert(2 * VM <= MQ, "staging fits in quarter 0");
+  static_assert(SP <= MQ, "staging fits in quarter 0");
   auto kstep = [&](__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, const float* SA, const float* SB,
                    float* NA, float* NBp) {
     swrite(NA, NBp);
@@ -329,27 +350,27 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
       __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
     }
 #pragma unroll
-    for (int i = 0; i < VM; ++i) {
+    for (int i = 0; i < VL / LPM; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, LPM, 0);
     }
     // Quarter 0: after the staging, quarter 1's reads over the products
     // left; quarters 1-2: the next quarter's reads one per RP products from
     // the start, so the last arrives well before the quarter ends.
     constexpr int RP = (MQ / 2) / NF;
-    __builtin_amdgcn_sched_group_barrier(0x008, (MQ - 2 * VM) % NF, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, (MQ - SP) % NF, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, RB, 0);
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
-      __builtin_amdgcn_sched_group_barrier(0x008, (MQ - 2 * VM) / NF, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, (MQ - SP) / NF, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);
     }
 #pragma unroll
     for (int f = 5; f < NF; ++f) {
-      __builtin_amdgcn_sched_group_barrier(0x008, (MQ - 2 * VM) / NF, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, (MQ - SP) / NF, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, RB, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, (MQ - 2 * VM) / NF, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, (MQ - SP) / NF, 0);
 #pragma unroll
     for (int q = 1; q < 3; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, RP, 0);

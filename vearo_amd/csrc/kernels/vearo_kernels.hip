@@ -213,13 +213,19 @@ K_GEMMP(false, false, vh_gemmp_m4_n4)
 extern "C" __global__ void __launch_bounds__(256) vh_gemm_reduce(GemmReduceArgs a) { gemm_reduce_impl(a); }
 
 // Large dense products: vh_gemmb_<A><B>_192, persistent 256 x 192 tiles (one
-// workgroup per CU), and the fix-up of its stream-K round.
-#define K_GEMMB(AK, BK, NAME) \
-  extern "C" __global__ void __launch_bounds__(256, 1) NAME(GemmArgs a) { gemm_big_impl<AK, BK, 192>(a); }
-K_GEMMB(true, true, vh_gemmb_kk_192)
-K_GEMMB(true, false, vh_gemmb_kn_192)
-K_GEMMB(false, true, vh_gemmb_mk_192)
-K_GEMMB(false, false, vh_gemmb_mn_192)
+// workgroup per CU), and the fix-up of its stream-K round. The _ua, _ub and
+// _uab variants read A, B or both (only 4-byte aligned) with 32-bit loads.
+#define K_GEMMB(AK, BK, AU, BU, NAME) \
+  extern "C" __global__ void __launch_bounds__(256, 1) NAME(GemmArgs a) { gemm_big_impl<AK, BK, 192, AU, BU>(a); }
+#define K_GEMMB4(AK, BK, NAME)                  \
+  K_GEMMB(AK, BK, false, false, NAME)           \
+  K_GEMMB(AK, BK, true, false, NAME##_ua)       \
+  K_GEMMB(AK, BK, false, true, NAME##_ub)       \
+  K_GEMMB(AK, BK, true, true, NAME##_uab)
+K_GEMMB4(true, true, vh_gemmb_kk_192)
+K_GEMMB4(true, false, vh_gemmb_kn_192)
+K_GEMMB4(false, true, vh_gemmb_mk_192)
+K_GEMMB4(false, false, vh_gemmb_mn_192)
 extern "C" __global__ void __launch_bounds__(256) vh_gemmb_fix_192(GemmArgs a) { gemm_big_fix_impl<192>(a); }
 
 // AdamW
