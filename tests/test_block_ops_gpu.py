@@ -441,6 +441,9 @@ PERSISTENT_CASES = [
     ("lm_head dW^T, odd V", 768, 50257, 512, False, False, "", 1.0, 0),
     ("m-contiguous A, odd M", 1001, 777, 1536, False, True, "", 1.0, 0),
     ("edges, bases one float off", 1000, 1001, 2052, True, True, "alpha_acc", 1.0, 1),
+    # k-contiguous B with rows 32 KB apart (its lines prefetched a k tile ahead)
+    ("m-contiguous A, far-apart B rows", 1024, 768, 8192, False, True, "", 1.0, 0),
+    ("far-apart A rows, bias", 1024, 776, 5000, True, False, "bias", 1.0, 0),
 ]
 
 
