@@ -370,6 +370,28 @@ def test_reduce_and_strided_copy(vh):
     np.testing.assert_array_equal(fetch(vh, OUT, (300, 4)), O.reduce(xt, 1))
 
 
+def test_strided_copy_transposed_views(vh):
+    """contiguous() of transposed views (a last dim with a stride, the one before
+    it unit-stride; up to two leading dims) runs the LDS-tiled transpose:
+    exact copies, edge tiles included."""
+    r = rng(8)
+    cases = [((777, 1000), None), ((3, 130, 67), (0, 2, 1)), ((3, 130, 67), (1, 0, 2)), ((2, 3, 65, 129), (0, 1, 3, 2)),
+             ((64, 64), None), ((17, 5000), None)]
+    for shape, perm in cases:
+        x = r.normal(size=shape).astype(np.float32)
+        X = dev(vh, x)
+        if perm is None:  # the 2-D transpose
+            view = x.T
+            dims, strides = view.shape, (1, shape[1])
+        else:
+            view = np.transpose(x, perm)
+            cstr = [int(np.prod(shape[i + 1:])) for i in range(len(shape))]
+            dims, strides = view.shape, tuple(cstr[p] for p in perm)
+        OUT = out(vh, dims)
+        vh.check(vh.lib.vh_strided_copy(X.ptr, vh.layout(dims, strides), OUT.ptr, None))
+        np.testing.assert_array_equal(fetch(vh, OUT, dims), np.ascontiguousarray(view), err_msg=str(shape))
+
+
 def test_arena_reuse_and_zeroing(vh):
     before = vh.mem_stats()
     bufs = [vh.DeviceBuffer(1 << 20, zero=True) for _ in range(4)]

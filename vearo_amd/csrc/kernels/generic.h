@@ -85,6 +85,32 @@ VH_DEV void strided_copy_impl(const CopyArgs& a) {
     a.dst[i] = a.src[strided_offset<IT>((IT)i, a.sl, a.sl)];
 }
 
+// A transposed view made contiguous through a 64 x 64 LDS tile: reads run
+// along the source's unit-stride dim (r), writes along the destination's (c),
+// both 256 bytes per wave instruction; the tile is padded to 65 columns so
+// the column reads hit 64 different banks.
+VH_DEV void transpose_impl(const TransposeArgs& a) {
+  __shared__ float t[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t c0 = (int64_t)blockIdx.x * 64, r0 = (int64_t)blockIdx.y * 64;
+  const int64_t b = blockIdx.z;
+  const float* src = a.src + (b / a.nb1) * a.sb0 + (b % a.nb1) * a.sb1;
+  float* dst = a.dst + b * a.R * a.C;
+  const int64_t r = r0 + tx;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t c = c0 + ty + 4 * i;
+    if (r < a.R && c < a.C) t[ty + 4 * i][tx] = src[r + c * a.sc];
+  }
+  __syncthreads();
+  const int64_t c = c0 + tx;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t rr = r0 + ty + 4 * i;
+    if (rr < a.R && c < a.C) dst[rr * a.C + c] = t[tx][ty + 4 * i];
+  }
+}
+
 VH_DEV void fill_impl(const FillArgs& a) {
   const int64_t n4 = (reinterpret_cast<uintptr_t>(a.p) & 15) ? 0 : a.n / 4;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;

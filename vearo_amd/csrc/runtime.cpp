@@ -87,12 +87,12 @@ int get_fn(const std::string& name, hipFunction_t* out) {
 
 template <typename A>
 int launch(const std::string& name, unsigned gx, unsigned gy, unsigned block, unsigned shmem,
-           hipStream_t s, A args) {
-  if (gx == 0 || gy == 0) return VH_OK;
+           hipStream_t s, A args, unsigned gz = 1) {
+  if (gx == 0 || gy == 0 || gz == 0) return VH_OK;
   hipFunction_t f;
   VH_TRY(get_fn(name, &f));
   void* params[] = {&args};
-  VH_HIP(hipModuleLaunchKernel(f, gx, gy, 1, block, 1, 1, shmem, s, params, nullptr));
+  VH_HIP(hipModuleLaunchKernel(f, gx, gy, gz, block, 1, 1, shmem, s, params, nullptr));
   return VH_OK;
 }
 
@@ -1127,6 +1127,26 @@ int vh_strided_copy(const float* src, const vh_layout* sl, float* dst, void* str
   if (is_contig(sl)) {
     VH_HIP(hipMemcpyAsync(dst, src, (size_t)n * sizeof(float), hipMemcpyDeviceToDevice, s));
     return VH_OK;
+  }
+  // A transposed view (last dim strided, the one before it unit-stride; up to
+  // two leading dims): the LDS-tiled transpose, coalesced on both sides.
+  const int r = sl->rank;
+  if (r >= 2 && r <= 4 && sl->strides[r - 2] == 1 && sl->strides[r - 1] != 1 && sl->dims[r - 2] >= 16 &&
+      sl->dims[r - 1] >= 16) {
+    TransposeArgs t{src, dst, sl->dims[r - 2], sl->dims[r - 1], sl->strides[r - 1], 1, 0, 0};
+    int64_t nb = 1;
+    if (r == 3) {
+      nb = sl->dims[0];
+      t.nb1 = sl->dims[0];
+      t.sb1 = sl->strides[0];
+    } else if (r == 4) {
+      nb = sl->dims[0] * sl->dims[1];
+      t.nb1 = sl->dims[1];
+      t.sb0 = sl->strides[0];
+      t.sb1 = sl->strides[1];
+    }
+    if (cdiv(t.C, 64) < (int64_t(1) << 31) && cdiv(t.R, 64) < 65536 && nb < 65536)
+      return launch("vh_transpose", (unsigned)cdiv(t.C, 64), (unsigned)cdiv(t.R, 64), 256, 0, s, t, (unsigned)nb);
   }
   CopyArgs a{src, dst, to_kl(*sl), n};
   const int64_t blocks = std::min<int64_t>(cdiv(n, 256), 16384);

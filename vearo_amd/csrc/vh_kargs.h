@@ -317,6 +317,16 @@ struct CopyArgs {
   int64_t n;
 };
 
+// dst[b][r][c] = src[b0 * sb0 + b1 * sb1 + r + c * sc] for a view whose last
+// dim is strided and whose second-to-last has unit stride (a transpose), with
+// up to two leading dims flattened into b = b0 * nb1 + b1.
+struct TransposeArgs {
+  const float* src;
+  float* dst;
+  int64_t R, C, sc;
+  int64_t nb1, sb0, sb1;
+};
+
 struct FillArgs {
   float* p;
   int64_t n;
