@@ -315,6 +315,27 @@ def test_cross_entropy_kats_and_panics(vh):
 
 
 # --------------------------------------------------------- composites (a13)
+def test_binary_row_broadcast(vh):
+    """A contiguous operand against a vector over its last dim (a bias add, or
+    the vector on the left of a sub/div) takes the row-broadcast stream: the
+    same values as the broadcast rule, both operand orders, 16-byte and 4-byte
+    units."""
+    r = rng(16)
+    for full_shape, vec_shape in (((64, 3072), (3072,)), ((4, 33, 769), (769,)), ((5, 7, 128), (1, 1, 128))):
+        f = r.normal(size=full_shape).astype(np.float32)
+        v = (r.normal(size=vec_shape) + 3).astype(np.float32)
+        F, Vd = dev(vh, f), dev(vh, v)
+        for op, fn in enumerate((np.add, np.subtract, np.multiply, np.divide)):
+            for left in (False, True):
+                OUT = out(vh, full_shape)
+                a, al, b, bl = (Vd, v.shape, F, f.shape) if left else (F, f.shape, Vd, v.shape)
+                vh.check(vh.lib.vh_binary(op, a.ptr, vh.layout(al), b.ptr, vh.layout(bl), OUT.ptr, None))
+                want = fn(v, f) if left else fn(f, v)
+                np.testing.assert_array_equal(fetch(vh, OUT, full_shape), want.astype(np.float32),
+                                              err_msg=f"{full_shape} op={op} left={left}")
+
+
+
 def test_binary_broadcast_and_strided(vh):
     r = rng(6)
     cases = [((64, 3072), (3072,)), ((3, 1, 5), (4, 1)), ((16, 12, 128, 128), (16, 12, 128, 1)),

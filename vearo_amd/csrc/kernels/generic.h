@@ -43,6 +43,25 @@ VH_DEV void binary_contig_impl(const BinaryArgs& a) {
   }
 }
 
+// op(full, vec) or op(vec, full) with a contiguous vector of length bn
+// repeating along the rows of a contiguous full operand (a bias add): one unit
+// per thread over the whole output, streaming loads and stores of the full
+// operand, the vector read through the caches. VW divides bn, so a unit stays
+// within one row.
+template <int VW>
+VH_DEV void binary_rowbcast_impl(const BinaryArgs& a) {
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (u >= a.n / VW) return;
+  const float* full = a.vec_lhs ? a.r : a.l;
+  const float* vec = a.vec_lhs ? a.l : a.r;
+  const Unit<VW> f = load_stream<VW>(full + u * VW);
+  const Unit<VW> v = *reinterpret_cast<const Unit<VW>*>(vec + (u * VW) % a.bn);
+  Unit<VW> o;
+#pragma unroll
+  for (int j = 0; j < VW; ++j) o.v[j] = a.vec_lhs ? apply_op(a.op, v.v[j], f.v[j]) : apply_op(a.op, f.v[j], v.v[j]);
+  store_stream<VW>(a.out + u * VW, o);
+}
+
 template <typename IT>
 VH_DEV void binary_strided_impl(const BinaryArgs& a) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;

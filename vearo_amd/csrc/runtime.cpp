@@ -1071,12 +1071,28 @@ int vh_binary(int op, const float* l, const vh_layout* ll, const float* r, const
   if (!l || !r || !out) return fail(VH_ERR_INVALID, "vh_binary: null pointer");
   bool same = ll->rank == rl->rank;
   for (int i = 0; same && i < ll->rank; ++i) same = ll->dims[i] == rl->dims[i];
-  BinaryArgs a{l, r, out, ol, lk, rk, n, op, 0};
+  BinaryArgs a{l, r, out, ol, lk, rk, n, op, 0, 0, 0};
   hipStream_t s = S(stream);
   if (same && is_contig(ll) && is_contig(rl)) {
     const bool vec = n % 4 == 0 && aligned16(l) && aligned16(r) && aligned16(out);
     const int64_t blocks = std::min<int64_t>(cdiv(n / (vec ? 4 : 1), 256), 16384);
     return launch(vec ? "vh_binary_contig_v4" : "vh_binary_contig_v1", (unsigned)blocks, 1, 256, 0, s, a);
+  }
+  // A contiguous operand covering the whole output and a contiguous vector
+  // over its last dim (a bias): the row-broadcast stream.
+  const int64_t N = ol.dims[R - 1];
+  auto covers = [&](const vh_layout* t) { return is_contig(t) && numel(t) == n; };
+  auto last_vec = [&](const vh_layout* t) {
+    return t->rank >= 1 && is_contig(t) && numel(t) == N && t->dims[t->rank - 1] == N;
+  };
+  const bool rvec = covers(ll) && last_vec(rl), lvec = !rvec && covers(rl) && last_vec(ll);
+  if ((rvec || lvec) && N > 0 && n / N > 1 && cdiv(n, 256) < (int64_t(1) << 31)) {
+    a.bn = N;
+    a.vec_lhs = lvec ? 1 : 0;
+    const bool vec = N % 4 == 0 && aligned16(l) && aligned16(r) && aligned16(out);
+    const int vw = vec ? 4 : 1;
+    return launch(vec ? "vh_binary_rowbcast_v4" : "vh_binary_rowbcast_v1", (unsigned)cdiv(n / vw, 256), 1, 256, 0, s,
+                  a);
   }
   const int64_t blocks = std::min<int64_t>(cdiv(n, 256), 16384);
   return launch(n < INT32_MAX ? "vh_binary_strided_i32" : "vh_binary_strided_i64", (unsigned)blocks, 1,
