@@ -156,3 +156,31 @@ def test_dropin_overfits_like_the_reference_test(vh):
     loss = d.step(backward=False)
     assert loss < 0.05, loss
     d.close()
+
+
+def test_steps_do_not_grow_device_memory(vh):
+    """The reference's memory-regression check (crates/vearo/tests/memory_regression.rs:
+    103-137: slots must not grow over 25 training steps), for both step drivers
+    on one device: after a few warm-up steps the library's live bytes and the
+    bytes it holds from hipMalloc stay where they were over 25 more steps."""
+    from vearo_amd import _block
+    cfg = (2, 128, 128, 4, 512, 1000, 128)
+    params, ids, tg = random_model(cfg, 5)
+    for name, make, run in (
+            ("dropin", lambda: dropin(cfg), lambda m: m.step(backward=True, adamw=True)),
+            ("fused", lambda: _block.Gpt(_block.GptConfig(*cfg)), lambda m: (m.train_step(), m.loss()))):
+        print("memory growth", name, flush=True)
+        m = make()
+        m.set_params(params)
+        m.set_inputs(ids, tg)
+        for _ in range(3):
+            run(m)
+        vh.sync()
+        before = vh.mem_stats()
+        for _ in range(25):
+            run(m)
+        vh.sync()
+        after = vh.mem_stats()
+        assert after.live_bytes == before.live_bytes, (name, before.live_bytes, after.live_bytes)
+        assert after.hip_bytes <= before.hip_bytes, (name, before.hip_bytes, after.hip_bytes)
+        m.close()

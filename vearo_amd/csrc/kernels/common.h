@@ -29,16 +29,25 @@ VH_DEV float dpp_mov(float v) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+// Row value of 16-lane row `ROW` of the wave (wave-uniform, via v_readlane).
+template <int ROW>
+VH_DEV float row_value(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), ROW * 16));
+}
+
 // Sum / max over aligned groups of W lanes (W = 2..64); every lane of the group
 // ends with the same bits (each step combines the two halves commutatively).
+// A whole wave (W = 64) combines its four 16-lane row values with v_readlane
+// as (r0 + r1) + (r2 + r3) -- the same bits as an xor-16 then xor-32 exchange,
+// without the two LDS-unit permutes on the row's critical path.
 template <int W>
 VH_DEV float group_sum(float v) {
   if constexpr (W >= 2) v += dpp_mov<DPP_QUAD_XOR1>(v);
   if constexpr (W >= 4) v += dpp_mov<DPP_QUAD_XOR2>(v);
   if constexpr (W >= 8) v += dpp_mov<DPP_ROW_HALF_MIRROR>(v);
   if constexpr (W >= 16) v += dpp_mov<DPP_ROW_MIRROR>(v);
-  if constexpr (W >= 32) v += __shfl_xor(v, 16, 64);
-  if constexpr (W >= 64) v += __shfl_xor(v, 32, 64);
+  if constexpr (W == 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (W == 64) v = (row_value<0>(v) + row_value<1>(v)) + (row_value<2>(v) + row_value<3>(v));
   return v;
 }
 
@@ -48,8 +57,9 @@ VH_DEV float group_max(float v) {
   if constexpr (W >= 4) v = fmaxf(v, dpp_mov<DPP_QUAD_XOR2>(v));
   if constexpr (W >= 8) v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
   if constexpr (W >= 16) v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
-  if constexpr (W >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
-  if constexpr (W >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+  if constexpr (W == 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+  if constexpr (W == 64)
+    v = fmaxf(fmaxf(row_value<0>(v), row_value<1>(v)), fmaxf(row_value<2>(v), row_value<3>(v)));
   return v;
 }
 
