@@ -133,12 +133,13 @@ struct GbSeg {
 };
 #define GB_SLOTS VH_GEMMB_SLOTS  // workspace slots per workgroup: stream-K first / last piece
 
-// A_U / B_U: the operand is only 4-byte aligned (a leading dimension or base
-// not a multiple of 16 bytes, or a row-contiguous extent not a multiple of 4):
-// its pieces load as four 32-bit reads, each bounds-checked on its own, so a
-// piece that straddles a row end or the operand's end reads exactly what lies
-// in range.
-template <bool A_KC, bool B_KC, int BN, bool A_U = false, bool B_U = false, int PFA = 0, int PFB = 0>
+// Operands need only 4-byte alignment: a 128-bit buffer load at a 4-byte-aligned
+// offset returns the four floats there, and the record-count check applies to
+// each of its dwords on its own (a load straddling the record's end returns
+// the in-range dwords and zeros; measured on MI355X), so a leading dimension
+// like 50257 floats or a base one float into an allocation takes the same
+// loads as an aligned operand.
+template <bool A_KC, bool B_KC, int BN, int PFA = 0, int PFB = 0>
 VH_DEV void gemm_big_impl(const GemmArgs& a) {
   static_assert(BN == 256 || BN == 192, "tile width");
   constexpr int NB = BN / 64;  // 32-wide n tiles per wave
@@ -215,23 +216,14 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
   };
   // Staging registers: one k tile's pieces of A and B.
   vh_f4 ga[OA::PER], gb[OB::PER];
-  auto piece = [](__amdgpu_buffer_rsrc_t r, uint32_t off, auto unaligned) -> vh_f4 {
-    if constexpr (decltype(unaligned)::value) {
-      vh_f4 v;
-      v.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
-      v.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 4, 0, 0));
-      v.z = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 8, 0, 0));
-      v.w = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 12, 0, 0));
-      return v;
-    } else {
-      return __builtin_bit_cast(vh_f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-    }
+  auto piece = [](__amdgpu_buffer_rsrc_t r, uint32_t off) -> vh_f4 {
+    return __builtin_bit_cast(vh_f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
   };
   auto gload = [&](__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb) {
 #pragma unroll
-    for (int i = 0; i < OA::PER; ++i) ga[i] = piece(ra, goa[i], std::integral_constant<bool, A_U>{});
+    for (int i = 0; i < OA::PER; ++i) ga[i] = piece(ra, goa[i]);
 #pragma unroll
-    for (int i = 0; i < OB::PER; ++i) gb[i] = piece(rb, gob[i], std::integral_constant<bool, B_U>{});
+    for (int i = 0; i < OB::PER; ++i) gb[i] = piece(rb, gob[i]);
   };
   auto swrite = [&](float* SA, float* SB) {
 #pragma unroll
@@ -326,10 +318,8 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
   //      second half of quarter 3, so the next step starts on fragments
   //      already in registers.
   constexpr int VM = OA::PER + OB::PER;                  // LDS writes per step
-  constexpr int VL = (A_U ? 4 : 1) * OA::PER + (B_U ? 4 : 1) * OB::PER;  // load instructions
-  constexpr int LPM = (A_U || B_U) ? 2 : 1;              // loads placed per product
-  static_assert(VL % LPM == 0, "loads pair up");
-  constexpr int SP = VM + VL / LPM;                      // quarter-0 products that carry the staging
+  constexpr int VL = OA::PER + OB::PER;                  // load instructions per step
+  constexpr int SP = VM + VL;                            // quarter-0 products that carry the staging
   constexpr int MQ = 16 * NB;                            // products per quarter
   constexpr int RA = A_KC ? 1 : 4, RB = B_KC ? 1 : 4;    // LDS read instructions per fragment
   static_assert(SP <= MQ, "staging fits in quarter 0");
@@ -372,9 +362,9 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
       __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
     }
 #pragma unroll
-    for (int i = 0; i < VL / LPM; ++i) {
+    for (int i = 0; i < VL; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, LPM, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
     // Quarter 0: after the staging, quarter 1's reads over the products
     // left; quarters 1-2: the next quarter's reads one per RP products from

@@ -216,27 +216,18 @@ K_GEMMP(false, false, vh_gemmp_m4_n4)
 extern "C" __global__ void __launch_bounds__(256) vh_gemm_reduce(GemmReduceArgs a) { gemm_reduce_impl(a); }
 
 // Large dense products: vh_gemmb_<A><B>_192, persistent 256 x 192 tiles (one
-// workgroup per CU), and the fix-up of its stream-K round. The _ua, _ub and
-// _uab variants read A, B or both (only 4-byte aligned) with 32-bit loads.
-#define K_GEMMB(AK, BK, AU, BU, PA, PB, NAME) \
-  extern "C" __global__ void __launch_bounds__(256, 1) NAME(GemmArgs a) { gemm_big_impl<AK, BK, 192, AU, BU, PA, PB>(a); }
-#define K_GEMMB4(AK, BK, NAME)                        \
-  K_GEMMB(AK, BK, false, false, 0, 0, NAME)           \
-  K_GEMMB(AK, BK, true, false, 0, 0, NAME##_ua)       \
-  K_GEMMB(AK, BK, false, true, 0, 0, NAME##_ub)       \
-  K_GEMMB(AK, BK, true, true, 0, 0, NAME##_uab)
-K_GEMMB4(true, true, vh_gemmb_kk_192)
-K_GEMMB4(true, false, vh_gemmb_kn_192)
-K_GEMMB4(false, true, vh_gemmb_mk_192)
-K_GEMMB4(false, false, vh_gemmb_mn_192)
+// workgroup per CU), and the fix-up of its stream-K round.
+#define K_GEMMB(AK, BK, PA, PB, NAME) \
+  extern "C" __global__ void __launch_bounds__(256, 1) NAME(GemmArgs a) { gemm_big_impl<AK, BK, 192, PA, PB>(a); }
+K_GEMMB(true, true, 0, 0, vh_gemmb_kk_192)
+K_GEMMB(true, false, 0, 0, vh_gemmb_kn_192)
+K_GEMMB(false, true, 0, 0, vh_gemmb_mk_192)
+K_GEMMB(false, false, 0, 0, vh_gemmb_mn_192)
 // _pa / _pb: a k-contiguous A / B whose rows lie far apart (the logits
 // gradient as A of lm_head's dx product) prefetches its lines a k tile ahead.
-K_GEMMB(true, true, false, false, 1, 0, vh_gemmb_kk_192_pa)
-K_GEMMB(true, true, true, false, 1, 0, vh_gemmb_kk_192_ua_pa)
-K_GEMMB(true, false, false, false, 1, 0, vh_gemmb_kn_192_pa)
-K_GEMMB(true, false, true, false, 1, 0, vh_gemmb_kn_192_ua_pa)
-K_GEMMB(false, true, false, false, 0, 1, vh_gemmb_mk_192_pb)
-K_GEMMB(false, true, false, true, 0, 1, vh_gemmb_mk_192_ub_pb)
+K_GEMMB(true, true, 1, 0, vh_gemmb_kk_192_pa)
+K_GEMMB(true, false, 1, 0, vh_gemmb_kn_192_pa)
+K_GEMMB(false, true, 0, 1, vh_gemmb_mk_192_pb)
 extern "C" __global__ void __launch_bounds__(256) vh_gemmb_fix_192(GemmArgs a) { gemm_big_fix_impl<192>(a); }
 
 // AdamW

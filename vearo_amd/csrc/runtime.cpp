@@ -1296,22 +1296,17 @@ thread_local int g_gemm_path = VH_GEMM_PATH_NONE;
 
 // The persistent 256 x 192-tile kernel (kernels/gemm_big.h) for a large dense
 // unbatched product, when its conditions hold; *taken reports whether it ran.
-// Conditions: a tile's reads within 2^32 bytes of its origin (leading
-// dimensions < 2^22); k tile and tile counts below 2^31 (K < 2^26). An operand
-// loads 128-bit pieces when its base and leading dimension are multiples of 16
-// bytes and, if row-contiguous, its extent (M or N) is a multiple of 4, so no
-// piece straddles the operand's end; otherwise the _ua/_ub/_uab variant loads
-// its pieces as 32-bit reads. A k-contiguous operand with K % 32 != 0 splits
-// K: the kernel takes the whole 32-wide k tiles and the tiled kernel adds the
-// rest (alpha times the tail product) into C.
+// Conditions: 4-byte-aligned operand bases (its 128-bit loads need no more); a
+// tile's reads within 2^32 bytes of its origin (leading dimensions < 2^22); k
+// tile and tile counts below 2^31 (K < 2^26). A k-contiguous operand with
+// K % 32 != 0 splits K: the kernel takes the whole 32-wide k tiles and the
+// tiled kernel adds the rest (alpha times the tail product) into C.
 int gemm_big(const vh_gemm_desc* d, bool akc, bool bkc, int64_t lda, int64_t ldb, hipStream_t s, bool* taken) {
   *taken = false;
   const int64_t M = d->M, N = d->N, K = d->K;
   if (d->batch[0] * d->batch[1] != 1 || d->causal != VH_GEMM_DENSE || K <= 0) return VH_OK;
   if (M < VH_GEMMB_TM || N < VH_GEMMB_TN || (double)M * (double)N * (double)K < 67108864.0) return VH_OK;
   if (reinterpret_cast<uintptr_t>(d->a) % 4 != 0 || reinterpret_cast<uintptr_t>(d->b) % 4 != 0) return VH_OK;
-  const bool ua = !(aligned16(d->a) && lda % 4 == 0 && (akc || M % 4 == 0));
-  const bool ub = !(aligned16(d->b) && ldb % 4 == 0 && (bkc || N % 4 == 0));
   if (lda >= (int64_t(1) << 22) || ldb >= (int64_t(1) << 22) || K >= (int64_t(1) << 26)) return VH_OK;
   const int G = std::max(8, g_rt.cu_count / 8 * 8);
   const int64_t K32 = (akc || bkc) ? K / 32 * 32 : K;
@@ -1328,13 +1323,12 @@ int gemm_big(const vh_gemm_desc* d, bool akc, bool bkc, int64_t lda, int64_t ldb
   }
   // A k-contiguous operand whose rows are 16 KB or more apart streams its
   // lines from HBM one k tile (128 bytes a row) at a time: prefetch them a k
-  // tile ahead when the tiles run long enough in k for it to pay (A first).
-  // (Variants exist for a prefetched A with B aligned, and a prefetched B
-  // with A aligned and row-contiguous.)
-  const bool pfa = akc && lda >= 4096 && K >= 1024 && !ub;
-  const bool pfb = !akc && bkc && ldb >= 4096 && K >= 1024 && !ua;
+  // tile ahead when the tiles run long enough in k for it to pay (A first; a
+  // prefetched B only with A row-contiguous).
+  const bool pfa = akc && lda >= 4096 && K >= 1024;
+  const bool pfb = !akc && bkc && ldb >= 4096 && K >= 1024;
   const std::string name = std::string("vh_gemmb_") + (akc ? "k" : "m") + (bkc ? "k" : "n") + "_192" +
-                           (ua && ub ? "_uab" : ua ? "_ua" : ub ? "_ub" : "") + (pfa ? "_pa" : pfb ? "_pb" : "");
+                           (pfa ? "_pa" : pfb ? "_pb" : "");
   int rc = launch(name, (unsigned)G, 1, 256, 0, s, g);
   if (rc == VH_OK && rem > 0) {
     GemmArgs f = g;
