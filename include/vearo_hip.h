@@ -344,6 +344,21 @@ int vh_fused_attention_bwd(const float* q, const vh_layout* ql, const float* k,
                            const vh_layout* dvl, void* scratch, size_t scratch_bytes,
                            void* stream);
 size_t vh_fused_attention_scratch_bytes(int64_t B, int64_t H, int64_t S, int backward);
+/* Whether this call's additive mask may be dropped for causal = 1 with the
+ * same results: *is_causal = 1 when the mask's last two dims are [S, S], its
+ * entries on and below the diagonal are +-0 and those above are at most -1,
+ * q, k, v (and dout, when not NULL) are finite, and the smallest masked |value|
+ * exceeds twice the largest score the product can form (scale * Dk *
+ * max|q| * max|k|) by enough that every masked exp() underflows to exactly 0
+ * -- so the skipped blocks would have contributed exact zeros. One pass over
+ * the operands and the mask on `stream`, then a wait for the answer (the
+ * call returns after the stream drains). No counterpart in the reference: the
+ * BackendOps fused_attention slots call it so that a model's -1e9 triangle
+ * (nn:763-771) takes the causal kernels. */
+int vh_attention_mask_is_causal(const float* q, const vh_layout* ql, const float* k,
+                                const vh_layout* kl, const float* v, const vh_layout* vl,
+                                const float* dout, const vh_layout* dol, const float* mask,
+                                const vh_layout* ml, int* is_causal, void* stream);
 /* The backward from the probabilities the forward computed: a caller-supplied
  * forward scratch holds P [B, H, S, S] on return, and passing it here as P skips
  * recomputing it (same results as vh_fused_attention_bwd; P already carries the

@@ -398,6 +398,59 @@ int main() {
     CHECK(maxdiff(dv.to_vec_f32(), rv) < 1e-4, "dv");
   });
 
+  // The slot drops SimpleGPT's -1e9 triangle (nn:763-771) for the causal
+  // kernels only when vh_attention_mask_is_causal proves every masked exp()
+  // is exactly 0: then out, dq, dk and dv are the dense masked form's bits.
+  run("fused_attention_causal_mask_same_bits", [] {
+    const int B = 2, H = 3, S = 200, DK = 32, n = B * H * S * DK;
+    const auto qv = randn(n, 71), kv = randn(n, 72), vv = randn(n, 73), gv = randn(n, 74);
+    const Shape sh{B, H, S, DK};
+    auto dense = [&](const std::vector<float>& mv, const std::vector<float>& qx) {
+      Tensor q = Tensor::from_f32(qx, sh), k = Tensor::from_f32(kv, sh), v = Tensor::from_f32(vv, sh);
+      Tensor m = Tensor::from_f32(mv, Shape{S, S}), g = Tensor::from_f32(gv, sh);
+      Tensor o = Tensor::zeros(sh), dq = Tensor::zeros(sh), dk = Tensor::zeros(sh), dv = Tensor::zeros(sh);
+      vh_layout l{}, ml{};
+      l.rank = 4;
+      const int64_t d[4] = {B, H, S, DK}, st[4] = {(int64_t)H * S * DK, (int64_t)S * DK, DK, 1};
+      for (int i = 0; i < 4; ++i) { l.dims[i] = d[i]; l.strides[i] = st[i]; }
+      ml.rank = 2;
+      ml.dims[0] = ml.dims[1] = S;
+      ml.strides[0] = S;
+      ml.strides[1] = 1;
+      vh_ok(vh_fused_attention_fwd(q.data(), &l, k.data(), &l, v.data(), &l, m.data(), &ml, 0, o.data(), &l,
+                                   nullptr, 0, nullptr));
+      vh_ok(vh_fused_attention_bwd(q.data(), &l, k.data(), &l, v.data(), &l, m.data(), &ml, 0, g.data(), &l,
+                                   dq.data(), &l, dk.data(), &l, dv.data(), &l, nullptr, 0, nullptr));
+      return std::vector<std::vector<float>>{o.to_vec_f32(), dq.to_vec_f32(), dk.to_vec_f32(), dv.to_vec_f32()};
+    };
+    auto slot = [&](const std::vector<float>& mv, const std::vector<float>& qx) {
+      Tensor q = Tensor::from_f32(qx, sh), k = Tensor::from_f32(kv, sh), v = Tensor::from_f32(vv, sh);
+      Tensor m = Tensor::from_f32(mv, Shape{S, S}), g = Tensor::from_f32(gv, sh);
+      const auto o = q.fused_attention(k, v, &m).to_vec_f32();
+      auto [dq, dk, dv] = q.fused_attention_backward(k, v, &m, g);
+      return std::vector<std::vector<float>>{o, dq.to_vec_f32(), dk.to_vec_f32(), dv.to_vec_f32()};
+    };
+    auto same_bits = [](const std::vector<float>& a, const std::vector<float>& b) {
+      return a.size() == b.size() && std::memcmp(a.data(), b.data(), a.size() * 4) == 0;
+    };
+    std::vector<float> tri(S * S, 0.0f);
+    for (int r = 0; r < S; ++r)
+      for (int c = r + 1; c < S; ++c) tri[r * S + c] = -1e9f;
+    std::vector<float> shallow = tri;  // masked at -50: exponents that need not underflow
+    for (float& x : shallow)
+      if (x != 0.0f) x = -50.0f;
+    std::vector<float> qbig = qv;  // scores near 1e9 defeat the proof
+    qbig[5] = 4e9f;
+    const char* names[4] = {"out", "dq", "dk", "dv"};
+    for (int c = 0; c < 3; ++c) {
+      const auto& mv = c == 1 ? shallow : tri;
+      const auto& qx = c == 2 ? qbig : qv;
+      const auto a = dense(mv, qx), b = slot(mv, qx);
+      for (int i = 0; i < 4; ++i)
+        CHECK(same_bits(a[i], b[i]), std::string("case ") + std::to_string(c) + " " + names[i] + " bits");
+    }
+  });
+
   run("empty_tensors", [] {
     // crates/vearo-backend-cpu/src/lib.rs:2832-2864.
     Tensor x = Tensor::zeros(Shape{2, 0, 4});

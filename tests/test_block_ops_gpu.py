@@ -354,6 +354,76 @@ def test_attention_gpt_shape(vh):
             assert_parity(g[sl], c, name=f"{name}[{b},{h}]")
 
 
+def mask_is_causal(vh, q, k, v, mask, go=None):
+    """vh_attention_mask_is_causal on contiguous [B, H, S, Dk] operands."""
+    l = vh.layout(q.shape)
+    Q, K, V, M = dev(vh, q), dev(vh, k), dev(vh, v), dev(vh, mask)
+    ml = vh.layout(mask.shape)
+    G = dev(vh, go) if go is not None else None
+    c = ctypes.c_int(-1)
+    vh.check(vh.lib.vh_attention_mask_is_causal(Q.ptr, ctypes.byref(l), K.ptr, ctypes.byref(l), V.ptr,
+                                                ctypes.byref(l), G.ptr if G else None,
+                                                ctypes.byref(l) if G else None, M.ptr, ctypes.byref(ml),
+                                                ctypes.byref(c), None))
+    return c.value
+
+
+@pytest.mark.parametrize("case,want", [
+    ("tri -1e9", 1), ("tri -inf", 1), ("tri [1,1,S,S]", 1), ("tri [B,1,S,S]", 1), ("tri, bwd operands", 1),
+    ("allowed entry 0.5", 0), ("masked entry -0.5", 0), ("masked entry 0", 0), ("masked entry NaN", 0),
+    ("masked -1e3, scores ~1e4", 0), ("q holds inf", 0), ("v holds NaN", 0), ("dout holds inf", 0),
+    ("row-broadcast mask [1,S]", 0), ("masked -1e3, small scores", 1)])
+def test_attention_mask_probe(vh, case, want):
+    """The probe that lets the BackendOps attention slots take the causal
+    kernels: yes for the model's -1e9 (or -inf) triangle in any broadcast form
+    with ordinary operands; no for any entry off the pattern, a masked value
+    that small scores could overtake, or a non-finite operand (whose zero
+    probabilities would still make NaN in the dense form). When it says yes the
+    causal kernels give the dense masked form's bits."""
+    B, H, S, Dk = 2, 3, 160, 32
+    r = np.random.default_rng(abs(hash(case)) % 2**32)
+    q, k, v, go = (r.standard_normal((B, H, S, Dk), dtype=np.float32) for _ in range(4))
+    tri = np.zeros((S, S), np.float32)
+    tri[np.triu_indices(S, 1)] = -1e9
+    mask, g = tri, None
+    if case == "tri -inf":
+        mask = np.where(tri < 0, -np.inf, 0).astype(np.float32)
+    elif case == "tri [1,1,S,S]":
+        mask = tri[None, None]
+    elif case == "tri [B,1,S,S]":
+        mask = np.stack([tri, tri])[:, None]
+    elif case == "tri, bwd operands":
+        g = go
+    elif case == "allowed entry 0.5":
+        mask = tri.copy(); mask[7, 3] = 0.5
+    elif case == "masked entry -0.5":
+        mask = tri.copy(); mask[3, 7] = -0.5
+    elif case == "masked entry 0":
+        mask = tri.copy(); mask[3, 7] = 0.0
+    elif case == "masked entry NaN":
+        mask = tri.copy(); mask[3, 7] = np.nan
+    elif case == "masked -1e3, scores ~1e4":
+        mask = np.where(tri < 0, -1e3, 0).astype(np.float32)
+        q, k = q * 10, k * 10
+    elif case == "masked -1e3, small scores":
+        mask = np.where(tri < 0, -1e3, 0).astype(np.float32)
+    elif case == "q holds inf":
+        q[1, 2, 3, 4] = np.inf
+    elif case == "v holds NaN":
+        v[0, 1, 150, 5] = np.nan
+    elif case == "dout holds inf":
+        g = go.copy(); g[1, 0, 0, 0] = -np.inf
+    elif case == "row-broadcast mask [1,S]":
+        mask = np.zeros((1, S), np.float32)
+    print("mask probe", case, flush=True)
+    assert mask_is_causal(vh, q, k, v, mask, g) == want
+    if want:
+        dense = attention_gpu(vh, q, k, v, mask, 0, go)
+        causal = attention_gpu(vh, q, k, v, None, 1, go)
+        for name, a, b in zip(("out", "dq", "dk", "dv"), dense, causal):
+            np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32), err_msg=f"{case} {name}")
+
+
 @pytest.mark.parametrize("n", [4096, 1000003])
 def test_adamw_matches_oracle(vh, n):
     r = np.random.default_rng(n)

@@ -153,6 +153,11 @@ SIGNATURES = {
          POINTER(VhLayout), c_void_p, c_size_t, c_void_p],
     ),
     "vh_fused_attention_scratch_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int]),
+    "vh_attention_mask_is_causal": (
+        c_int,
+        [fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp,
+         POINTER(VhLayout), POINTER(c_int), c_void_p],
+    ),
     "vh_fused_attention_bwd_probs": (
         c_int,
         [fp, fp, POINTER(VhLayout), fp, POINTER(VhLayout), fp, POINTER(VhLayout), c_int, fp,

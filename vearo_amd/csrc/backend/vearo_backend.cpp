@@ -467,6 +467,22 @@ static void attention_checks(const Tensor& q, const Tensor& k, const Tensor& v) 
                                        " != q shape " + q.shape().str());
 }
 
+// An additive mask that is the causal triangle (exact zeros on and below the
+// diagonal, at most -1 above) with scores small enough that every masked
+// exponent underflows to exactly 0 -- SimpleGPT's -1e9 mask (nn:763-771) with
+// any ordinary activations -- gives the same bits as the causal kernels,
+// which skip the masked blocks; vh_attention_mask_is_causal proves that per
+// call (one pass over the operands and the mask, and a wait for its answer).
+static int causal_mask(const Tensor& q, const vh_layout& ql, const Tensor& k, const vh_layout& kl, const Tensor& v,
+                       const vh_layout& vl, const Tensor* g, const vh_layout* gl, const float* mask,
+                       const vh_layout& ml) {
+  if (!mask) return 0;
+  int c = 0;
+  check(vh_attention_mask_is_causal(q.data(), &ql, k.data(), &kl, v.data(), &vl, g ? g->data() : nullptr, gl,
+                                    mask, &ml, &c, nullptr));
+  return c;
+}
+
 // cpu:2366-2464: softmax(q k^T / sqrt(Dk) + mask) v, mask broadcast from the right.
 Tensor fused_attention(const Tensor& q0, const Tensor& k0, const Tensor& v0, const Tensor* mask) {
   attention_checks(q0, k0, v0);
@@ -476,8 +492,11 @@ Tensor fused_attention(const Tensor& q0, const Tensor& k0, const Tensor& v0, con
   const vh_layout ql = layout_of(q), kl = layout_of(k), vl = layout_of(v), ol = layout_of(out);
   vh_layout ml{};
   if (mask) ml = layout_of(*mask);
-  check(vh_fused_attention_fwd(q.data(), &ql, k.data(), &kl, v.data(), &vl, mask ? mask->data() : nullptr,
-                               mask ? &ml : nullptr, 0, out.data(), &ol, nullptr, 0, nullptr));
+  const float* mp = mask ? mask->data() : nullptr;
+  const int causal = causal_mask(q, ql, k, kl, v, vl, nullptr, nullptr, mp, ml);
+  if (causal) mp = nullptr;
+  check(vh_fused_attention_fwd(q.data(), &ql, k.data(), &kl, v.data(), &vl, mp, mp ? &ml : nullptr, causal,
+                               out.data(), &ol, nullptr, 0, nullptr));
   return out;
 }
 
@@ -498,9 +517,12 @@ std::tuple<Tensor, Tensor, Tensor> fused_attention_backward(const Tensor& q0, co
                   dl = layout_of(dq);
   vh_layout ml{};
   if (mask) ml = layout_of(*mask);
-  check(vh_fused_attention_bwd(q.data(), &ql, k.data(), &kl, v.data(), &vl, mask ? mask->data() : nullptr,
-                               mask ? &ml : nullptr, 0, g.data(), &gl, dq.data(), &dl, dk.data(), &dl,
-                               dv.data(), &dl, nullptr, 0, nullptr));
+  const float* mp = mask ? mask->data() : nullptr;
+  const int causal = causal_mask(q, ql, k, kl, v, vl, &g, &gl, mp, ml);
+  if (causal) mp = nullptr;
+  check(vh_fused_attention_bwd(q.data(), &ql, k.data(), &kl, v.data(), &vl, mp, mp ? &ml : nullptr, causal,
+                               g.data(), &gl, dq.data(), &dl, dk.data(), &dl, dv.data(), &dl, nullptr, 0,
+                               nullptr));
   return {dq, dk, dv};
 }
 

@@ -170,3 +170,88 @@ VH_DEV void col_partial_impl(const ColPartialArgs& a) {
   for (; r < r1; ++r) s += p[r * a.C];
   a.part[(int64_t)blockIdx.x * a.C + c] = s;
 }
+
+// One pass over an attention call's mask and operands. Grid (ceil(S / 16),
+// 5 * Y): grid y = segment * Y + the leading (b, h) pair; a workgroup takes 16
+// consecutive rows of one [.., S, last] block, 16 lanes to a row (128-bit
+// loads when the row is contiguous and 16-byte aligned). Mask element
+// (i, j) of its last two dims: j <= i must be +-0 (else flag 1); j > i must be
+// <= -1 and not NaN (else flag 2), and the smallest |value| of those is
+// tracked. q, k, v, g: the largest |x| as bits (NaN and inf sort above every
+// finite value). The workgroup folds its lanes, then adds to slot
+// (blockIdx.x + blockIdx.y) % 64 of `words` (8 words a slot: [0] flags (or),
+// [1] 0x7f800000 - min |masked| bits (max), [2 + seg - 1] max |x| bits (max)),
+// so no one address takes more than about a thousand atomics; the host folds the
+// 64 slots. Integer or / max only: the result does not depend on timing.
+VH_DEV void attn_probe_impl(const AttnProbeArgs& a) {
+  __shared__ uint32_t red[3][4];
+  const int seg = (int)(blockIdx.y / a.Y);
+  const int32_t bh = (int32_t)(blockIdx.y % a.Y);
+  const float* t = a.t[seg];
+  const int32_t d1 = a.d1[seg], d2 = a.d2[seg], d3 = a.d3[seg];
+  if (!t || bh >= a.d0[seg] * d1) return;
+  const int l16 = threadIdx.x & 15;
+  const float* blk = t + (int64_t)(bh / d1) * a.s0[seg] + (int64_t)(bh % d1) * a.s1[seg];
+  const int64_t s2 = a.s2[seg], s3 = a.s3[seg];
+  uint32_t hi = 0, lo = 0, bad = 0;  // lo: 0x7f800000 - |masked value| bits, largest kept
+  auto see = [&](float x, int32_t j, int32_t i2) {
+    const uint32_t m = __float_as_uint(x) & 0x7fffffffu;
+    if (seg == 0) {
+      if (j <= i2) {
+        if (m != 0) bad |= 1u;
+      } else if (!(x <= -1.0f)) {
+        bad |= 2u;
+      } else {
+        const uint32_t c = 0x7f800000u - m;  // m <= 0x7f800000 here (NaN fails above)
+        lo = c > lo ? c : lo;
+      }
+    } else {
+      hi = m > hi ? m : hi;
+    }
+  };
+  const int32_t i2 = (int32_t)blockIdx.x * 16 + (int32_t)(threadIdx.x >> 4);
+  if (i2 < d2) {
+    const float* row = blk + (int64_t)i2 * s2;
+    if (s3 == 1 && d3 % 4 == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
+#pragma unroll 4
+      for (int32_t j = 4 * l16; j < d3; j += 64) {
+        const float4 x = *reinterpret_cast<const float4*>(row + j);
+        see(x.x, j, i2);
+        see(x.y, j + 1, i2);
+        see(x.z, j + 2, i2);
+        see(x.w, j + 3, i2);
+      }
+    } else {
+#pragma unroll 4
+      for (int32_t j = l16; j < d3; j += 16) see(row[j * s3], j, i2);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t h2 = (uint32_t)__shfl_xor((int)hi, off, 64), l2 = (uint32_t)__shfl_xor((int)lo, off, 64);
+    hi = h2 > hi ? h2 : hi;
+    lo = l2 > lo ? l2 : lo;
+    bad |= (uint32_t)__shfl_xor((int)bad, off, 64);
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[0][w] = bad;
+    red[1][w] = lo;
+    red[2][w] = hi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 4; ++i) {
+      bad |= red[0][i];
+      lo = red[1][i] > lo ? red[1][i] : lo;
+      hi = red[2][i] > hi ? red[2][i] : hi;
+    }
+    uint32_t* slot = a.words + 8 * ((blockIdx.x + blockIdx.y) % 64);
+    if (seg == 0) {
+      if (bad) atomicOr(slot, bad);
+      if (lo) atomicMax(slot + 1, lo);
+    } else if (hi) {
+      atomicMax(slot + 1 + seg, hi);
+    }
+  }
+}

@@ -1767,6 +1767,80 @@ size_t vh_fused_attention_scratch_bytes(int64_t B, int64_t H, int64_t S, int bac
   return backward ? 2 * one : one;
 }
 
+int vh_attention_mask_is_causal(const float* q, const vh_layout* ql, const float* k, const vh_layout* kl,
+                                const float* v, const vh_layout* vl, const float* g, const vh_layout* gl,
+                                const float* mask, const vh_layout* ml, int* is_causal, void* stream) {
+  VH_TRY(require_init());
+  if (!is_causal) return fail(VH_ERR_INVALID, "vh_attention_mask_is_causal: null result pointer");
+  *is_causal = 0;
+  AttnShape sh;
+  VH_TRY(attn_layout(ql, "attention mask probe q", &sh, true));
+  VH_TRY(attn_layout(kl, "attention mask probe k", &sh, false));
+  VH_TRY(attn_layout(vl, "attention mask probe v", &sh, false));
+  if (g) VH_TRY(attn_layout(gl, "attention mask probe grad", &sh, false));
+  if (!mask || !ml) return fail(VH_ERR_INVALID, "vh_attention_mask_is_causal: no mask");
+  int64_t mst[4];
+  VH_TRY(attn_mask(ml, sh, mst));
+  if (sh.B * sh.H * sh.S * sh.Dk == 0 || !q || !k || !v) return VH_OK;
+  // The mask must carry the [S, S] block itself (a broadcast row or column
+  // cannot hold the triangle), each leading dim either its own or broadcast.
+  if (ml->rank < 2 || ml->dims[ml->rank - 1] != sh.S || ml->dims[ml->rank - 2] != sh.S) return VH_OK;
+  if (sh.S > INT32_MAX || sh.Dk > INT32_MAX || sh.B * sh.H > INT32_MAX) return VH_OK;
+  AttnProbeArgs a{};
+  const vh_layout* ls[5] = {ml, ql, kl, vl, g ? gl : nullptr};
+  const float* ts[5] = {mask, q, k, v, g};
+  for (int i = 0; i < 5; ++i) {
+    a.t[i] = ts[i];
+    if (!ts[i]) continue;
+    const vh_layout* l = ls[i];
+    int64_t dm[4], st[4];
+    for (int j = 0; j < 4; ++j) {
+      const int lj = j - (4 - l->rank);
+      dm[j] = lj >= 0 ? l->dims[lj] : 1;
+      st[j] = lj >= 0 ? l->strides[lj] : 0;
+    }
+    a.d0[i] = (int32_t)dm[0]; a.d1[i] = (int32_t)dm[1]; a.d2[i] = (int32_t)dm[2]; a.d3[i] = (int32_t)dm[3];
+    a.s0[i] = st[0]; a.s1[i] = st[1]; a.s2[i] = st[2]; a.s3[i] = st[3];
+  }
+  hipStream_t s = S(stream);
+  a.Y = (int32_t)std::max<int64_t>(sh.B * sh.H, (int64_t)a.d0[0] * a.d1[0]);
+  if ((int64_t)a.Y * 5 > 65535) return VH_OK;  // grid y limit: leave such calls on the dense path
+  Scratch sc;
+  VH_TRY(sc.get(s, nullptr, 0, 64 * 8 * sizeof(uint32_t)));
+  uint32_t* w = static_cast<uint32_t*>(sc.p);
+  VH_TRY(fill(w, 0.0f, 64 * 8, s));
+  a.words = w;
+  VH_TRY(launch("vh_attn_probe", (unsigned)cdiv(sh.S, 16), (unsigned)(5 * a.Y), 256, 0, s, a));
+  uint32_t slots[64 * 8];
+  VH_HIP(hipMemcpyAsync(slots, w, sizeof(slots), hipMemcpyDeviceToHost, s));
+  VH_HIP(hipStreamSynchronize(s));
+  uint32_t h[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int i = 0; i < 64; ++i) {
+    h[0] |= slots[8 * i];
+    for (int j = 1; j < 6; ++j) h[j] = std::max(h[j], slots[8 * i + j]);
+  }
+  h[1] = 0x7f800000u - h[1];  // the smallest |masked value| (inf when there is none)
+  auto fl = [](uint32_t b) { float f; std::memcpy(&f, &b, 4); return (double)f; };
+  if (h[0] != 0) return VH_OK;  // an allowed entry not +-0, or a masked one above -1 or NaN
+  const uint32_t kInf = 0x7f800000u;
+  if (h[2] >= kInf || h[3] >= kInf || h[4] >= kInf || (g && h[5] >= kInf)) return VH_OK;  // NaN or inf
+  // Largest |score| the product can form: |s| <= scale * Dk * max|q| * max|k|,
+  // widened for the f32 accumulation (relative Dk * 2^-24, under 1e-5 here).
+  const double scale = (double)(1.0f / std::sqrt((float)sh.Dk));
+  const double smax = scale * (double)sh.Dk * fl(h[2]) * fl(h[3]) * (1.0 + 1e-5) + 1e-30;
+  // A masked x = fl(s + m) less the row max (>= the diagonal's score, >= -smax)
+  // is at most 2 smax - |m| plus two roundings of ~|m| 2^-24 each; expf of
+  // anything below -104 is exactly 0 in f32, so ask for -256 with margin.
+  const double mmin = fl(h[1]);
+  if (!(mmin * (1.0 - 0x1p-22) - 2.0 * smax * (1.0 + 0x1p-22) > 256.0)) return VH_OK;
+  // The zero probabilities multiply v (and, backward, dP = dO v^T): those
+  // products stay finite, so 0 * x is exactly 0 as in the dense form.
+  const double vmax = fl(h[4]), gmax = g ? fl(h[5]) : 0.0;
+  if (g && !((double)sh.Dk * vmax * gmax < 1e37)) return VH_OK;
+  *is_causal = 1;
+  return VH_OK;
+}
+
 int vh_fused_attention_fwd(const float* q, const vh_layout* ql, const float* k, const vh_layout* kl,
                            const float* v, const vh_layout* vl, const float* mask, const vh_layout* ml,
                            int causal, float* out, const vh_layout* ol, void* scratch, size_t scratch_bytes,

@@ -341,3 +341,15 @@ struct StreamCopyArgs {
   float* dst;
   int64_t n4;
 };
+
+// Whether an additive attention mask may be replaced by the causal kernels
+// (vh_attention_mask_is_causal): segment 0 is the mask over its own dims
+// (right-aligned to 4, the last two [S, S]), segments 1-4 are q, k, v and the
+// output gradient ([B, H, S, Dk], unit last stride; rows = 0 for an absent one).
+struct AttnProbeArgs {
+  const float* t[5];
+  int32_t d0[5], d1[5], d2[5], d3[5];     // dims
+  int64_t s0[5], s1[5], s2[5], s3[5];     // strides (elements)
+  uint32_t* words;  // 64 slots of 8: [0] mask pattern failures, [1] 0x7f800000 - min |masked| bits, [2..5] max |x| bits of q, k, v, g
+  int32_t Y;        // grid y per segment: the largest leading (b, h) count
+};
