@@ -93,9 +93,14 @@ VH_DEV int gb_loff(int tid, int i) {
 
 // Buffer resource for the tile whose origin is `org`, covering `bytes` bytes
 // (clamped to 32 bits: the host guarantees a tile's reads fit below that).
+// The record count: bytes clamped to [0, 2^32 - 1], from the two 32-bit halves
+// (scalar compares only; a 64-bit compare needs a vector register, whose
+// write the compiler fences with a wait for every outstanding load).
 VH_DEV __amdgpu_buffer_rsrc_t gb_rsrc(const float* org, int64_t bytes) {
-  const int64_t b = bytes < 0 ? 0 : (bytes > 0xFFFFFFFFll ? 0xFFFFFFFFll : bytes);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(org), (short)0, (int)(uint32_t)b, GB_RSRC_W3);
+  const uint64_t u = (uint64_t)bytes;
+  const uint32_t hi = (uint32_t)(u >> 32), lo = (uint32_t)u;
+  const uint32_t nrec = (hi & 0x80000000u) ? 0u : (hi ? 0xFFFFFFFFu : lo);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(org), (short)0, (int)nrec, GB_RSRC_W3);
 }
 
 // Tile order index u -> (tm, tn): groups of GB_GROUP tile rows swept column
