@@ -217,18 +217,13 @@ K_GEMMP(false, false, vh_gemmp_m4_n4)
 extern "C" __global__ void __launch_bounds__(256) vh_gemm_reduce(GemmReduceArgs a) { gemm_reduce_impl(a); }
 
 // Large dense products: vh_gemmb_<A><B>_192, persistent 256 x 192 tiles (one
-// workgroup per CU), and the fix-up of its stream-K round.
-#define K_GEMMB(AK, BK, PA, PB, NAME) \
-  extern "C" __global__ void __launch_bounds__(256, 1) NAME(GemmArgs a) { gemm_big_impl<AK, BK, 192, PA, PB>(a); }
-K_GEMMB(true, true, 0, 0, vh_gemmb_kk_192)
-K_GEMMB(true, false, 0, 0, vh_gemmb_kn_192)
-K_GEMMB(false, true, 0, 0, vh_gemmb_mk_192)
-K_GEMMB(false, false, 0, 0, vh_gemmb_mn_192)
-// _pa / _pb: a k-contiguous A / B whose rows lie far apart (the logits
-// gradient as A of lm_head's dx product) prefetches its lines a k tile ahead.
-K_GEMMB(true, true, 1, 0, vh_gemmb_kk_192_pa)
-K_GEMMB(true, false, 1, 0, vh_gemmb_kn_192_pa)
-K_GEMMB(false, true, 0, 1, vh_gemmb_mk_192_pb)
+// 512-thread workgroup per CU), and the fix-up of its stream-K round.
+#define K_GEMMB(AK, BK, NAME) \
+  extern "C" __global__ void __launch_bounds__(512, 1) NAME(GemmArgs a) { gemm_big_impl<AK, BK, 192, 8>(a); }
+K_GEMMB(true, true, vh_gemmb_kk_192)
+K_GEMMB(true, false, vh_gemmb_kn_192)
+K_GEMMB(false, true, vh_gemmb_mk_192)
+K_GEMMB(false, false, vh_gemmb_mn_192)
 extern "C" __global__ void __launch_bounds__(256) vh_gemmb_fix_192(GemmArgs a) { gemm_big_fix_impl<192>(a); }
 
 // AdamW

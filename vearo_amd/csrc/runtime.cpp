@@ -1321,15 +1321,8 @@ int gemm_big(const vh_gemm_desc* d, bool akc, bool bkc, int64_t lda, int64_t ldb
     VH_TRY(g_arena.alloc((size_t)G * VH_GEMMB_SLOTS * VH_GEMMB_TM * VH_GEMMB_TN * sizeof(float), s, &ws));
     g.ws = static_cast<float*>(ws);
   }
-  // A k-contiguous operand whose rows are 16 KB or more apart streams its
-  // lines from HBM one k tile (128 bytes a row) at a time: prefetch them a k
-  // tile ahead when the tiles run long enough in k for it to pay (A first; a
-  // prefetched B only with A row-contiguous).
-  const bool pfa = akc && lda >= 4096 && K >= 1024;
-  const bool pfb = !akc && bkc && ldb >= 4096 && K >= 1024;
-  const std::string name = std::string("vh_gemmb_") + (akc ? "k" : "m") + (bkc ? "k" : "n") + "_192" +
-                           (pfa ? "_pa" : pfb ? "_pb" : "");
-  int rc = launch(name, (unsigned)G, 1, 256, 0, s, g);
+  const std::string name = std::string("vh_gemmb_") + (akc ? "k" : "m") + (bkc ? "k" : "n") + "_192";
+  int rc = launch(name, (unsigned)G, 1, 512, 0, s, g);
   if (rc == VH_OK && rem > 0) {
     GemmArgs f = g;
     f.ksplit = G;
