@@ -112,7 +112,8 @@ def test_matmul_folds_shared_weight_batches(vh):
     input.matmul(weight.transpose(0, 1)), crates/vearo-nn/src/lib.rs:121-122)
     runs as one product over B*S rows, on the large-product kernel at this
     size; a left operand whose batches are not evenly spaced rows (its
-    transposed view) stays a batched product. Same results either way."""
+    transposed view) stays a batched product (on the large-product kernel's
+    batched walk at this size). Same results either way."""
     r = np.random.default_rng(12)
     a = r.standard_normal((4, 1024, 768), dtype=np.float32)
     w = (r.standard_normal((2304, 768)) * 0.02).astype(np.float32)
@@ -122,7 +123,7 @@ def test_matmul_folds_shared_weight_batches(vh):
     assert vh.lib.vh_gemm_last_path() == vh.GEMM_PATH_PERSISTENT
     assert_parity(got, ref, ref64, name="folded batches")
     got_t = run_matmul(vh, a, w.T, a_view="T", b_view="T")
-    assert vh.lib.vh_gemm_last_path() in (vh.GEMM_PATH_TILED, vh.GEMM_PATH_BATCHED)
+    assert vh.lib.vh_gemm_last_path() in (vh.GEMM_PATH_TILED, vh.GEMM_PATH_BATCHED, vh.GEMM_PATH_PERSISTENT)
     assert_parity(got_t, ref, ref64, name="batched")
 
 
@@ -154,6 +155,13 @@ def gemm_desc(vh, M, N, K, a, a_sm, a_sk, b, b_sk, b_sn, c, c_sm, **kw):
     d.causal = kw.get("causal", 0)
     if "e" in kw:
         d.e, d.e_sm, d.e_sn = kw["e"], kw["e_sm"], kw["e_sn"]
+    if "batch" in kw:
+        d.batch[0], d.batch[1] = kw["batch"]
+        d.a_sb[0], d.a_sb[1] = kw["a_sb"]
+        d.b_sb[0], d.b_sb[1] = kw["b_sb"]
+        d.c_sb[0], d.c_sb[1] = kw["c_sb"]
+        if "e_sb" in kw:
+            d.e_sb[0], d.e_sb[1] = kw["e_sb"]
     d.engine = kw.get("engine", vh.GEMM_ENGINE_DEFAULT)
     return d
 
@@ -571,6 +579,93 @@ def test_gemm_persistent_block_shapes(vh, case):
         d = gemm_desc(vh, M, N, K, A.ptr, a_sm, a_sk, B.ptr, b_sk, b_sn, C2.ptr, N, **kw)
         vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
         np.testing.assert_array_equal(fetch(vh, C2, (M, N)), got)
+
+
+def test_gemm_persistent_few_k_tiles_after_workspace_reuse(vh):
+    """Stream-K with fewer k tiles than workgroups leaves some workgroups an
+    empty run inside a split tile; the fix-up must skip their workspace slots,
+    which hold whatever an earlier product left there. A product with many
+    partial pieces first fills the (reused) workspace, then products with
+    102 and 120 k tiles in their stream-K round run against the oracle."""
+    r = np.random.default_rng(21)
+    def prod(M, N, K):
+        a = r.standard_normal((M, K), dtype=np.float32)
+        b = (r.standard_normal((K, N)) * 0.05).astype(np.float32)
+        A, B, C = dev(vh, a), dev(vh, np.ascontiguousarray(b.T)), out(vh, (M, N))
+        d = gemm_desc(vh, M, N, K, A.ptr, K, 1, B.ptr, 1, K, C.ptr, N)
+        vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+        assert vh.lib.vh_gemm_last_path() == vh.GEMM_PATH_PERSISTENT
+        return fetch(vh, C, (M, N)), a, b
+    prod(1024, 1000, 2048)  # 24 tiles x 64 k tiles split over every workgroup
+    for M, N, K in ((256, 1000, 544), (300, 400, 640)):
+        print("few k tiles", M, N, K, flush=True)
+        got, a, b = prod(M, N, K)
+        assert_parity(got, O.matmul(a, b), a.astype(np.float64) @ b.astype(np.float64), name=f"few k tiles {M}x{N}x{K}")
+
+
+BATCHED_PERSISTENT_CASES = [
+    # name, (B0, B1), M, N, K, akc, bkc, B shared over batches, epilogue
+    ("drop-in weight gradients: x^T g per batch", (4, 1), 768, 768, 1024, False, False, False, ""),
+    ("two batch dims, shared k-contiguous B, bias", (2, 3), 300, 200, 544, True, True, True, "bias"),
+    ("k tail, accumulate, alpha", (3, 1), 256, 192, 1000, True, False, False, "acc alpha"),
+    ("per-batch addend, stream-K remainder", (2, 1), 520, 400, 640, False, True, False, "full"),
+]
+
+
+@pytest.mark.parametrize("case", BATCHED_PERSISTENT_CASES, ids=[c[0] for c in BATCHED_PERSISTENT_CASES])
+def test_gemm_persistent_batched(vh, case):
+    """Batched dense products with k loops of 512 and more on the persistent
+    kernel: the tile list runs over every batch (tile-major within a batch),
+    each segment offsets A, B, C and the addend by its batch's strides, and a
+    batch's k-contiguous tail past the whole k tiles goes through the tiled
+    kernel. Against the oracle's batched matmul and float64, and the same bits
+    on a second call."""
+    name, (B0, B1), M, N, K, akc, bkc, shared, epi = case
+    print("persistent batched", name, flush=True)
+    r = np.random.default_rng(M + N + K)
+    nb = B0 * B1
+    a = r.standard_normal((B0, B1, M, K), dtype=np.float32)
+    b = (r.standard_normal((1 if shared else B0, 1 if shared else B1, K, N)) * 0.05).astype(np.float32)
+    A = dev(vh, np.ascontiguousarray(a if akc else np.swapaxes(a, 2, 3)))
+    Bd = dev(vh, np.ascontiguousarray(np.swapaxes(b, 2, 3) if bkc else b))
+    a_sm, a_sk = (K, 1) if akc else (1, M)
+    b_sk, b_sn = (1, K) if bkc else (N, 1)
+    kw = {}
+    ref = O.matmul(a, b)
+    ref64 = np.matmul(a.astype(np.float64), b.astype(np.float64))
+    c0 = np.zeros((B0, B1, M, N), np.float32)
+    keep = []
+    if "alpha" in epi:
+        kw["alpha"] = 0.5
+        ref, ref64 = ref * np.float32(0.5), ref64 * 0.5
+    if epi == "bias":
+        bias = (r.standard_normal(N) * 0.1).astype(np.float32)
+        keep.append(dev(vh, bias))
+        kw.update(e=keep[-1].ptr, e_sm=0, e_sn=1)
+        ref, ref64 = ref + bias, ref64 + bias
+    if epi == "full":
+        e = r.standard_normal((B0, B1, M, N), dtype=np.float32)
+        keep.append(dev(vh, e))
+        kw.update(e=keep[-1].ptr, e_sm=N, e_sn=1, e_sb=(B1 * M * N, M * N))
+        ref, ref64 = ref + e, ref64 + e
+    if "acc" in epi:
+        c0 = r.standard_normal((B0, B1, M, N), dtype=np.float32)
+        kw["accumulate"] = 1
+        ref, ref64 = c0 + ref, c0 + ref64
+    C = dev(vh, c0)
+    bsb = (0, 0) if shared else (B1 * K * N, K * N)
+    d = gemm_desc(vh, M, N, K, A.ptr, a_sm, a_sk, Bd.ptr, b_sk, b_sn, C.ptr, N, batch=(B0, B1),
+                  a_sb=(B1 * M * K, M * K), b_sb=bsb, c_sb=(B1 * M * N, M * N), **kw)
+    vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+    assert vh.lib.vh_gemm_last_path() == vh.GEMM_PATH_PERSISTENT, name
+    got = fetch(vh, C, (B0, B1, M, N))
+    assert_parity(got, ref, ref64, name=f"batched persistent {name}")
+    if "acc" not in epi:
+        C2 = out(vh, (B0, B1, M, N))
+        d = gemm_desc(vh, M, N, K, A.ptr, a_sm, a_sk, Bd.ptr, b_sk, b_sn, C2.ptr, N, batch=(B0, B1),
+                      a_sb=(B1 * M * K, M * K), b_sb=bsb, c_sb=(B1 * M * N, M * N), **kw)
+        vh.check(vh.lib.vh_gemm(ctypes.byref(d), None))
+        np.testing.assert_array_equal(fetch(vh, C2, (B0, B1, M, N)), got)
 
 
 def test_gemm_library_engine_is_an_ab_only(vh):

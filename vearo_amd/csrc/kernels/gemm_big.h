@@ -127,7 +127,7 @@ VH_DEV void gb_tile_of(int u, int tiles_m, int tiles_n, int& tm, int& tn) {
 struct GbSplit {
   int tiles, nk, full, rem, W, G;
   VH_DEV GbSplit(const GemmArgs& a, int G_) : G(G_) {
-    tiles = a.tiles_m * a.tiles_n;
+    tiles = a.tiles_m * a.tiles_n * (int)a.nbat;  // tiles of all batches (the host keeps it < 2^31)
     nk = (int)((a.K + GB_TK - 1) / GB_TK);
     full = tiles / G;
     rem = tiles - full * G;
@@ -137,11 +137,26 @@ struct GbSplit {
   VH_DEV int end(int g) const { return (int)((int64_t)W * (g + 1) / G); }
 };
 
-// One segment of a workgroup's list: C tile (m0, n0), k tiles [kt0, kt1).
+// One segment of a workgroup's list: C tile (m0, n0) of one batch, k tiles
+// [kt0, kt1), and that batch's element offsets into A, B, C and E.
 struct GbSeg {
   int m0, n0, kt0, kt1;
   int slot;  // -1: store C; else the workspace slot this partial piece goes to
+  int64_t ao, bo, co, eo;
 };
+
+// Tile u of the whole list -> batch (tile-major within a batch), its (tm, tn)
+// and the batch's offsets (batch = outer * nb2 + inner, each with its stride).
+VH_DEV void gb_locate(const GemmArgs& a, int u, int& tm, int& tn, GbSeg& s) {
+  const int tpb = a.tiles_m * a.tiles_n;
+  const int bat = u / tpb;
+  gb_tile_of(u - bat * tpb, a.tiles_m, a.tiles_n, tm, tn);
+  const int b1 = bat / a.nb2, b2 = bat - b1 * a.nb2;
+  s.ao = b1 * a.sa1 + b2 * a.sa2;
+  s.bo = b1 * a.sb1 + b2 * a.sb2;
+  s.co = b1 * a.sc1 + b2 * a.sc2;
+  s.eo = b1 * a.se1 + b2 * a.se2;
+}
 #define GB_SLOTS VH_GEMMB_SLOTS  // workspace slots per workgroup: stream-K first / last piece
 
 // Operands need only 4-byte alignment: a 128-bit buffer load at a 4-byte-aligned
@@ -197,7 +212,7 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
       if (kt0 != 0 || kt1 != sp.nk) s.slot = p == 0 ? 0 : 1;
     }
     int tm, tn;
-    gb_tile_of(u, a.tiles_m, a.tiles_n, tm, tn);
+    gb_locate(a, u, tm, tn, s);
     s.m0 = tm * GB_TM;
     s.n0 = tn * BN;
     s.kt0 = kt0;
@@ -213,21 +228,24 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
   // Buffer resources of k tile kt of the tile at rows m0 (A) / columns n0 (B):
   // origin and the bytes from there to the operand's last element; a
   // resource of no bytes where the k tile stream has ended (reads give 0).
-  auto rsrc_a = [&](int64_t m0, int64_t kt, bool valid) -> __amdgpu_buffer_rsrc_t {
-    const int64_t k0 = kt * GB_TK;
+  // (Per batch: the bound is that batch's last element, so k past K reads 0.)
+  auto rsrc_a = [&](const GbSeg& sg, int64_t kt, bool valid) -> __amdgpu_buffer_rsrc_t {
+    const int64_t k0 = kt * GB_TK, m0 = sg.m0;
     if (!valid) return gb_rsrc(a.A, 0);
+    const float* A = a.A + sg.ao;
     if constexpr (A_KC)
-      return gb_rsrc(a.A + m0 * a.lda + k0, ((a.M - 1 - m0) * a.lda + a.K - k0) * 4);
+      return gb_rsrc(A + m0 * a.lda + k0, ((a.M - 1 - m0) * a.lda + a.K - k0) * 4);
     else
-      return gb_rsrc(a.A + k0 * a.lda + m0, ((a.K - 1 - k0) * a.lda + a.M - m0) * 4);
+      return gb_rsrc(A + k0 * a.lda + m0, ((a.K - 1 - k0) * a.lda + a.M - m0) * 4);
   };
-  auto rsrc_b = [&](int64_t n0, int64_t kt, bool valid) -> __amdgpu_buffer_rsrc_t {
-    const int64_t k0 = kt * GB_TK;
+  auto rsrc_b = [&](const GbSeg& sg, int64_t kt, bool valid) -> __amdgpu_buffer_rsrc_t {
+    const int64_t k0 = kt * GB_TK, n0 = sg.n0;
     if (!valid) return gb_rsrc(a.B, 0);
+    const float* B = a.B + sg.bo;
     if constexpr (B_KC)
-      return gb_rsrc(a.B + n0 * a.ldb + k0, ((a.N - 1 - n0) * a.ldb + a.K - k0) * 4);
+      return gb_rsrc(B + n0 * a.ldb + k0, ((a.N - 1 - n0) * a.ldb + a.K - k0) * 4);
     else
-      return gb_rsrc(a.B + k0 * a.ldb + n0, ((a.K - 1 - k0) * a.ldb + a.N - n0) * 4);
+      return gb_rsrc(B + k0 * a.ldb + n0, ((a.K - 1 - k0) * a.ldb + a.N - n0) * 4);
   };
   // Staging registers: one k tile's pieces of A and B.
   vh_f4 ga[OA::PER], gb[OB::PER];
@@ -267,10 +285,10 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
     }
   };
   GbSeg cur = lseg;
-  gload(rsrc_a(lseg.m0, lkt, true), rsrc_b(lseg.n0, lkt, true));
+  gload(rsrc_a(lseg, lkt, true), rsrc_b(lseg, lkt, true));
   swrite(LA0, LB0);
   advance();
-  gload(rsrc_a(lseg.m0, lkt, lv), rsrc_b(lseg.n0, lkt, lv));
+  gload(rsrc_a(lseg, lkt, lv), rsrc_b(lseg, lkt, lv));
   lds_barrier();
   vh_f32x16 acc[WM][NB];
 
@@ -438,8 +456,10 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
       return;
     }
     const bool inner = cur.m0 + GB_TM <= a.M && cur.n0 + BN <= a.N;
+    float* const Cb = a.C + cur.co;
+    const float* const Eb = a.E ? a.E + cur.eo : nullptr;
     if (inner && !a.E && !a.accumulate) {
-      float* base = a.C + (cur.m0 + lrow) * ldo + cur.n0 + lcol;
+      float* base = Cb + (cur.m0 + lrow) * ldo + cur.n0 + lcol;
 #pragma unroll
       for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -454,8 +474,8 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
       // Whole tile inside C: v = alpha acc (+ E) (+ old C), in gm_finish's
       // order, without bounds tests; an addend over the columns only (a
       // bias, E stride 0 along m) is read once per column.
-      float* base = a.C + (cur.m0 + lrow) * ldo + cur.n0 + lcol;
-      const float* E = a.E;
+      float* base = Cb + (cur.m0 + lrow) * ldo + cur.n0 + lcol;
+      const float* E = Eb;
       const bool ecol = E && a.sem == 0;
       float eb[NB];
 #pragma unroll
@@ -489,8 +509,8 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
           const int rl = 32 * i + 8 * (r >> 2) + (r & 3);
           const int64_t m = cur.m0 + lrow + rl;
           if (m < a.M && n < a.N) {
-            float* cp = a.C + m * ldo + n;
-            *cp = gm_finish(a, a.E, false, acc[i][jj][r], m, n, a.accumulate ? *cp : 0.0f);
+            float* cp = Cb + m * ldo + n;
+            *cp = gm_finish(a, Eb, false, acc[i][jj][r], m, n, a.accumulate ? *cp : 0.0f);
           }
         }
       }
@@ -505,7 +525,7 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
       for (int jj = 0; jj < NB; ++jj) acc[i][jj] = vh_f32x16{};
     for (int kt = cur.kt0; kt < cur.kt1; ++kt) {
       advance();
-      kstep(rsrc_a(lseg.m0, lkt, lv), rsrc_b(lseg.n0, lkt, lv), s ? LA1 : LA0, s ? LB1 : LB0, s ? LA0 : LA1,
+      kstep(rsrc_a(lseg, lkt, lv), rsrc_b(lseg, lkt, lv), s ? LA1 : LA0, s ? LB1 : LB0, s ? LA0 : LA1,
             s ? LB0 : LB1);
       s ^= 1;
     }
@@ -545,13 +565,19 @@ VH_DEV void gemm_big_fix_impl(const GemmArgs& a) {
   }
   if (glo == ghi) return;  // one workgroup covered the whole tile and stored it
   int tm, tn;
-  gb_tile_of(sp.full * G + t, a.tiles_m, a.tiles_n, tm, tn);
+  GbSeg sg;
+  gb_locate(a, sp.full * G + t, tm, tn, sg);
+  float* const Cb = a.C + sg.co;
+  const float* const Eb = a.E ? a.E + sg.eo : nullptr;
   const int64_t m0 = (int64_t)tm * GB_TM, n0 = (int64_t)tn * BN;
   constexpr int Q = BN / 4;  // 128-bit pieces per row
   for (int f = threadIdx.x; f < 16 * Q; f += 256) {
     const int rl = rows0 + f / Q, cl = (f % Q) * 4;
     vh_f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int gg = glo; gg <= ghi; ++gg) {
+      // With fewer k tiles than workgroups (W < G) some runs are empty and
+      // wrote no piece: skip them (their slots hold an earlier call's data).
+      if (sp.begin(gg) == sp.end(gg)) continue;
       const int slot = sp.begin(gg) / sp.nk == t ? 0 : 1;
       const vh_f4 p = *reinterpret_cast<const vh_f4*>(a.ws + ((int64_t)gg * GB_SLOTS + slot) * GB_TM * BN + rl * BN + cl);
       v += p;
@@ -562,8 +588,8 @@ VH_DEV void gemm_big_fix_impl(const GemmArgs& a) {
     for (int e = 0; e < 4; ++e) {
       const int64_t n = n0 + cl + e;
       if (n < a.N) {
-        float* cp = a.C + m * a.ldc + n;
-        *cp = gm_finish(a, a.E, false, v[e], m, n, a.accumulate ? *cp : 0.0f);
+        float* cp = Cb + m * a.ldc + n;
+        *cp = gm_finish(a, Eb, false, v[e], m, n, a.accumulate ? *cp : 0.0f);
       }
     }
   }

@@ -1303,19 +1303,24 @@ thread_local int g_gemm_path = VH_GEMM_PATH_NONE;
 // tiled kernel adds the rest (alpha times the tail product) into C.
 int gemm_big(const vh_gemm_desc* d, bool akc, bool bkc, int64_t lda, int64_t ldb, hipStream_t s, bool* taken) {
   *taken = false;
-  const int64_t M = d->M, N = d->N, K = d->K;
-  if (d->batch[0] * d->batch[1] != 1 || d->causal != VH_GEMM_DENSE || K <= 0) return VH_OK;
-  if (M < VH_GEMMB_TM || N < VH_GEMMB_TN || (double)M * (double)N * (double)K < 67108864.0) return VH_OK;
+  const int64_t M = d->M, N = d->N, K = d->K, nb = d->batch[0] * d->batch[1];
+  if (d->causal != VH_GEMM_DENSE || K <= 0) return VH_OK;
+  // Batched products need k loops long enough for a persistent walk (short-K
+  // batched products, such as attention's scores, have their own kernel).
+  if (nb > 1 && K < 512) return VH_OK;
+  if (M < VH_GEMMB_TM || N < VH_GEMMB_TN || (double)M * (double)N * (double)K * (double)nb < 67108864.0)
+    return VH_OK;
   if (reinterpret_cast<uintptr_t>(d->a) % 4 != 0 || reinterpret_cast<uintptr_t>(d->b) % 4 != 0) return VH_OK;
   if (lda >= (int64_t(1) << 22) || ldb >= (int64_t(1) << 22) || K >= (int64_t(1) << 26)) return VH_OK;
   const int G = std::max(8, g_rt.cu_count / 8 * 8);
   const int64_t K32 = (akc || bkc) ? K / 32 * 32 : K;
   if (K32 == 0) return VH_OK;
   const int64_t tiles_m = cdiv(M, VH_GEMMB_TM), tiles_n = cdiv(N, VH_GEMMB_TN);
-  if (tiles_m * tiles_n >= INT32_MAX) return VH_OK;
-  const int64_t tiles = tiles_m * tiles_n, rem = tiles % G;
+  if (tiles_m * tiles_n * nb >= INT32_MAX) return VH_OK;
+  const int64_t tiles = tiles_m * tiles_n * nb, rem = tiles % G;
   GemmArgs g = gemm_args(d, lda, ldb, tiles_m, tiles_n);
   g.K = K32;
+  g.nbat = nb;
   void* ws = nullptr;
   if (rem > 0) {
     VH_TRY(g_arena.alloc((size_t)G * VH_GEMMB_SLOTS * VH_GEMMB_TM * VH_GEMMB_TN * sizeof(float), s, &ws));
