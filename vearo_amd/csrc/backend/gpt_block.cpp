@@ -222,7 +222,7 @@ struct vb_gpt {
     // columns of dlogits meet the zero rows after the weight.
     // dx = dlogits W reads W through a transposed copy: both operands are then
     // k-contiguous, which the large-product kernel runs faster than W's
-    // row-contiguous form (the 154 MB copy, ~90 us, costs less than that saves).
+    // row-contiguous form (8.6 against 8.8 ms; the 154 MB copy costs ~90 us).
     {
       const vh_layout wl{2, 0, {D, Vp}, {1, D}};
       VB(vh_strided_copy(p(20), &wl, wT, nullptr));
@@ -244,10 +244,10 @@ struct vb_gpt {
       VB(vh_gemm(&d, nullptr));
     }
     // dW = dlogits^T lnf runs as its transpose dW^T = lnf^T dlogits from a
-    // transposed copy of lnf (k-contiguous A, prefetched) into wT's buffer,
-    // then one transposing copy into the gradient: two copies of ~20 and ~90
-    // us against the slower row-contiguous product they replace. Each element
-    // is the same sum over the R rows.
+    // transposed copy of lnf (k-contiguous A) into wT's buffer, then one
+    // transposing copy into the gradient: two copies of ~30 and ~75 us against
+    // the slower row-contiguous product they replace (8.85 against 9.09 ms).
+    // Each element is the same sum over the R rows.
     {
       const vh_layout ll{2, 0, {D, R}, {1, D}};
       VB(vh_strided_copy(lnf, &ll, lnfT, nullptr));
