@@ -1823,9 +1823,12 @@ int vh_attention_mask_is_causal(const float* q, const vh_layout* ql, const float
   const uint32_t kInf = 0x7f800000u;
   if (h[2] >= kInf || h[3] >= kInf || h[4] >= kInf || (g && h[5] >= kInf)) return VH_OK;  // NaN or inf
   // Largest |score| the product can form: |s| <= scale * Dk * max|q| * max|k|,
-  // widened for the f32 accumulation (relative Dk * 2^-24, under 1e-5 here).
+  // widened by twice the f32 bound for a sum of Dk products in any order
+  // (gamma = Dk u / (1 - Dk u), u = 2^-24) and the scaling's rounding.
+  const double u = 0x1p-24, nu = (double)sh.Dk * u;
+  if (nu >= 0.25) return VH_OK;
   const double scale = (double)(1.0f / std::sqrt((float)sh.Dk));
-  const double smax = scale * (double)sh.Dk * fl(h[2]) * fl(h[3]) * (1.0 + 1e-5) + 1e-30;
+  const double smax = scale * (double)sh.Dk * fl(h[2]) * fl(h[3]) * (1.0 + 2.0 * nu / (1.0 - nu)) * (1.0 + 2.0 * u);
   // A masked x = fl(s + m) less the row max (>= the diagonal's score, >= -smax)
   // is at most 2 smax - |m| plus two roundings of ~|m| 2^-24 each; expf of
   // anything below -104 is exactly 0 in f32, so ask for -256 with margin.
