@@ -102,9 +102,9 @@ def launcher_kernel_names():
             names |= {f"vh_ln_fwd_t{t}_n{v}_v{vw}_r2", f"vh_ln_fwd_t{t}_n{v}_v{vw}_r4",
                       f"vh_sm_fwd_t{t}_n{v}_v{vw}_r2", f"vh_sm_bwd_t{t}_n{v}_v{vw}_r2"}
         for v in (1, 2, 3, 4):
-            names.add(f"vh_ln_bwd_t64_n{v}_v{vw}_b1024")
+            names.add(f"vh_ln_bwd_t64_n{v}_v{vw}_b512")
             if vw == 4:
-                names |= {f"vh_ln_bwd_t64_n{v}_v4_b1024_f", f"vh_ln_fwd_t64_n{v}_v4_r4_f"}
+                names |= {f"vh_ln_bwd_t64_n{v}_v4_b512_f", f"vh_ln_fwd_t64_n{v}_v4_r4_f"}
         for v in nv:
             names.add(f"vh_gelu_bias_fwd_n{v}_v{vw}")
         names.add(f"vh_gelu_bias_bwd_tile_v{vw}")

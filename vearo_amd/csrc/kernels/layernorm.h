@@ -104,7 +104,7 @@ VH_DEV void ln_fwd_impl(const LnFwdArgs& a) {
 // reference's; the division by C is div_rn (bit-identical, 3 instructions).
 // dgamma/dbeta: each lane accumulates its columns over its team's rows; the G
 // teams of a workgroup fold through LDS in a fixed order -- FULL forms (C a
-// compile-time TEAM*NV*VW, G = 16) in one level (every team parks its partial
+// compile-time TEAM*NV*VW, G = 8) in one level (every team parks its partial
 // row, one barrier, each thread sums one 4-column unit over the 16 slots in
 // team order), the others in a fixed pairwise tree in dynamic LDS of
 // (G/2)*2*C floats -- and one partial row per workgroup goes to scratch for

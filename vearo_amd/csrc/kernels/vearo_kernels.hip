@@ -60,16 +60,16 @@ K_LN_FWD_F(64, 1) K_LN_FWD_F(64, 2) K_LN_FWD_F(64, 3) K_LN_FWD_F(64, 4)
 #define BSLIT_1024 1024
 #define K_LN_BWD_X(T, N, VW, BS) K_LN_BWD_B(T, N, VW, BS)  // expands BS before pasting
 #define K_LN_BWD(T, N, VW) K_LN_BWD_X(T, N, VW, BSLIT_##T)
-#define K_LN_BWD_1024(T, N, VW) K_LN_BWD_B(T, N, VW, 1024)
+#define K_LN_BWD_512(T, N, VW) K_LN_BWD_B(T, N, VW, 512)
 ROW_CFG_SMALL(K_LN_BWD, 1)
 ROW_CFG_SMALL(K_LN_BWD, 4)
-// Wave teams with rows up to 1024 units: 16 row-groups per workgroup.
-K_LN_BWD_1024(64, 1, 1) K_LN_BWD_1024(64, 2, 1) K_LN_BWD_1024(64, 3, 1) K_LN_BWD_1024(64, 4, 1)
-K_LN_BWD_1024(64, 1, 4) K_LN_BWD_1024(64, 2, 4) K_LN_BWD_1024(64, 3, 4) K_LN_BWD_1024(64, 4, 4)
+// Wave teams with rows up to 1024 units: 8 row-groups per workgroup.
+K_LN_BWD_512(64, 1, 1) K_LN_BWD_512(64, 2, 1) K_LN_BWD_512(64, 3, 1) K_LN_BWD_512(64, 4, 1)
+K_LN_BWD_512(64, 1, 4) K_LN_BWD_512(64, 2, 4) K_LN_BWD_512(64, 3, 4) K_LN_BWD_512(64, 4, 4)
 #define K_LN_BWD_F(T, N)                                                          \
-  extern "C" __global__ void __launch_bounds__(1024) vh_ln_bwd_t##T##_n##N##_v4_b1024_f(LnBwdArgs a) { \
+  extern "C" __global__ void __launch_bounds__(512) vh_ln_bwd_t##T##_n##N##_v4_b512_f(LnBwdArgs a) { \
     extern __shared__ float dyn_lds[];                                            \
-    ln_bwd_impl<T, N, 4, 1024, true>(a, dyn_lds);                                 \
+    ln_bwd_impl<T, N, 4, 512, true>(a, dyn_lds);                                  \
   }
 K_LN_BWD_F(64, 1) K_LN_BWD_F(64, 2) K_LN_BWD_F(64, 3) K_LN_BWD_F(64, 4)
 
