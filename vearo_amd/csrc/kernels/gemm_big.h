@@ -470,10 +470,56 @@ VH_DEV void gemm_big_impl(const GemmArgs& a) {
         }
       return;
     }
+    if (inner && (!Eb || a.sem == 0)) {
+      // Whole tile inside C with at most a per-column addend (a bias, E
+      // stride 0 along m, read once per column): v = alpha acc (+ bias)
+      // (+ old C), in gm_finish's order, no bounds tests. The stores may
+      // alias the old-C reads as far as the compiler knows, so it keeps
+      // each read behind the stores before it: the reads go out 8 rows x
+      // NB columns at a time, ahead of their stores, so a wave waits on
+      // memory 2 WM times, not once per element.
+      float* base = Cb + (cur.m0 + lrow) * ldo + cur.n0 + lcol;
+      float eb[NB];
+#pragma unroll
+      for (int jj = 0; jj < NB; ++jj) eb[jj] = Eb ? Eb[(cur.n0 + lcol + 32 * jj) * a.sen] : 0.0f;
+      auto tile = [&](auto has_bias, auto acc_c) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+          for (int r0 = 0; r0 < 16; r0 += 8) {
+            float old[8][NB];
+            if constexpr (decltype(acc_c)::value) {
+#pragma unroll
+              for (int r = 0; r < 8; ++r)
+#pragma unroll
+                for (int jj = 0; jj < NB; ++jj)
+                  old[r][jj] = base[(32 * i + 8 * ((r0 + r) >> 2) + ((r0 + r) & 3)) * ldo + 32 * jj];
+            }
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+              float* row = base + (32 * i + 8 * ((r0 + r) >> 2) + ((r0 + r) & 3)) * ldo;
+#pragma unroll
+              for (int jj = 0; jj < NB; ++jj) {
+                float v = acc[i][jj][r0 + r] * a.alpha;
+                if constexpr (decltype(has_bias)::value) v = v + eb[jj];
+                if constexpr (decltype(acc_c)::value) v = old[r][jj] + v;
+                row[32 * jj] = v;
+              }
+            }
+          }
+      };
+      using T = std::true_type;
+      using F = std::false_type;
+      if (Eb) {
+        if (a.accumulate) tile(T{}, T{}); else tile(T{}, F{});
+      } else {
+        tile(F{}, T{});  // accumulate (the plain store returned above)
+      }
+      return;
+    }
     if (inner) {
-      // Whole tile inside C: v = alpha acc (+ E) (+ old C), in gm_finish's
-      // order, without bounds tests; an addend over the columns only (a
-      // bias, E stride 0 along m) is read once per column.
+      // Whole tile inside C with a full addend E[m, n]: v = alpha acc + E
+      // (+ old C), in gm_finish's order, without bounds tests.
       float* base = Cb + (cur.m0 + lrow) * ldo + cur.n0 + lcol;
       const float* E = Eb;
       const bool ecol = E && a.sem == 0;
