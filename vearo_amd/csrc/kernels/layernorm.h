@@ -289,17 +289,21 @@ VH_DEV void ln_bwd_impl(const LnBwdArgs& a, float* lds) {
   }
 }
 
-// Stage 2: out_c[col] = sum over p of part[p][c][col]. Wave w of the 16 owns the
-// contiguous partial range [w*per, (w+1)*per) and sums it in order with up to 16
-// loads in flight; the 16 wave sums are then added in wave order, so the result
-// is the partials summed in index order with a fixed grouping (deterministic).
-// Grid: (ceil(C/64), ncomp), 1024 threads.
+// Stage 2: out_c[col] = sum over p of part[p][c][col]. A workgroup owns CW =
+// VH_COLR_COLS consecutive columns; thread group w of the 16 owns the contiguous
+// partial range [w*per, (w+1)*per) and sums it in order with up to 16 loads in
+// flight; the 16 range sums are then added in range order, so the result is the
+// partials summed in index order with a fixed grouping (deterministic). Narrow
+// workgroups spread the 1.5 MiB of LayerNorm partials over 96 CUs instead of
+// 24 (LayerNorm backward + reduce 32.2 -> 31.6 us, same bits).
+// Grid: (ceil(C/CW), ncomp), CW * 16 threads.
 VH_DEV void col_reduce_impl(const ColReduceArgs& a) {
-  __shared__ float red[16][64];
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  constexpr int CW = VH_COLR_COLS;
+  __shared__ float red[16][CW];
+  const int lane = threadIdx.x % CW;
+  const int w = threadIdx.x / CW;
   const int comp = blockIdx.y;
-  const int col = blockIdx.x * 64 + lane;
+  const int col = blockIdx.x * CW + lane;
   const int per = (a.P + 15) / 16;
   const int p0 = w * per;
   const int p1 = min(p0 + per, a.P);

@@ -103,7 +103,7 @@ K_SM_BWD(128, 2, 4)
 ROW_CFG_MULTI(K_SM_BWD_M, 1)
 ROW_CFG_MULTI(K_SM_BWD_M, 4)
 
-extern "C" __global__ void __launch_bounds__(1024) vh_col_reduce(ColReduceArgs a) {
+extern "C" __global__ void __launch_bounds__(VH_COLR_COLS * 16) vh_col_reduce(ColReduceArgs a) {
   col_reduce_impl(a);
 }
 

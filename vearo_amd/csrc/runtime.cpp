@@ -598,7 +598,7 @@ int ln_bwd_launch(const LnBwdPlan& p, const float* x, const float* w, const floa
   LnBwdArgs a{x, w, dy, dx, part, rows, (int32_t)C, eps};
   VH_TRY(launch(bwd_kernel("vh_ln_bwd", p.c), (unsigned)p.G, 1, bs, shmem, s, a));
   ColReduceArgs r{part, dw, db, (int32_t)p.G, (int32_t)C, 2};
-  return launch("vh_col_reduce", (unsigned)cdiv(C, 64), 2, 1024, 0, s, r);
+  return launch("vh_col_reduce", (unsigned)cdiv(C, VH_COLR_COLS), 2, VH_COLR_COLS * 16, 0, s, r);
 }
 
 // Argument checks shared by both entries; *done is set when nothing is left
@@ -737,7 +737,7 @@ int vh_gelu_bias_bwd(const float* x, const float* bias, const float* dy, float* 
   VH_TRY(launch("vh_gelu_bias_bwd_tile_v" + std::to_string(vw), (unsigned)cdiv(C / vw, 64), (unsigned)G, 256,
                 0, s, a));
   ColReduceArgs r{static_cast<float*>(sc.p), dbias, nullptr, (int32_t)G, (int32_t)C, 1};
-  return launch("vh_col_reduce", (unsigned)cdiv(C, 64), 1, 1024, 0, s, r);
+  return launch("vh_col_reduce", (unsigned)cdiv(C, VH_COLR_COLS), 1, VH_COLR_COLS * 16, 0, s, r);
 }
 
 // --------------------------------------------------------------- softmax --
@@ -1202,7 +1202,7 @@ int vh_sum_rows(const float* x, int64_t rows, int64_t C, float* out, void* scrat
   ColPartialArgs a{x, part, rows, rpb, (int32_t)C};
   VH_TRY(launch("vh_col_partial", (unsigned)G, (unsigned)cdiv(C, 256), 256, 0, s, a));
   ColReduceArgs r{part, out, nullptr, (int32_t)G, (int32_t)C, 1};
-  return launch("vh_col_reduce", (unsigned)cdiv(C, 64), 1, 1024, 0, s, r);
+  return launch("vh_col_reduce", (unsigned)cdiv(C, VH_COLR_COLS), 1, VH_COLR_COLS * 16, 0, s, r);
 }
 
 // ------------------------------------------------------------------ gemm --

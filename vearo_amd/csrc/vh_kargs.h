@@ -41,6 +41,9 @@ struct LnBwdArgs {
 };
 
 // Column reduction of [P][2][C] partials into dw[C], db[C] (fixed order).
+// Column reduce launch shape: VH_COLR_COLS columns per workgroup, 16 partial
+// ranges per column, so VH_COLR_COLS * 16 threads.
+#define VH_COLR_COLS 16
 struct ColReduceArgs {
   const float* part;
   float* out0;  // component 0 (dgamma / dbias)
