@@ -620,13 +620,25 @@ VH_DEV void gemm_big_fix_impl(const GemmArgs& a) {
   for (int f = threadIdx.x; f < 16 * Q; f += 256) {
     const int rl = rows0 + f / Q, cl = (f % Q) * 4;
     vh_f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int gg = glo; gg <= ghi; ++gg) {
-      // With fewer k tiles than workgroups (W < G) some runs are empty and
-      // wrote no piece: skip them (their slots hold an earlier call's data).
-      if (sp.begin(gg) == sp.end(gg)) continue;
-      const int slot = sp.begin(gg) / sp.nk == t ? 0 : 1;
-      const vh_f4 p = *reinterpret_cast<const vh_f4*>(a.ws + ((int64_t)gg * GB_SLOTS + slot) * GB_TM * BN + rl * BN + cl);
-      v += p;
+    // The pieces of workgroups glo..ghi, four at a time: the four loads go
+    // out together, then the pieces are added in workgroup order. Indices
+    // past ghi are clamped to ghi and not added; with fewer k tiles than
+    // workgroups (W < G) some runs are empty and wrote no piece: their slots
+    // (in bounds, holding an earlier call's data) are read but not added.
+    for (int g0 = glo; g0 <= ghi; g0 += 4) {
+      vh_f4 p[4];
+      bool used[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int gg = g0 + j <= ghi ? g0 + j : ghi;
+        const int b = sp.begin(gg);
+        used[j] = g0 + j <= ghi && b != sp.end(gg);
+        const int slot = b / sp.nk == t ? 0 : 1;
+        p[j] = *reinterpret_cast<const vh_f4*>(a.ws + ((int64_t)gg * GB_SLOTS + slot) * GB_TM * BN + rl * BN + cl);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (used[j]) v += p[j];
     }
     const int64_t m = m0 + rl;
     if (m >= a.M) continue;
