@@ -164,3 +164,13 @@ def test_gemm_desc_layout_matches_header(tmp_path):
                                           text=True).stdout.split()]
     want = [ctypes.sizeof(_abi.VhGemmDesc)] + [getattr(_abi.VhGemmDesc, f).offset for f in fields]
     assert got == want
+
+
+def test_hipblaslt_is_not_a_link_dependency():
+    # The hipBLASLt A/B engine opens the library at its first use; the
+    # product library itself must load where hipBLASLt is not installed.
+    import subprocess
+
+    out = subprocess.run(["readelf", "-d", LIB], capture_output=True, text=True, check=True).stdout
+    needed = re.findall(r"\(NEEDED\)\s+Shared library: \[([^\]]+)\]", out)
+    assert needed and not any("hipblas" in n for n in needed), needed

@@ -143,6 +143,27 @@ def test_matmul_zero_k_and_errors(vh):
                                       C.ptr, None))
 
 
+def test_matmul_operands_broadcast_along_k(vh):
+    """Operands whose k dim has stride 0 (a [M, 1] column and a [1, N] row
+    broadcast to [M, K] and [K, N]) at a size the large-product kernel would
+    take, with K % 32 != 0: the last k tile must not read the broadcast
+    values again past K (each would add 32 - K % 32 extra products), so the
+    partial tile goes to the kernel that tests k < K."""
+    r = np.random.default_rng(31)
+    M, N = 1024, 1024
+    for K in (100, 1000):
+        acol = r.standard_normal(M, dtype=np.float32)
+        brow = (r.standard_normal(N) * 0.05).astype(np.float32)
+        A, B, C = dev(vh, acol), dev(vh, brow), out(vh, (M, N))
+        al = vh.layout((M, K), (1, 0))
+        bl = vh.layout((K, N), (0, 1))
+        vh.check(vh.lib.vh_matmul(A.ptr, ctypes.byref(al), B.ptr, ctypes.byref(bl), C.ptr, None))
+        a = np.ascontiguousarray(np.broadcast_to(acol[:, None], (M, K)))
+        b = np.ascontiguousarray(np.broadcast_to(brow[None, :], (K, N)))
+        assert_parity(fetch(vh, C, (M, N)), O.matmul(a, b), a.astype(np.float64) @ b.astype(np.float64),
+                      name=f"stride-0 k, K={K}")
+
+
 def gemm_desc(vh, M, N, K, a, a_sm, a_sk, b, b_sk, b_sn, c, c_sm, **kw):
     d = vh.VhGemmDesc()
     d.M, d.N, d.K = M, N, K

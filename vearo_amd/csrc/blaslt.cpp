@@ -1,14 +1,19 @@
-// blaslt.cpp -- plain f32 products through hipBLASLt.
+// blaslt.cpp -- the A/B engine: plain f32 products through hipBLASLt.
 //
-// A product with no batch and no causal range, whose addend E is absent or a
-// bias over the output columns, with or without accumulation into C (the
-// lm_head products, the Linear forwards, every weight and input gradient of
-// the block step) is a library GEMM: D = alpha A B (+ C) (+ bias), the bias
-// through hipBLASLt's bias epilogue. Its gfx950 kernels (128x128x64 macro
-// tiles, stream-K) run these shapes faster than the hand-written kernel in
-// kernels/gemm.h, which keeps every product they do not cover (strided
-// batches, causal ranges, other addends). Compute type HIPBLAS_COMPUTE_32F:
-// f32 products and sums, no reduced-precision path.
+// The default engine never comes here: every product runs on this library's
+// own kernels (kernels/gemm_big.h, kernels/gemm.h). A caller that sets
+// vh_gemm_desc.engine = VH_GEMM_ENGINE_LIBRARY (or vb_gpt_set_gemm_engine)
+// hands the products the library takes -- no batch, no causal range, an
+// addend E that is absent or a bias over the output columns, with or without
+// accumulation into C -- to hipBLASLt instead, so its kernels can be timed
+// beside the own ones on the same step: D = alpha A B (+ C) (+ bias), the
+// bias through hipBLASLt's bias epilogue, compute type HIPBLAS_COMPUTE_32F
+// (f32 products and sums). Anything it does not take runs on the own kernels.
+//
+// libhipblaslt.so.1 is not a link-time dependency: it is opened with dlopen
+// on the first library-engine call, so a deployment that never asks for the
+// A/B engine does not need it installed. Without it that call fails with
+// VH_ERR_HIP and a message naming the library.
 //
 // hipBLASLt is column-major: the row-major C[M, N] = A[M, K] B[K, N] is issued
 // as the column-major C^T[N, M] = B^T[N, K] A^T[K, M], each operand transposed
@@ -17,10 +22,13 @@
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <dlfcn.h>
+
 #include <map>
 #include <mutex>
 #include <string>
 #include <tuple>
+#include <type_traits>
 
 #include "../../include/vearo_hip.h"
 #include "rt_internal.h"
@@ -30,6 +38,24 @@ namespace {
 using vh_rt::fail;
 
 constexpr size_t kWorkspace = size_t(64) << 20;  // bytes the algorithms may use
+
+// The hipBLASLt entry points this file calls, resolved from the library at
+// its first use (the header supplies only their types).
+struct Api {
+  void* so = nullptr;
+  decltype(&hipblasLtCreate) Create = nullptr;
+  decltype(&hipblasLtDestroy) Destroy = nullptr;
+  decltype(&hipblasLtMatmulDescCreate) MatmulDescCreate = nullptr;
+  decltype(&hipblasLtMatmulDescDestroy) MatmulDescDestroy = nullptr;
+  decltype(&hipblasLtMatmulDescSetAttribute) MatmulDescSetAttribute = nullptr;
+  decltype(&hipblasLtMatrixLayoutCreate) MatrixLayoutCreate = nullptr;
+  decltype(&hipblasLtMatrixLayoutDestroy) MatrixLayoutDestroy = nullptr;
+  decltype(&hipblasLtMatmulPreferenceCreate) MatmulPreferenceCreate = nullptr;
+  decltype(&hipblasLtMatmulPreferenceDestroy) MatmulPreferenceDestroy = nullptr;
+  decltype(&hipblasLtMatmulPreferenceSetAttribute) MatmulPreferenceSetAttribute = nullptr;
+  decltype(&hipblasLtMatmulAlgoGetHeuristic) MatmulAlgoGetHeuristic = nullptr;
+  decltype(&hipblasLtMatmul) Matmul = nullptr;
+};
 
 struct Plan {
   hipblasLtMatmulDesc_t op = nullptr;
@@ -43,6 +69,7 @@ using Key = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int
 
 struct Lib {
   std::mutex mu;
+  Api api;
   hipblasLtHandle_t handle = nullptr;
   // One workspace per stream: products on different streams may overlap, and
   // the work in one stream is ordered, so each stream reuses its own.
@@ -55,6 +82,45 @@ int status(hipblasStatus_t st, const char* what) {
   return fail(VH_ERR_HIP, std::string("hipBLASLt ") + what + " failed: status " + std::to_string((int)st));
 }
 
+// Opens libhipblaslt.so.1 and resolves every entry point (once; the caller
+// holds g_lib.mu). A missing library or symbol is an error, not a fallback:
+// the caller asked for this engine by name.
+int load_api() {
+  Api& a = g_lib.api;
+  if (a.so) return VH_OK;
+  void* so = dlopen("libhipblaslt.so.1", RTLD_NOW | RTLD_LOCAL);
+  if (!so) so = dlopen("libhipblaslt.so", RTLD_NOW | RTLD_LOCAL);
+  if (!so) {
+    const char* e = dlerror();
+    return fail(VH_ERR_HIP, std::string("the hipBLASLt A/B engine needs libhipblaslt.so.1: ") + (e ? e : "not found"));
+  }
+  Api t;
+  t.so = so;
+  bool ok = true;
+  auto sym = [&](auto& fp, const char* name) {
+    fp = reinterpret_cast<std::remove_reference_t<decltype(fp)>>(dlsym(so, name));
+    ok = ok && fp != nullptr;
+  };
+  sym(t.Create, "hipblasLtCreate");
+  sym(t.Destroy, "hipblasLtDestroy");
+  sym(t.MatmulDescCreate, "hipblasLtMatmulDescCreate");
+  sym(t.MatmulDescDestroy, "hipblasLtMatmulDescDestroy");
+  sym(t.MatmulDescSetAttribute, "hipblasLtMatmulDescSetAttribute");
+  sym(t.MatrixLayoutCreate, "hipblasLtMatrixLayoutCreate");
+  sym(t.MatrixLayoutDestroy, "hipblasLtMatrixLayoutDestroy");
+  sym(t.MatmulPreferenceCreate, "hipblasLtMatmulPreferenceCreate");
+  sym(t.MatmulPreferenceDestroy, "hipblasLtMatmulPreferenceDestroy");
+  sym(t.MatmulPreferenceSetAttribute, "hipblasLtMatmulPreferenceSetAttribute");
+  sym(t.MatmulAlgoGetHeuristic, "hipblasLtMatmulAlgoGetHeuristic");
+  sym(t.Matmul, "hipblasLtMatmul");
+  if (!ok) {
+    dlclose(so);
+    return fail(VH_ERR_HIP, "libhipblaslt.so.1 lacks an entry point the A/B engine calls");
+  }
+  a = t;
+  return VH_OK;
+}
+
 #define LT(expr, what)                       \
   do {                                       \
     int rc_ = status((expr), what);          \
@@ -62,10 +128,10 @@ int status(hipblasStatus_t st, const char* what) {
   } while (0)
 
 void destroy(Plan& p) {
-  if (p.op) hipblasLtMatmulDescDestroy(p.op);
-  if (p.lx) hipblasLtMatrixLayoutDestroy(p.lx);
-  if (p.ly) hipblasLtMatrixLayoutDestroy(p.ly);
-  if (p.lc) hipblasLtMatrixLayoutDestroy(p.lc);
+  if (p.op) g_lib.api.MatmulDescDestroy(p.op);
+  if (p.lx) g_lib.api.MatrixLayoutDestroy(p.lx);
+  if (p.ly) g_lib.api.MatrixLayoutDestroy(p.ly);
+  if (p.lc) g_lib.api.MatrixLayoutDestroy(p.lc);
   p = Plan{};
 }
 
@@ -80,28 +146,28 @@ int make_plan(const Key& k, Plan* out) {
   const hipblasOperation_t opy = ty ? HIPBLAS_OP_T : HIPBLAS_OP_N;
   hipblasLtMatmulPreference_t pref = nullptr;
   auto build = [&]() -> int {
-    LT(hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F), "MatmulDescCreate");
-    LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &opx, sizeof(opx)), "set TRANSA");
-    LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &opy, sizeof(opy)), "set TRANSB");
+    LT(g_lib.api.MatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F), "MatmulDescCreate");
+    LT(g_lib.api.MatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &opx, sizeof(opx)), "set TRANSA");
+    LT(g_lib.api.MatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &opy, sizeof(opy)), "set TRANSB");
     if (bias) {
       // A bias of length N (D's rows in the column-major view) on every column.
       const uint32_t epi = HIPBLASLT_EPILOGUE_BIAS;
       const int32_t bt = HIP_R_32F;
-      LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi)), "set EPILOGUE");
-      LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt)),
+      LT(g_lib.api.MatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi)), "set EPILOGUE");
+      LT(g_lib.api.MatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt)),
          "set BIAS_DATA_TYPE");
     }
-    LT(hipblasLtMatrixLayoutCreate(&p.lx, HIP_R_32F, tx ? K : N, tx ? N : K, ldx), "layout X");
-    LT(hipblasLtMatrixLayoutCreate(&p.ly, HIP_R_32F, ty ? M : K, ty ? K : M, ldy), "layout Y");
-    LT(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc), "layout C");
-    LT(hipblasLtMatmulPreferenceCreate(&pref), "PreferenceCreate");
+    LT(g_lib.api.MatrixLayoutCreate(&p.lx, HIP_R_32F, tx ? K : N, tx ? N : K, ldx), "layout X");
+    LT(g_lib.api.MatrixLayoutCreate(&p.ly, HIP_R_32F, ty ? M : K, ty ? K : M, ldy), "layout Y");
+    LT(g_lib.api.MatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc), "layout C");
+    LT(g_lib.api.MatmulPreferenceCreate(&pref), "PreferenceCreate");
     uint64_t wsb = kWorkspace;
-    LT(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb)),
+    LT(g_lib.api.MatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb)),
        "set workspace");
     hipblasLtMatmulHeuristicResult_t res[1];
     int found = 0;
     const hipblasStatus_t st =
-        hipblasLtMatmulAlgoGetHeuristic(g_lib.handle, p.op, p.lx, p.ly, p.lc, p.lc, pref, 1, res, &found);
+        g_lib.api.MatmulAlgoGetHeuristic(g_lib.handle, p.op, p.lx, p.ly, p.lc, p.lc, pref, 1, res, &found);
     if (st == HIPBLAS_STATUS_SUCCESS && found > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS &&
         res[0].workspaceSize <= kWorkspace) {
       p.algo = res[0].algo;
@@ -110,7 +176,7 @@ int make_plan(const Key& k, Plan* out) {
     return VH_OK;
   };
   const int rc = build();
-  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+  if (pref) g_lib.api.MatmulPreferenceDestroy(pref);
   if (rc != VH_OK) {
     destroy(p);
     return rc;
@@ -136,7 +202,11 @@ int blaslt_gemm(const vh_gemm_desc* d, bool akc, bool bkc, void* stream, bool* t
   if (ldx < (tx ? K : N) || ldy < (ty ? M : K) || ldc < N) return VH_OK;  // not a layout it takes
   const hipStream_t s = stream_of(stream);
   std::lock_guard<std::mutex> lk(g_lib.mu);
-  if (!g_lib.handle) LT(hipblasLtCreate(&g_lib.handle), "Create");
+  {
+    const int rc = load_api();
+    if (rc != VH_OK) return rc;
+  }
+  if (!g_lib.handle) LT(g_lib.api.Create(&g_lib.handle), "Create");
   void*& ws = g_lib.ws[s];
   if (!ws) {
     const hipError_t e = hipMalloc(&ws, kWorkspace);
@@ -160,10 +230,10 @@ int blaslt_gemm(const vh_gemm_desc* d, bool akc, bool bkc, void* stream, bool* t
   const Plan& p = it->second;
   if (bias) {
     const void* bp = d->e;
-    LT(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bp, sizeof(bp)),
+    LT(g_lib.api.MatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bp, sizeof(bp)),
        "set BIAS_POINTER");
   }
-  LT(hipblasLtMatmul(g_lib.handle, p.op, &alpha, d->b, p.lx, d->a, p.ly, &beta, d->c, p.lc, d->c, p.lc, &p.algo,
+  LT(g_lib.api.Matmul(g_lib.handle, p.op, &alpha, d->b, p.lx, d->a, p.ly, &beta, d->c, p.lc, d->c, p.lc, &p.algo,
                      ws, kWorkspace, s),
      "Matmul");
   *taken = true;
@@ -172,11 +242,12 @@ int blaslt_gemm(const vh_gemm_desc* d, bool akc, bool bkc, void* stream, bool* t
 
 void blaslt_shutdown() {
   std::lock_guard<std::mutex> lk(g_lib.mu);
+  if (!g_lib.api.so) return;  // the library was never opened: nothing of it to release
   for (auto& kv : g_lib.plans) destroy(kv.second);
   g_lib.plans.clear();
   for (auto& kv : g_lib.ws) (void)hipFree(kv.second);
   g_lib.ws.clear();
-  if (g_lib.handle) hipblasLtDestroy(g_lib.handle);
+  if (g_lib.handle) g_lib.api.Destroy(g_lib.handle);
   g_lib.handle = nullptr;
 }
 

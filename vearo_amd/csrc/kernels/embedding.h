@@ -6,32 +6,42 @@
 // loads/stores when D % 4 == 0. ids are f32 as in the reference API.
 //
 // Backward (lib.rs:920-980): dW = zeros[V, D]; dW[tok_i] += dy[i] for i ascending.
-// No float atomics; dy is read once.
-// Sorted path (n <= 16384, V < 65535 -- every BASELINE config), three launches:
-//   1. emb_sort    : workgroup 0 sorts the n keys (token << 14 | position) by
-//                    token in LDS -- a stable LSD radix sort, two 8-bit passes,
-//                    each key's rank among equal digits taken from eight wave
-//                    ballots (no atomics) -- so positions stay ascending within
-//                    a token; then it cuts the sorted array into one segment
-//                    per distinct token and numbers the heavy tokens (more than
-//                    EMB_LIGHT hits) and their 32-hit tasks with block-wide
-//                    prefix sums. Meanwhile workgroups 1.. write dW's zeros
-//                    (the sort, ~10 us on one CU, hides under that 154 MB
-//                    write at GPT-2 size); the rows with hits are rewritten by
-//                    launches 2 and 3.
-//   2. emb_sum     : one wave per light segment adds its dy rows in ascending
-//                    position order from 0.0 -- the CPU loop's exact f32 order,
-//                    so those rows are bit-exact -- and writes the row; one
-//                    wave per (heavy task, 64-unit column slice) adds its 32
-//                    hits' rows in order into a partial row.
-//   3. emb_heavy_final (below).
-// General path (larger n or V), six launches and integer atomics on counters:
+// No float atomics; dy is read once. A token with at most EMB_LIGHT (16) hits is
+// "light": its row is the sum of its dy rows in ascending position order from
+// 0.0 -- the CPU loop's exact f32 order, so the row is bit-exact. A "heavy"
+// token's hits are cut, in position order, into tasks of EMB_CHUNK_HITS (32);
+// each task's dy rows are summed in order into a partial row, and the row is
+// the sum, in order from 0.0, of the sums of groups of EMB_GROUP (8) tasks in
+// task order (a fixed grouping: deterministic, within f32 rounding of the CPU's
+// single chain; one chain of the Zipf top id's 2292 rows would alone outlast
+// the whole backward).
+//
+// Sorted path (n <= 16384, V <= 65534 -- every BASELINE config), two launches:
+//   1. emb_sort : workgroups 0..15 each own the tokens t % 16 == k: each reads
+//                 all n ids, keeps its range's keys (t / 16 << 14 | position),
+//                 sorts them by token in LDS (a stable LSD radix sort, two 6-bit
+//                 passes; ranks among equal digits from wave ballots, no
+//                 atomics), cuts the sorted keys into one segment per token and
+//                 numbers the heavy tokens and their tasks with prefix sums
+//                 (segment records, heavy entries, task map). The other
+//                 workgroups write dW's zeros meanwhile (154 MB at GPT-2 size,
+//                 long enough to hide the sorts).
+//   2. emb_sum  : one wave per (heavy task, 64-unit column slice) first, then
+//                 one wave per segment. A light segment's wave adds its dy rows
+//                 and writes the row. A heavy task's wave writes its partial
+//                 and counts itself done; the wave that finishes a group adds
+//                 the group's partials, and the wave that finishes a row's last
+//                 group adds the group sums into dW -- with device-coherent
+//                 stores and loads and a wait for the stores before each count,
+//                 so no launch boundary or whole-L2 fence is needed between
+//                 them. The heavy waves start first, so those combines run
+//                 under the light segments' stream.
+// General path (larger n or V), five launches and integer atomics on counters:
 //   1. emb_tokens : validate/round ids; integer histogram of tokens, with the
 //                   duplicates inside each wave merged first (one atomic per
 //                   distinct token per wave, so hot tokens do not serialise)
-//   2. emb_alloc  : rows with more than EMB_LIGHT (16) hits become "heavy": an
-//                   entry and one task per 32 hits (ranked in position order),
-//                   claimed with one atomic per wave
+//   2. emb_alloc  : heavy rows get an entry and their tasks (ranked in
+//                   position order), claimed with one atomic per wave
 //   3. emb_place  : light positions drop into their row's 16 fixed slots; heavy
 //                   hits are counted per block of positions (512 or more)
 //   4. emb_rows   : the leading workgroups run heavy tasks while the rest stream
@@ -40,17 +50,9 @@
 //                   and the dy rows added in ascending position order from 0.0.
 //                   A heavy task gathers the positions of its 32 ranks (visiting
 //                   only blocks that hold them) and sums their rows in order into
-//                   a partial row, as one wave per 64-unit column slice (one unit
-//                   per lane, 16 rows in flight).
-// Both paths end with
-//   emb_heavy_final: one wave per (heavy row, column slice) adds the row's
-//                   partials: each group of 8 in task order, then the group sums
-//                   in group order, into dW (a fixed grouping of the same sum:
-//                   deterministic, within f32 rounding of the CPU's order). A
-//                   kernel of its own: an in-kernel completion tree needs
-//                   device-scope fences, and on this GPU each one writes back
-//                   and invalidates an XCD's whole L2 (measured: they made the
-//                   Zipf case 1.8x slower once the tasks were split in slices).
+//                   a partial row, as one wave per 64-unit column slice.
+//   5. emb_heavy_final: one wave per (heavy row, column slice) adds the row's
+//                   partials with the grouping above.
 // The two paths give the same bits: the same light-row order, the same 32-hit
 // tasks and the same final grouping.
 #pragma once
@@ -509,8 +511,11 @@ VH_DEV uint32_t lanes_below(unsigned long long m) {
 // into its own spos region, then cuts them into one segment per token and
 // numbers the heavy tokens (> EMB_LIGHT hits) and their 32-hit tasks, in token
 // order, with prefix sums. The other workgroups write dW's zeros (154 MB at
-// GPT-2 size, long enough to hide the sorts); rows with hits are rewritten by
-// launches 2 and 3.
+// GPT-2 size, long enough to hide the sorts); launch 2 rewrites the rows with
+// hits. (Zeroing only the rows no id names, from a row bitmap each filler
+// builds from all ids, was measured: 2.5 us faster on uniform ids, 2-4 us
+// slower on Zipf ids, whose hot ids share bitmap words and serialise the
+// atomics that set them.)
 VH_DEV void emb_sort_impl(const EmbSortArgs& a) {
   if ((int)blockIdx.x >= EMB_RANGES) {
     const int64_t stride = (int64_t)(gridDim.x - EMB_RANGES) * blockDim.x;
@@ -529,6 +534,12 @@ VH_DEV void emb_sort_impl(const EmbSortArgs& a) {
   const int tid = threadIdx.x;
   const int rk = blockIdx.x;
   for (int e = tid; e < 2 * 64 * EMB_CNT_STRIDE; e += 1024) (&cnt[0][0])[e] = 0;
+  // Launch 2 counts finished groups per (heavy entry, slice) and finished
+  // tasks per (group, slice) from zero.
+  {
+    int32_t* c = a.ctr + (size_t)rk * (a.hmax + a.tmax) * a.slices;
+    for (int e = tid; e < (a.hmax + a.tmax) * a.slices; e += 1024) c[e] = 0;
+  }
 
   // 1. Lane l of wave w holds position w*1024 + r*64 + l in slot r. Range 0
   // reports invalid ids. Each wave keeps its range's keys (local token << 14
@@ -617,7 +628,13 @@ VH_DEV void emb_sort_impl(const EmbSortArgs& a) {
   }
   const uint32_t* sorted = kb[0];
   int32_t* sposk = a.spos + (size_t)rk * a.n;
-  for (uint32_t j = tid; j < m; j += 1024) sposk[j] = (int32_t)(sorted[j] & 0x3FFFu);
+  // m <= EMB_SORT_N = 16 x 1024: a fixed count of predicated rounds (a loop
+  // bounded by m left the kernel with an unused private-memory frame).
+#pragma unroll
+  for (int r = 0; r < EMB_SORT_N / 1024; ++r) {
+    const uint32_t j = (uint32_t)(r * 1024 + tid);
+    if (j < m) sposk[j] = (int32_t)(sorted[j] & 0x3FFFu);
+  }
   // 3. Segments: heads (a local token differing from the previous key's),
   // numbered by the count of heads before them.
   const uint32_t jw = (uint32_t)w * per;
@@ -681,8 +698,16 @@ VH_DEV void emb_sort_impl(const EmbSortArgs& a) {
         const uint32_t t0 = tb + tinc - nt;
         *reinterpret_cast<int4*>(heavyk + 4 * e) = make_int4(tok, (int32_t)t0, (int32_t)nt, (int32_t)h);
         hstk[e] = (int32_t)st;
-        for (uint32_t c = 0; c < nt; ++c) tmapk[t0 + c] = (int32_t)e;
       }
+    }
+    // Task map: the wave writes each heavy lane's run of tasks together (one
+    // lane at a time, its tasks spread over the lanes).
+    for (unsigned long long rem = hv; rem; rem &= rem - 1) {
+      const int l = __builtin_ctzll(rem);
+      const uint32_t nl = (uint32_t)__builtin_amdgcn_readlane((int)nt, l);
+      const uint32_t t0l = tb + (uint32_t)__builtin_amdgcn_readlane((int)tinc, l) - nl;
+      const int32_t el = (int32_t)(hb + (uint32_t)__popcll(hv & ((1ull << l) - 1ull)));
+      for (uint32_t c = (uint32_t)lane; c < nl; c += 64) tmapk[t0l + c] = el;
     }
     if (hv) tb += __shfl(tinc, 63, 64);
     hb += (uint32_t)__popcll(hv);
@@ -712,9 +737,64 @@ VH_DEV int range_of(uint32_t inc, uint32_t x, uint32_t* local) {
   return k;
 }
 
+// The sum, in order from 0.0, of cnt rows (at unit u) of the partial rows
+// first, first + step, first + 2 step, ..., read with device-coherent loads,
+// 8 rows in flight.
+template <int VW>
+VH_DEV Unit<VW> emb_coherent_sum(const float* partial, int64_t D, int64_t first, int64_t step, int32_t cnt, int u,
+                                 int U) {
+  Unit<VW> acc = zero_unit<VW>();
+  for (int32_t c0 = 0; c0 < cnt; c0 += EMB_GROUP) {
+    Unit<VW> d[EMB_GROUP];
+#pragma unroll
+    for (int r = 0; r < EMB_GROUP; ++r) {
+      if (c0 + r < cnt && u < U) {
+        const float* src = partial + (first + (int64_t)(c0 + r) * step) * D + u * VW;
+#pragma unroll
+        for (int j = 0; j < VW; ++j) d[r].v[j] = __hip_atomic_load(src + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        d[r] = zero_unit<VW>();
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < EMB_GROUP; ++r) {
+      if (c0 + r < cnt) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) acc.v[j] += d[r].v[j];
+      }
+    }
+  }
+  return acc;
+}
+
+// Stores v at unit u of partial row `row` with device-coherent stores, then
+// waits until they are done (every lane's), so a counter bumped after this
+// by the wave tells another wave that the row can be read.
+template <int VW>
+VH_DEV void emb_coherent_store(float* partial, int64_t D, int64_t row, const Unit<VW>& v, int u, int U) {
+  if (u < U) {
+    float* dst = partial + row * D + u * VW;
+#pragma unroll
+    for (int j = 0; j < VW; ++j) __hip_atomic_store(dst + j, v.v[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Bumps a device-scope counter once for the wave; returns its old value to
+// every lane.
+VH_DEV int32_t emb_count_done(int32_t* c) {
+  int32_t old = 0;
+  if ((threadIdx.x & 63) == 0) old = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __shfl(old, 0, 64);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  return old;
+}
+
 // Launch 2 of the sorted path: 256-thread workgroups, waves striding over the
-// items [0, segments) (light segments; heavy ones are skipped) and then
-// (heavy task, column slice) pairs; tasks are numbered range by range.
+// (heavy task, column slice) pairs (tasks numbered range by range), then the
+// segments (light ones summed; heavy ones are skipped).
 template <int VW>
 VH_DEV void emb_sum_impl(const EmbSumArgs& a) {
   const int lane = threadIdx.x & 63;
@@ -722,12 +802,15 @@ VH_DEV void emb_sum_impl(const EmbSumArgs& a) {
   uint32_t nseg, ntask;
   const uint32_t seg_inc = range_prefix(a.counts, 0, &nseg);
   const uint32_t task_inc = range_prefix(a.counts, 1, &ntask);
-  const int64_t nitems = (int64_t)nseg + (int64_t)ntask * a.slices;
+  // Heavy tasks first: the waves that start first take them, so the combine
+  // of each heavy row's slices overlaps the light segments' stream.
+  const int64_t nheavy_items = (int64_t)ntask * a.slices;
+  const int64_t nitems = (int64_t)nseg + nheavy_items;
   const int64_t nw = (int64_t)gridDim.x * 4;
   for (int64_t it = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); it < nitems; it += nw) {
-    if (it < nseg) {
+    if (it >= nheavy_items) {
       uint32_t s;
-      const int k = range_of(seg_inc, (uint32_t)it, &s);
+      const int k = range_of(seg_inc, (uint32_t)(it - nheavy_items), &s);
       // One load of the record: lanes 0-3 the header, 4 .. 4+hits the positions.
       const int32_t* rec = a.seg + ((size_t)k * a.n + s) * EMB_REC;
       const int32_t rv = lane < EMB_REC ? rec[lane] : 0;
@@ -752,7 +835,7 @@ VH_DEV void emb_sum_impl(const EmbSumArgs& a) {
         }
       }
     } else {
-      const int64_t item = it - nseg;
+      const int64_t item = it;
       const uint32_t t = (uint32_t)(item / a.slices);  // global task index
       const int u = (int)(item % a.slices) * 64 + lane;
       uint32_t lt;
@@ -770,72 +853,37 @@ VH_DEV void emb_sum_impl(const EmbSumArgs& a) {
           src[r] = a.dy + (int64_t)__shfl(mypos, jj + r < got ? jj + r : jj, 64) * a.D;
         emb_add_slice<VW, true, EMB_BATCH>(acc, src, got - jj < EMB_BATCH ? got - jj : EMB_BATCH, u, U);
       }
-      if (u < U) store_unit<VW>(a.partial + (int64_t)t * a.D + u * VW, acc);
+      // A heavy row's slice is finished by the waves that end last, with no
+      // further launch: partials go out with device-coherent stores (past this
+      // XCD's L2) and each wave waits for its stores before it bumps a counter;
+      // the wave that counts the last task of a group of EMB_GROUP tasks reads
+      // the group's partials back with device-coherent loads and sums them in
+      // task order (into the group's first partial row), and the wave that
+      // counts a row's last group sums the group sums in group order into dW.
+      // That is the device-scope release / acquire pair without the whole-L2
+      // write-back and invalidate a fence performs, which these rows -- never
+      // read by plain loads -- do not need. Same grouping, same bits as the
+      // general path's final kernel.
+      emb_coherent_store<VW>(a.partial, a.D, (int64_t)t, acc, u, U);
+      const int sl = (int)(item % a.slices);
+      const int32_t nch = hv.z, ngrp = (nch + EMB_GROUP - 1) / EMB_GROUP;
+      const int32_t g = ((int32_t)lt - hv.y) / EMB_GROUP;
+      const int32_t gsize = min(EMB_GROUP, nch - g * EMB_GROUP);
+      int32_t* ck = a.ctr + (size_t)k * (a.hmax + a.tmax) * a.slices;
+      if (emb_count_done(ck + ((size_t)a.hmax + hv.y + g * EMB_GROUP) * a.slices + sl) != gsize - 1) continue;
+      const int64_t tg = (int64_t)t - ((int32_t)lt - hv.y - g * EMB_GROUP);  // the group's first task
+      const Unit<VW> gs = emb_coherent_sum<VW>(a.partial, a.D, tg, 1, gsize, u, U);
+      float* o = a.dW + (int64_t)hv.x * a.D + u * VW;
+      if (ngrp == 1) {
+        if (u < U) store_stream<VW>(o, gs);
+        continue;
+      }
+      emb_coherent_store<VW>(a.partial, a.D, tg, gs, u, U);
+      if (emb_count_done(ck + ((size_t)e * a.slices + sl)) != ngrp - 1) continue;
+      const int64_t tb = (int64_t)t - ((int32_t)lt - hv.y);  // the row's first task
+      const Unit<VW> gsum = emb_coherent_sum<VW>(a.partial, a.D, tb, EMB_GROUP, ngrp, u, U);
+      if (u < U) store_stream<VW>(o, gsum);
     }
   }
 }
 
-// Launch 3 of the sorted path: one wave per (heavy entry, column slice of 64
-// units), striding over the entries of all ranges: dW[token] at the slice's
-// units = the sum over groups (in order, from 0.0) of the group's partials
-// summed in task order from 0.0 (groups of EMB_GROUP tasks; a row with one
-// group takes that group's sum as it is) -- the grouping of emb_heavy_final,
-// with 4 groups' partials (32 rows) in flight per batch.
-#define EMB_FINAL_GROUPS_S 4
-template <int VW>
-VH_DEV void emb_final_sorted_impl(const EmbSumArgs& a) {
-  const int lane = threadIdx.x & 63;
-  const int U = a.D / VW;
-  uint32_t nheavy, ntask;
-  const uint32_t heavy_inc = range_prefix(a.counts, 2, &nheavy);
-  const uint32_t task_inc = range_prefix(a.counts, 1, &ntask);
-  const int64_t nitems = (int64_t)nheavy * a.slices;
-  const int64_t nw = (int64_t)gridDim.x * 4;
-  for (int64_t it = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); it < nitems; it += nw) {
-    uint32_t e;
-    const int k = range_of(heavy_inc, (uint32_t)(it / a.slices), &e);
-    const int u = (int)(it % a.slices) * 64 + lane;
-    const int4 hv = *reinterpret_cast<const int4*>(a.heavy + ((size_t)k * a.hmax + e) * 4);
-    const int32_t tok = hv.x, nch = hv.z;
-    const int64_t tb = (int64_t)(k > 0 ? __shfl(task_inc, k - 1, 64) : 0u) + hv.y;  // global first task
-    const int32_t ngrp = (nch + EMB_GROUP - 1) / EMB_GROUP;
-    Unit<VW> total = zero_unit<VW>();
-    for (int32_t g0 = 0; g0 < ngrp; g0 += EMB_FINAL_GROUPS_S) {
-      Unit<VW> d[EMB_FINAL_GROUPS_S][EMB_GROUP];
-#pragma unroll
-      for (int q = 0; q < EMB_FINAL_GROUPS_S; ++q) {
-        const int32_t g = g0 + q;
-        const int32_t gsize = g < ngrp ? min(EMB_GROUP, nch - g * EMB_GROUP) : 0;
-#pragma unroll
-        for (int r = 0; r < EMB_GROUP; ++r) {
-          if (r < gsize && u < U)
-            d[q][r] = load_unit<VW>(a.partial + (tb + g * EMB_GROUP + r) * a.D + u * VW);
-          else
-            d[q][r] = zero_unit<VW>();
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < EMB_FINAL_GROUPS_S; ++q) {
-        const int32_t g = g0 + q;
-        if (g < ngrp) {
-          const int32_t gsize = min(EMB_GROUP, nch - g * EMB_GROUP);
-          Unit<VW> gs = zero_unit<VW>();
-#pragma unroll
-          for (int r = 0; r < EMB_GROUP; ++r) {
-            if (r < gsize) {
-#pragma unroll
-              for (int j = 0; j < VW; ++j) gs.v[j] += d[q][r].v[j];
-            }
-          }
-          if (ngrp == 1) {
-            total = gs;
-          } else {
-#pragma unroll
-            for (int j = 0; j < VW; ++j) total.v[j] += gs.v[j];
-          }
-        }
-      }
-    }
-    if (u < U) store_stream<VW>(a.dW + (int64_t)tok * a.D + u * VW, total);
-  }
-}

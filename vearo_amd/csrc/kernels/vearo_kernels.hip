@@ -141,8 +141,6 @@ extern "C" __global__ void __launch_bounds__(256) vh_emb_heavy_final_v4(EmbFinal
 extern "C" __global__ void __launch_bounds__(1024) vh_emb_sort(EmbSortArgs a) { emb_sort_impl(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_emb_sum_v1(EmbSumArgs a) { emb_sum_impl<1>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_emb_sum_v4(EmbSumArgs a) { emb_sum_impl<4>(a); }
-extern "C" __global__ void __launch_bounds__(256) vh_emb_final_sorted_v1(EmbSumArgs a) { emb_final_sorted_impl<1>(a); }
-extern "C" __global__ void __launch_bounds__(256) vh_emb_final_sorted_v4(EmbSumArgs a) { emb_final_sorted_impl<4>(a); }
 
 // Cross-entropy
 // Up to NV = 104 (V <= 53,248) the kernels are held to 128 VGPRs: 4 waves per

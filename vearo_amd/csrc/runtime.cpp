@@ -841,18 +841,19 @@ EmbScratchLayout emb_layout(int64_t n, int64_t V, int64_t D) {
 // t % EMB_RANGES == k in LDS ((t / EMB_RANGES) << 14 | position: n <= 16384,
 // t / EMB_RANGES < 4096).
 constexpr int64_t kEmbSortMaxN = 16384;
-constexpr int64_t kEmbSortMaxV = 65534;
+constexpr int64_t kEmbSortMaxV = EMB_SORT_MAXV;
 bool emb_sorted_path(int64_t n, int64_t V, int64_t D) {
   return n > 0 && n <= kEmbSortMaxN && V > 0 && V <= kEmbSortMaxV && D > 0;
 }
 struct EmbSortLayout {
-  size_t spos, seg, heavy, heavy_start, taskmap, counts, partial, total;
+  size_t spos, seg, heavy, heavy_start, taskmap, counts, ctr, partial, total;
   int64_t hmax, tmax;
 };
 EmbSortLayout emb_sort_layout(int64_t n, int64_t D) {
   EmbSortLayout L;
   L.hmax = n / (kEmbLight + 1) + 1;              // heavy tokens have > 16 hits
   L.tmax = n / kEmbChunkHits + L.hmax + 1;       // ceil(hits / 32) tasks each
+  const int64_t slices_max = cdiv(D, 64);        // column slices of a heavy row (1-float units)
   size_t o = 0;
   auto take = [&](size_t elems) {
     size_t at = o;
@@ -865,6 +866,7 @@ EmbSortLayout emb_sort_layout(int64_t n, int64_t D) {
   L.heavy_start = take((size_t)EMB_RANGES * L.hmax);
   L.taskmap = take((size_t)EMB_RANGES * L.tmax);
   L.counts = take(3 * EMB_RANGES);
+  L.ctr = take((size_t)EMB_RANGES * (L.hmax + L.tmax) * slices_max);
   L.partial = take((size_t)L.tmax * (size_t)D);
   L.total = o;
   return L;
@@ -878,7 +880,8 @@ size_t vh_embedding_bwd_scratch_bytes(int64_t n, int64_t V, int64_t D) {
 }
 
 namespace {
-// Sorted path: range sorts + zero fill, segment sums and heavy partials, heavy rows.
+// Sorted path: range sorts + zero fill, then segment sums and heavy partials with
+// each heavy row slice finished by its last task.
 int emb_bwd_sorted(const float* ids, const float* dy, float* dW, int64_t n, int64_t V, int64_t D, void* base_p,
                    hipStream_t s) {
   const EmbSortLayout L = emb_sort_layout(n, D);
@@ -890,19 +893,18 @@ int emb_bwd_sorted(const float* ids, const float* dy, float* dW, int64_t n, int6
   const int64_t fill_blocks =
       std::max<int64_t>(1, std::min<int64_t>(std::max(g_rt.cu_count, EMB_RANGES + 1) - EMB_RANGES,
                                              cdiv(fill_n, 8192)));
-  EmbSortArgs k1{ids, dW, I(L.spos), I(L.seg), I(L.heavy), I(L.heavy_start), I(L.taskmap), I(L.counts),
-                 g_rt.err, fill_n, (int32_t)n, (int32_t)V, (int32_t)L.hmax,
-                 (int32_t)L.tmax, vec ? 1 : 0};
-  VH_TRY(launch("vh_emb_sort", (unsigned)(EMB_RANGES + fill_blocks), 1, 1024, 0, s, k1));
   const int32_t slices = (int32_t)cdiv(D / (vec ? 4 : 1), 64);
-  EmbSumArgs k2{I(L.spos), I(L.seg), I(L.heavy), I(L.heavy_start), I(L.taskmap), I(L.counts),
+  EmbSortArgs k1{ids, dW, I(L.spos), I(L.seg), I(L.heavy), I(L.heavy_start), I(L.taskmap), I(L.counts),
+                 I(L.ctr), g_rt.err, fill_n, (int32_t)n, (int32_t)V, (int32_t)L.hmax,
+                 (int32_t)L.tmax, vec ? 1 : 0, slices};
+  VH_TRY(launch("vh_emb_sort", (unsigned)(EMB_RANGES + fill_blocks), 1, 1024, 0, s, k1));
+  EmbSumArgs k2{I(L.spos), I(L.seg), I(L.heavy), I(L.heavy_start), I(L.taskmap), I(L.counts), I(L.ctr),
                 reinterpret_cast<float*>(base + L.partial), dy, dW, (int32_t)n, (int32_t)L.hmax, (int32_t)L.tmax,
                 (int32_t)D, slices};
-  // A wave per item (segments, then heavy tasks' slices) up to 16384 waves.
-  VH_TRY(launch(vec ? "vh_emb_sum_v4" : "vh_emb_sum_v1",
-                (unsigned)std::min<int64_t>(4096, cdiv(n + L.tmax * slices, 4)), 1, 256, 0, s, k2));
-  return launch(vec ? "vh_emb_final_sorted_v4" : "vh_emb_final_sorted_v1",
-                (unsigned)std::min<int64_t>(256, cdiv(L.hmax * slices, 4)), 1, 256, 0, s, k2);
+  // A wave per item (heavy tasks' slices, then segments) up to 16384 waves;
+  // the last tasks of each heavy row's slice write that slice of dW.
+  return launch(vec ? "vh_emb_sum_v4" : "vh_emb_sum_v1",
+                (unsigned)std::min<int64_t>(4096, cdiv(n + L.tmax * slices, 4)), 1, 256, 0, s, k2);
 }
 }  // namespace
 
@@ -1303,7 +1305,11 @@ thread_local int g_gemm_path = VH_GEMM_PATH_NONE;
 // tile's reads within 2^32 bytes of its origin (leading dimensions < 2^22); k
 // tile and tile counts below 2^31 (K < 2^26). A k-contiguous operand with
 // K % 32 != 0 splits K: the kernel takes the whole 32-wide k tiles and the
-// tiled kernel adds the rest (alpha times the tail product) into C.
+// tiled kernel adds the rest (alpha times the tail product) into C. A
+// row-contiguous operand's reads past K land past its buffer bound, and so read
+// 0, only when its leading dimension covers its extent (lda >= M, ldb >= N):
+// one broadcast along k (stride 0) or with overlapping rows leaves a partial
+// last k tile to the tiled kernel, which tests k < K.
 int gemm_big(const vh_gemm_desc* d, bool akc, bool bkc, int64_t lda, int64_t ldb, hipStream_t s, bool* taken) {
   *taken = false;
   const int64_t M = d->M, N = d->N, K = d->K, nb = d->batch[0] * d->batch[1];
@@ -1318,6 +1324,7 @@ int gemm_big(const vh_gemm_desc* d, bool akc, bool bkc, int64_t lda, int64_t ldb
   const int G = std::max(8, g_rt.cu_count / 8 * 8);
   const int64_t K32 = (akc || bkc) ? K / 32 * 32 : K;
   if (K32 == 0) return VH_OK;
+  if (K32 % 32 != 0 && ((!akc && lda < M) || (!bkc && ldb < N))) return VH_OK;
   const int64_t tiles_m = cdiv(M, VH_GEMMB_TM), tiles_n = cdiv(N, VH_GEMMB_TN);
   if (tiles_m * tiles_n * nb >= INT32_MAX) return VH_OK;
   const int64_t tiles = tiles_m * tiles_n * nb, rem = tiles % G;

@@ -215,10 +215,12 @@ struct EmbSegArgs {
 
 // Embedding backward, sorted path (n <= 16384, V <= 65534). Launch 1:
 // workgroup k < EMB_RANGES sorts the keys of the tokens t % EMB_RANGES == k
-// and writes that range's lists (below); the others write dW's zeros. Launches 2
-// (segment sums, heavy partial rows) and 3 (heavy rows) walk the lists, each
-// wave taking the 16 ranges' counts and their prefix sums itself.
+// and writes that range's lists (below); the others write dW's zeros. Launch 2
+// walks the lists (light segment sums; heavy partial rows, the last task of a
+// heavy row's column slice adding them into dW), each wave taking the 16
+// ranges' counts and their prefix sums itself.
 #define EMB_RANGES 16
+#define EMB_SORT_MAXV 65534  // vocabulary bound of the sorted path (t / EMB_RANGES < 4096)
 #define EMB_REC 20  // ints per segment record: token, start, hits, 0, then a light token's positions
 struct EmbSortArgs {
   const float* ids;
@@ -230,6 +232,8 @@ struct EmbSortArgs {
   int32_t* heavy_start;  // [EMB_RANGES][hmax]: start in the range's spos of each heavy token's hits
   int32_t* taskmap;      // [EMB_RANGES][tmax]: range-local heavy entry of each task
   int32_t* counts;       // [3][EMB_RANGES]: segments, tasks, heavy entries of each range
+  int32_t* ctr;          // [EMB_RANGES][hmax + tmax][slices]: launch 2's counters (groups finished per
+                         // heavy entry and slice, then tasks finished per group and slice), zeroed here
   VhErrRecord* err;
   int64_t fill_n;
   int32_t n;
@@ -237,6 +241,7 @@ struct EmbSortArgs {
   int32_t hmax;
   int32_t tmax;
   int32_t vec;
+  int32_t slices;        // column slices per heavy row (64 units each)
 };
 
 struct EmbSumArgs {
@@ -246,6 +251,8 @@ struct EmbSumArgs {
   const int32_t* heavy_start;
   const int32_t* taskmap;
   const int32_t* counts;
+  int32_t* ctr;    // [EMB_RANGES][hmax + tmax][slices]: groups finished per (heavy entry, slice), then
+                   // tasks finished per (group's first task, slice); zero at launch
   float* partial;  // [tasks][D], tasks numbered range by range
   const float* dy;
   float* dW;
