@@ -27,8 +27,10 @@ rows only for embedding gathers). Per kernel, "avg_us" is the op run alone
 average launch duration, the figure a kernel trace reports) and "in_step_us"
 the HIP events around it inside a second pass of the steps (each event's own
 cost included). `roofline` reports the longest kernel by avg_us, with
-`traffic` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes when
-present. cpu_baseline times the CPU oracle (the C restatement of the
+`traffic` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+(profiles/pmc_traffic.json, written by --pmc-summarize); every op with such a
+record carries "traffic_bytes" and "traffic_ratio" (measured over
+algorithmic). cpu_baseline times the CPU oracle (the C restatement of the
 reference's CPU backend, one thread, as the reference's kernels are) on the
 whole headline step at its own shapes, and on bounded samples for the other
 configs; "host" records the CPU model, core count and glibc.
@@ -37,11 +39,12 @@ Warmup is at least --warmup steps and at least --min-warmup-ms of them: after
 the second or so of host-side input generation the GPU has lowered its clocks,
 and a few milliseconds of work do not bring them back (measured: the softmax
 backward runs 262 us back to back, 270-336 us for the first ~10 ms after a 1 s
-idle). The JSON's "warmup" is the number of warmup steps run; the timed region
-is exactly --steps steps either way.
+idle). The JSON's "warmup" is the requested --warmup and "warmup_steps_run"
+the number of warmup steps actually run; the timed region is exactly --steps
+steps either way.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--min-warmup-ms 1000] [--workload NAME]
-                       [--no-cpu] [--no-extra]
+                       [--no-cpu] [--no-extra] [--calibrate-copy] [--pmc-summarize DIR]
 """
 import argparse
 import ctypes
@@ -194,7 +197,7 @@ def wl_ln_softmax(vh):
 
     info = {"workload": "layernorm fwd+bwd [16384,768] + causal softmax fwd+bwd [16,12,1024,1024]",
             "ln_shape": [LN_ROWS, LN_C], "softmax_shape": [SM_B, SM_H, SM_T, SM_T]}
-    return ops, info, cpu, keep, "pmc_traffic_bench.json"
+    return ops, info, cpu, keep
 
 
 def wl_layernorm_cfg0(vh):
@@ -219,7 +222,7 @@ def wl_layernorm_cfg0(vh):
         return (lf + lb) * reps / t, f"layernorm fwd+bwd [{rows},{C}] (the whole config), {reps} reps, single thread"
 
     return ops, {"workload": "cfg[0] layernorm fwd+bwd [2048,128] (launch-bound, cache-resident)"}, cpu, \
-        (X, W, Bi, DY, Y, DX, DW, DB), None
+        (X, W, Bi, DY, Y, DX, DW, DB)
 
 
 def wl_gelu_bias(vh):
@@ -248,7 +251,7 @@ def wl_gelu_bias(vh):
         return (20 * sr * C + 12 * C) * reps / t, (f"bias add + gelu fwd and mask*dy + bias reduce_to on "
                                                    f"[{sr},{C}], {reps} reps, single thread")
 
-    return ops, {"workload": "cfg[1] gelu(x+bias) fwd+bwd [16384,3072]"}, cpu, (Bi, X, DY, Y, DX, DB, SC), None
+    return ops, {"workload": "cfg[1] gelu(x+bias) fwd+bwd [16384,3072]"}, cpu, (Bi, X, DY, Y, DX, DB, SC)
 
 
 def _embedding(vh, zipf):
@@ -274,7 +277,7 @@ def _embedding(vh, zipf):
 
     kind = "Zipf(1.1)" if zipf else "uniform"
     return ops, {"workload": f"cfg[3] embedding fwd+bwd, {kind} ids, V=50257 D=768 n=16384",
-                 "distinct_ids": U}, cpu, (I, Wd, DY, OUT, DW, SC), None
+                 "distinct_ids": U}, cpu, (I, Wd, DY, OUT, DW, SC)
 
 
 def wl_embedding_uniform(vh):
@@ -310,7 +313,7 @@ def wl_cross_entropy(vh):
         return (12 * sb_ * V + 16 * sb_) * reps / t, f"cross-entropy fwd+bwd on [{sb_},{V}], {reps} reps, single thread"
 
     return ops, {"workload": "cross-entropy fwd+bwd over logits [16384,50257] (cfg[4] lm_head output)"}, cpu, \
-        (L, T, GO, LOSS, DL, SC), None
+        (L, T, GO, LOSS, DL, SC)
 
 
 def wl_softmax_dense(vh):
@@ -337,7 +340,7 @@ def wl_softmax_dense(vh):
         return 20 * s.size * reps / t, f"softmax fwd + composite bwd on [1,2,{T},{T}], {reps} reps, single thread"
 
     return ops, {"workload": "softmax fwd+bwd [16,12,1024,1024], dense (the BackendOps slot form)"}, cpu, \
-        (S, G, P, DS), None
+        (S, G, P, DS)
 
 
 def gpt_fwd_flops(B, S, D, H, F, V):
@@ -461,7 +464,31 @@ def wl_gpt2_block(vh):
     info = {"workload": "cfg[4] GPT-2-small block training step: B=16, T=1024, C=768, H=12, MLP 3072, "
                         "V=50257, one block; fwd + backward + AdamW",
             "flops_per_step": flops, "_mode": "step_ms", "_probe": probe, "_ab": ab, "_dropin": dropin}
-    return ops, info, cpu, (g, A, W, C, d, dl), None
+    return ops, info, cpu, (g, A, W, C, d, dl)
+
+
+def wl_lm_head_gemm(vh):
+    """The dominant kernel of config[4] on its own (for counters and traces):
+    logits[16384, 50257] = lnf[16384, 768] W^T through vh_gemm (this library's
+    persistent kernel), the product the block step's roofline line reports.
+    Algorithmic bytes: A, B read once and C written once."""
+    B, S, D, V = 16, 1024, 768, 50257
+    r = np.random.default_rng(SEED + 4)
+    A = vh.DeviceBuffer.from_array(r.standard_normal((B * S, D), dtype=np.float32))
+    W = vh.DeviceBuffer.from_array(r.standard_normal((V, D), dtype=np.float32) * np.float32(0.02))
+    C = vh.DeviceBuffer(4 * B * S * V)
+    d = vh.VhGemmDesc()
+    d.M, d.N, d.K = B * S, V, D
+    d.a, d.a_sm, d.a_sk = A.ptr, D, 1
+    d.b, d.b_sk, d.b_sn = W.ptr, 1, D
+    d.c, d.c_sm = C.ptr, V
+    d.batch[0] = d.batch[1] = 1
+    d.alpha = 1.0
+    nb = 4 * (B * S * D + V * D + B * S * V)
+    ops = [("lm_head_gemm", nb, lambda i: vh.lib.vh_gemm(ctypes.byref(d), None))]
+    info = {"workload": "cfg[4] lm_head forward product [16384,768] x [768,50257] alone",
+            "flops": 2 * B * S * D * V}
+    return ops, info, None, (A, W, C, d)
 
 
 PEAK_PCIE_GBPS = 64.0  # MI355X host link, PCIe 5.0 x16, one direction
@@ -542,7 +569,96 @@ def run_checkpoint(args, vh):
 WORKLOADS = {"ln_softmax": wl_ln_softmax, "gpt2_block": wl_gpt2_block, "layernorm_cfg0": wl_layernorm_cfg0,
              "gelu_bias": wl_gelu_bias, "embedding_uniform": wl_embedding_uniform,
              "embedding_zipf": wl_embedding_zipf, "cross_entropy": wl_cross_entropy,
-             "softmax_dense": wl_softmax_dense, "checkpoint": run_checkpoint}
+             "softmax_dense": wl_softmax_dense, "lm_head_gemm": wl_lm_head_gemm, "checkpoint": run_checkpoint}
+
+# The kernels each op launches (name patterns), per workload: the per-dispatch
+# FETCH_SIZE / WRITE_SIZE averages of the matching kernels add up to the op's
+# measured HBM traffic (--pmc-summarize). gpt2_block's entry is the fused
+# cross-entropy pass of its step (the one kernel of its kind there).
+_LN = {"layernorm_fwd": r"^vh_ln_fwd_", "layernorm_bwd": r"^vh_ln_bwd_|^vh_col_reduce$"}
+PMC_KERNELS = {
+    "ln_softmax": dict(_LN, softmax_fwd=r"^vh_sm_fwd_", softmax_bwd=r"^vh_sm_bwd_"),
+    "layernorm_cfg0": _LN,
+    "gelu_bias": {"gelu_bias_fwd": r"^vh_gelu_bias_fwd", "gelu_bias_bwd": r"^vh_gelu_bias_bwd|^vh_col_reduce$"},
+    "embedding_uniform": {"embedding_fwd": r"^vh_emb_fwd", "embedding_bwd": r"^vh_emb_(sort|sum)"},
+    "embedding_zipf": {"embedding_fwd": r"^vh_emb_fwd", "embedding_bwd": r"^vh_emb_(sort|sum)"},
+    "cross_entropy": {"cross_entropy_fwd": r"^vh_xent_fwd|^vh_xent_reduce$", "cross_entropy_bwd": r"^vh_xent_bwd"},
+    "softmax_dense": {"softmax_dense_fwd": r"^vh_sm_fwd_", "softmax_dense_bwd": r"^vh_sm_bwd_"},
+    "lm_head_gemm": {"lm_head_gemm": r"^vh_gemm"},
+    "gpt2_block": {"cross_entropy_fused": r"^vh_xent_fb_|^vh_xent_reduce$"},
+}
+PMC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+
+
+def pmc_traffic(workload):
+    """{op: traffic record} for a workload from the committed counter summary."""
+    if not os.path.exists(PMC_FILE):
+        return {}
+    with open(PMC_FILE) as f:
+        return json.load(f).get("workloads", {}).get(workload, {})
+
+
+def pmc_summarize(root):
+    """Writes profiles/pmc_traffic.json from rocprofv3 --pmc runs under root:
+    <workload>_fetch/ and <workload>_write/ (FETCH_SIZE, WRITE_SIZE) for each
+    workload in PMC_KERNELS that has them, and copy_fetch/ + copy_write/
+    (--calibrate-copy: 4 copies of 1 GiB each way) for the scale factors."""
+    import csv
+    import glob
+    import re
+
+    def per_kernel(d):
+        files = glob.glob(os.path.join(root, d, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            return None
+        agg, names = {}, {}
+        for row in csv.DictReader(open(files[0])):
+            k = int(row["Dispatch_Id"])
+            agg[k] = agg.get(k, 0.0) + float(row["Counter_Value"])
+            names[k] = row["Kernel_Name"]
+        byk = {}
+        for k in sorted(agg):
+            byk.setdefault(names[k], []).append(agg[k])
+        return byk
+
+    cf, cw = per_kernel("copy_fetch"), per_kernel("copy_write")
+    exp_kib = float(1 << 30) / 1024
+    cfv = [v for n, vs in cf.items() if n == "vh_stream_copy" for v in vs]
+    cwv = [v for n, vs in cw.items() if n == "vh_stream_copy" for v in vs]
+    fmean, wmean = sum(cfv) / len(cfv), sum(cwv) / len(cwv)
+    fscale, wscale = exp_kib / fmean, exp_kib / wmean
+    out = {"note": "HBM bytes per op call = (FETCH_SIZE KiB x fetch_scale + WRITE_SIZE KiB x write_scale) x 1024, "
+                   "per-dispatch averages of the op's kernels summed; the scales make a copy of 1 GiB read as "
+                   "1 GiB each way",
+           "commands": {
+               "fetch": "cd /tmp && export TMPDIR=/tmp && rocprofv3 --pmc FETCH_SIZE --output-format csv -d "
+                        "$DIR/<workload>_fetch -o pmc -- python3 $REPO/bench.py --workload <workload> --steps 3 "
+                        "--warmup 1 --min-warmup-ms 0 --no-cpu --no-extra",
+               "write": "the same with --pmc WRITE_SIZE into $DIR/<workload>_write",
+               "copy": "rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) -d $DIR/copy_fetch (copy_write) -o pmc -- "
+                       "python3 $REPO/bench.py --calibrate-copy",
+               "summary": "python3 bench.py --pmc-summarize $DIR"},
+           "calibration": {"copy_kernel": "vh_d2d of 1 GiB, 4 dispatches", "expected_kib_each_way": exp_kib,
+                           "fetch_kib_measured": round(fmean, 1), "write_kib_measured": round(wmean, 1),
+                           "fetch_scale": round(fscale, 4), "write_scale": round(wscale, 4)},
+           "workloads": {}}
+    for wl, pats in PMC_KERNELS.items():
+        bf, bw = per_kernel(wl + "_fetch"), per_kernel(wl + "_write")
+        if bf is None or bw is None:
+            continue
+        res = {}
+        for op, pat in pats.items():
+            syms = sorted(n for n in bf if re.search(pat, n))
+            if not syms:
+                continue
+            f = sum(sum(bf[n]) / len(bf[n]) for n in syms)
+            w = sum(sum(bw[n]) / len(bw[n]) for n in syms if n in bw)
+            res[op] = {"symbols": syms, "fetch_kib": round(f, 1), "write_kib": round(w, 1),
+                       "traffic_bytes": int(round((f * fscale + w * wscale) * 1024))}
+        out["workloads"][wl] = res
+    with open(PMC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps({wl: {op: v["traffic_bytes"] for op, v in r.items()} for wl, r in out["workloads"].items()}))
 # Run by default after the headline, each reported under "configs" in the one line.
 EXTRA = ["gpt2_block", "gelu_bias", "embedding_uniform", "embedding_zipf", "cross_entropy", "softmax_dense",
          "layernorm_cfg0"]
@@ -611,19 +727,16 @@ def measure(vh, hip, stream, ops, K, warmup, min_warmup_ms):
     return {"warmup": warm, "wall": wall, "in_step_ms": in_step, "avg_ms": avg}
 
 
-def summarize_bytes(ops, m, K, traffic_file=None):
+def summarize_bytes(ops, m, K, workload):
     kernels = {}
+    tk = pmc_traffic(workload)
     for n, nb, _ in ops:
         a_s, s_s = m["avg_ms"][n] / 1e3, m["in_step_ms"][n] / 1e3
         kernels[n] = {"avg_us": round(a_s * 1e6, 2), "in_step_us": round(s_s * 1e6, 2), "bytes": nb,
                       "gbps": round(nb / a_s / 1e9, 1), "frac": round(nb / a_s / 1e9 / PEAK_GBPS, 4)}
-    tpath = os.path.join(ROOT, "profiles", traffic_file) if traffic_file else None
-    if tpath and os.path.exists(tpath):
-        with open(tpath) as f:
-            tk = json.load(f).get("kernels", {})
-        for n in kernels:
-            if n in tk:
-                kernels[n]["traffic_bytes"] = tk[n]["traffic_bytes"]
+        if n in tk:
+            kernels[n]["traffic_bytes"] = tk[n]["traffic_bytes"]
+            kernels[n]["traffic_ratio"] = round(tk[n]["traffic_bytes"] / nb, 3)
     step_bytes = sum(o[1] for o in ops)
     ms = m["wall"] / K * 1e3
     return {"ms_per_step": round(ms, 4), "bytes_per_step": step_bytes,
@@ -655,7 +768,7 @@ def lm_head_probe(vh, hip, stream, info):
 
 def run_one(name, vh, hip, stream, args, cpu_budget):
     """Set up one workload, measure it, time its CPU baseline; returns a summary."""
-    ops, info, cpu, keep, traffic_file = WORKLOADS[name](vh)
+    ops, info, cpu, keep = WORKLOADS[name](vh)
     m = measure(vh, hip, stream, ops, args.steps, args.warmup, args.min_warmup_ms)
     K = args.steps
     if info.get("_mode") == "step_ms":
@@ -665,11 +778,20 @@ def run_one(name, vh, hip, stream, args, cpu_budget):
         dropin = info.pop("_dropin", None)
         step_s = m["wall"] / K
         flops = info["flops_per_step"]
+        # HBM traffic of the lm_head product (counters over the product alone,
+        # workload lm_head_gemm) and of the step's fused cross-entropy pass.
+        lt = pmc_traffic("lm_head_gemm").get("lm_head_gemm")
+        if lt:
+            probe["traffic_bytes"] = lt["traffic_bytes"]
+        ce = pmc_traffic(name).get("cross_entropy_fused")
         res = {"ms_per_step": round(step_s * 1e3, 3), "tflops": round(flops / step_s / 1e12, 2),
                "frac_of_f32_mfma_peak": round(flops / step_s / 1e12 / PEAK_F32_MFMA_TFLOPS, 4),
                "kernels": {pname: probe}, "config": info,
                "roofline": {"bound": "mfma", "kernel": pname, "achieved": probe["tflops"],
-                            "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": probe["frac"], "traffic": None}}
+                            "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": probe["frac"],
+                            "traffic": lt["traffic_bytes"] if lt else None}}
+        if ce:
+            res["cross_entropy_fused_traffic_bytes"] = ce["traffic_bytes"]
         if ab is not None:
             res["ab_library"] = ab(hip, stream, max(3, min(K, 10)))
         if dropin is not None:
@@ -679,9 +801,9 @@ def run_one(name, vh, hip, stream, args, cpu_budget):
             res["cpu_baseline"] = {"value": round(ms, 1), "unit": "ms per step", "cores": threads, "kind": "port",
                                    "sample": sample, "host": host_info()}
     else:
-        res = summarize_bytes(ops, m, K, traffic_file)
+        res = summarize_bytes(ops, m, K, name)
         res["config"] = info
-        if cpu_budget is not None:
+        if cpu_budget is not None and cpu is not None:
             rate, sample = cpu(cpu_budget)
             res["cpu_baseline"] = {"value": round(rate / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
                                    "sample": sample + "; GB/s counts the same algorithmic bytes as the GPU figure"}
@@ -704,10 +826,16 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline only (no other configs in the line)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--pmc-summarize", metavar="DIR",
+                    help="only write profiles/pmc_traffic.json from the rocprofv3 --pmc runs under DIR "
+                         "(no GPU use)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 4 device-to-device copies of 1 GiB (a copy kernel of known "
                          "size, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    if args.pmc_summarize:
+        pmc_summarize(args.pmc_summarize)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box has one GPU); "
               "run with --gpus 1", file=sys.stderr)
@@ -741,8 +869,8 @@ def main():
     cpu_budget = None if args.no_cpu else args.cpu_seconds
     head = run_one(args.workload, vh, hip, stream, args, cpu_budget)
     K = args.steps
-    common = {"n_gpus": 1, "steps": K, "warmup": head.pop("warmup_steps"), "scaling": "weak",
-              "vs_baseline": None, "dtype": "f32"}
+    common = {"n_gpus": 1, "steps": K, "warmup": args.warmup, "warmup_steps_run": head.pop("warmup_steps"),
+              "scaling": "weak", "vs_baseline": None, "dtype": "f32"}
     if args.workload == "gpt2_block":
         res = {"metric": "GPT block step ms (config[4]: fwd + bwd + AdamW)", "value": head["ms_per_step"],
                "unit": "ms", **common, "ms_per_step": head["ms_per_step"], "higher_is_better": False,
