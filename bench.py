@@ -416,12 +416,15 @@ def wl_gpt2_block(vh):
             g.set_gemm_engine(vh.GEMM_ENGINE_DEFAULT)
         return out
 
-    def dropin(hip, stream, steps):
+    def dropin(hip, stream, steps, fused=True):
         # The same step issued op by op through the BackendOps mirror, in the
         # reference's own order (forward tape, backward_impl arms, AdamW::step):
         # what an unchanged vearo program gets. Timed like the headline, then
         # one step with an event after every op for the per-phase breakdown.
-        d = _block.DropIn(_block.GptConfig(*cfg))
+        # fused=False: MultiHeadAttention's unfused path (the reference with
+        # VEARO_USE_FUSED_ATTENTION=0), scores through the matmul, mul, add and
+        # softmax slots and back through the Softmax arm's slot calls.
+        d = _block.DropIn(_block.GptConfig(*cfg), fused_attention=fused)
         try:
             d.set_params(params)
             d.set_inputs(ids, tg)
@@ -463,7 +466,8 @@ def wl_gpt2_block(vh):
 
     info = {"workload": "cfg[4] GPT-2-small block training step: B=16, T=1024, C=768, H=12, MLP 3072, "
                         "V=50257, one block; fwd + backward + AdamW",
-            "flops_per_step": flops, "_mode": "step_ms", "_probe": probe, "_ab": ab, "_dropin": dropin}
+            "flops_per_step": flops, "_mode": "step_ms", "_probe": probe, "_ab": ab, "_dropin": dropin,
+            "_dropin_unfused": lambda hip, stream, steps: dropin(hip, stream, steps, fused=False)}
     return ops, info, cpu, (g, A, W, C, d, dl)
 
 
@@ -776,6 +780,7 @@ def run_one(name, vh, hip, stream, args, cpu_budget):
         pname, probe = lm_head_probe(vh, hip, stream, info)
         ab = info.pop("_ab", None)
         dropin = info.pop("_dropin", None)
+        dropin_unfused = info.pop("_dropin_unfused", None)
         step_s = m["wall"] / K
         flops = info["flops_per_step"]
         # HBM traffic of the lm_head product (counters over the product alone,
@@ -796,6 +801,8 @@ def run_one(name, vh, hip, stream, args, cpu_budget):
             res["ab_library"] = ab(hip, stream, max(3, min(K, 10)))
         if dropin is not None:
             res["dropin"] = dropin(hip, stream, max(3, min(K, 10)))
+        if dropin_unfused is not None:
+            res["dropin_unfused"] = dropin_unfused(hip, stream, max(3, min(K, 10)))
         if cpu_budget is not None:
             ms, threads, sample = cpu(cpu_budget)
             res["cpu_baseline"] = {"value": round(ms, 1), "unit": "ms per step", "cores": threads, "kind": "port",
@@ -916,6 +923,7 @@ def main():
         res["gpt2_block_frac_of_f32_mfma_peak"] = g["frac_of_f32_mfma_peak"]
         res["gpt2_block_ms_hipblaslt_ab"] = g.get("ab_library", {}).get("gpt2_block_ms_library")
         res["gpt2_block_dropin_ms"] = g.get("dropin", {}).get("ms_per_step")
+        res["gpt2_block_dropin_unfused_ms"] = g.get("dropin_unfused", {}).get("ms_per_step")
         res["configs"] = configs
     print(json.dumps(res), flush=True)
 

@@ -102,12 +102,19 @@ int vb_gpt_train_step(vb_gpt* g, float lr, float beta1, float beta2, float eps, 
  * timing == 0. No counterpart entry point in the reference: the drop-in
  * step's measurement and parity harness.
  * ------------------------------------------------------------------------- */
-#define VB_DROPIN_NPHASES 19
+#define VB_DROPIN_NPHASES 23
 
 typedef struct vb_dropin vb_dropin;
 
 int vb_dropin_create(const vb_gpt_config* cfg, vb_dropin** out);
 void vb_dropin_destroy(vb_dropin* d);
+/* MultiHeadAttention's path: fused != 0 the fused_attention slot (the
+ * default), 0 the unfused chain q.matmul(k^T).mul(scale).add(mask).softmax(3)
+ * .matmul(v) with its autograd arms (crates/vearo-nn/src/lib.rs:603-613).
+ * vb_dropin_create starts from the reference's switch, the environment
+ * variable VEARO_USE_FUSED_ATTENTION ("0" or "false": unfused). */
+int vb_dropin_set_fused_attention(vb_dropin* d, int fused);
+int vb_dropin_fused_attention(const vb_dropin* d);
 /* Host copies of parameter i (numel must match) and of its last gradient
  * (after a step with backward != 0). */
 int vb_dropin_set_param(vb_dropin* d, int i, const float* host, int64_t numel);

@@ -78,6 +78,10 @@ def _load():
                           c_float],
         "vo_gpt_param_numel": [POINTER(GptConfig), POINTER(c_int64)],
         "vo_gpt_step": [POINTER(GptConfig), POINTER(c_void_p), f, f, f, POINTER(c_void_p)] + err,
+        "vo_gpt_step_ex": [POINTER(GptConfig), POINTER(c_void_p), f, f, c_int, f, POINTER(c_void_p)] + err,
+        "vo_attention_unfused": [f, f, f, c_int64, c_int64, c_int64, c_int64, f, L, f] + err,
+        "vo_attention_unfused_backward": [f, f, f, c_int64, c_int64, c_int64, c_int64, f, L, f, f, f,
+                                          f] + err,
         "vo_checkpoint_save": [c_char_p, c_int, POINTER(c_void_p), L] + err,
         "vo_checkpoint_load": [c_char_p, c_int, POINTER(c_void_p), L] + err,
     }
@@ -341,6 +345,28 @@ def fused_attention_backward(q, k, v, mask, go):
     return dq, dk, dv
 
 
+def attention_unfused(q, k, v, mask=None):
+    """MultiHeadAttention's unfused path (VEARO_USE_FUSED_ATTENTION=0,
+    nn:603-613): q.matmul(k^T).mul(scale) (+ mask), softmax(3), matmul(v)."""
+    q, k, v, m, ml = _att_args(q, k, v, mask)
+    B, H, S, Dk = q.shape
+    out = np.zeros_like(q)
+    _call(lib.vo_attention_unfused, _ptr(q), _ptr(k), _ptr(v), B, H, S, Dk,
+          _ptr(m) if m is not None else None, ml, _ptr(out))
+    return out
+
+
+def attention_unfused_backward(q, k, v, mask, go):
+    """dq, dk, dv of the unfused path: its tape's arms walked back."""
+    q, k, v, m, ml = _att_args(q, k, v, mask)
+    go = np.ascontiguousarray(go, np.float32)
+    B, H, S, Dk = q.shape
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(q), np.zeros_like(q)
+    _call(lib.vo_attention_unfused_backward, _ptr(q), _ptr(k), _ptr(v), B, H, S, Dk,
+          _ptr(m) if m is not None else None, ml, _ptr(go), _ptr(dq), _ptr(dk), _ptr(dv))
+    return dq, dk, dv
+
+
 def adamw_step(p, g, m, v, t, lr, beta1, beta2, eps, wd):
     """In place on float32 contiguous arrays p, m, v."""
     for a in (p, m, v):
@@ -356,8 +382,9 @@ def gpt_param_shapes(cfg: GptConfig):
             (D,), (D,), (F, D), (F,), (D, F), (D,), (D,), (D,), (V, D)]
 
 
-def gpt_step(cfg: GptConfig, params, ids, targets, grads: bool = True):
-    """(loss, [grad per parameter] or None) of one SimpleGPT forward(+backward)."""
+def gpt_step(cfg: GptConfig, params, ids, targets, grads: bool = True, fused_attention: bool = True):
+    """(loss, [grad per parameter] or None) of one SimpleGPT forward(+backward);
+    fused_attention=False takes MultiHeadAttention's unfused path."""
     params = [np.ascontiguousarray(p, np.float32) for p in params]
     shapes = gpt_param_shapes(cfg)
     assert len(params) == len(shapes)
@@ -371,7 +398,8 @@ def gpt_step(cfg: GptConfig, params, ids, targets, grads: bool = True):
     if grads:
         gs = [np.zeros(sh, np.float32) for sh in shapes]
         gp = (c_void_p * len(gs))(*[g.ctypes.data for g in gs])
-    _call(lib.vo_gpt_step, ctypes.byref(cfg), pp, _ptr(ids), _ptr(targets), _ptr(loss), gp)
+    _call(lib.vo_gpt_step_ex, ctypes.byref(cfg), pp, _ptr(ids), _ptr(targets), 0 if fused_attention else 1,
+          _ptr(loss), gp)
     return float(loss[0]), gs
 
 

@@ -434,6 +434,124 @@ int vo_fused_attention_backward(const float* q, const float* k, const float* v, 
   return VO_OK;
 }
 
+/* ---------------------------------------------------- unfused attention -- */
+
+static float* falloc(int64_t n);
+
+/* [N][R][C] -> [N][C][R] (a transposed view made contiguous, as the CPU
+ * matmul does with every operand, cpu:307-308). */
+static void transpose_last2(const float* src, int64_t N, int64_t R, int64_t C, float* dst) {
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t r = 0; r < R; ++r)
+      for (int64_t c = 0; c < C; ++c) dst[(n * C + c) * R + r] = src[(n * R + r) * C + c];
+}
+
+static void lay4(vo_layout* l, int64_t a, int64_t b, int64_t c, int64_t d) {
+  const int64_t dims[4] = {a, b, c, d};
+  vo_contiguous_layout(l, 4, dims);
+}
+
+/* The intermediates of the unfused path (nn:603-613): scores after the mask
+ * (the Softmax node's saved input) and the probabilities. */
+static int unfused_scores(const float* q, const float* k, int64_t B, int64_t H, int64_t S, int64_t Dk,
+                          const float* mask, const vo_layout* ml, float* scores, float* probs, char* err,
+                          size_t errlen) {
+  const int64_t N = B * H;
+  vo_layout lq, lkT, ls, lsc;
+  lay4(&lq, B, H, S, Dk);
+  lay4(&lkT, B, H, Dk, S);
+  lay4(&ls, B, H, S, S);
+  const int64_t one = 1;
+  vo_contiguous_layout(&lsc, 1, &one);
+  /* scale = Tensor::from_f32(&[1.0 / (d_k as f32).sqrt()], [1]) */
+  const float scale = 1.0f / sqrtf((float)Dk);
+  float* kT = falloc(N * Dk * S);
+  float* raw = falloc(N * S * S);
+  transpose_last2(k, N, S, Dk, kT); /* k.transpose(2, 3) */
+  int rc = vo_matmul(q, &lq, kT, &lkT, raw, err, errlen);
+  free(kT);
+  if (rc == VO_OK) rc = vo_binary(2, raw, &ls, &scale, &lsc, mask ? raw : scores, &ls, err, errlen); /* .mul(&scale) */
+  if (rc == VO_OK && mask) rc = vo_binary(0, raw, &ls, mask, ml, scores, &ls, err, errlen);         /* .add(m) */
+  free(raw);
+  if (rc == VO_OK) rc = vo_softmax(scores, &ls, 3, probs, err, errlen); /* .softmax(3) */
+  return rc;
+}
+
+int vo_attention_unfused(const float* q, const float* k, const float* v, int64_t B, int64_t H, int64_t S,
+                         int64_t Dk, const float* mask, const vo_layout* ml, float* out, char* err, size_t errlen) {
+  const int64_t N = B * H;
+  vo_layout ls, lv;
+  lay4(&ls, B, H, S, S);
+  lay4(&lv, B, H, S, Dk);
+  float* scores = falloc(N * S * S);
+  float* probs = falloc(N * S * S);
+  int rc = unfused_scores(q, k, B, H, S, Dk, mask, ml, scores, probs, err, errlen);
+  free(scores);
+  if (rc == VO_OK) rc = vo_matmul(probs, &ls, v, &lv, out, err, errlen); /* probs.matmul(&v) */
+  free(probs);
+  return rc;
+}
+
+/* The tape of the unfused path walked back (autograd:429-760): the Matmul arm
+ * of probs.matmul(v) (autograd:503-515: go.matmul(v^T), probs^T.matmul(go)),
+ * the Softmax arm on the saved scores (547-553), the Add arm (the mask's
+ * share is dropped: the mask needs no gradient), the Mul arm (go.mul(scale)),
+ * the Matmul arm of q.matmul(k^T) and the Transpose arm back to k's layout. */
+int vo_attention_unfused_backward(const float* q, const float* k, const float* v, int64_t B, int64_t H,
+                                  int64_t S, int64_t Dk, const float* mask, const vo_layout* ml, const float* go,
+                                  float* dq, float* dk, float* dv, char* err, size_t errlen) {
+  const int64_t N = B * H;
+  vo_layout ls, lv, lvT, lkT, lsc;
+  lay4(&ls, B, H, S, S);
+  lay4(&lv, B, H, S, Dk);
+  lay4(&lvT, B, H, Dk, S);
+  lay4(&lkT, B, H, Dk, S);
+  const int64_t one = 1;
+  vo_contiguous_layout(&lsc, 1, &one);
+  const float scale = 1.0f / sqrtf((float)Dk);
+  float* scores = falloc(N * S * S);
+  float* probs = falloc(N * S * S);
+  float *tmp = NULL, *g = NULL, *gs = NULL;
+  int rc = unfused_scores(q, k, B, H, S, Dk, mask, ml, scores, probs, err, errlen);
+  if (rc != VO_OK) goto out;
+  /* probs.matmul(v): d probs = go.matmul(v^T), dv = probs^T.matmul(go).
+   * tmp holds [S, S] or [Dk, S] blocks: v^T, probs^T, then (as gs) the
+   * scores' gradient and k_t's. */
+  tmp = falloc(N * S * (S > Dk ? S : Dk));
+  g = falloc(N * S * S);
+  transpose_last2(v, N, S, Dk, tmp);
+  rc = vo_matmul(go, &lv, tmp, &lvT, g, err, errlen);
+  if (rc != VO_OK) goto out;
+  transpose_last2(probs, N, S, S, tmp);
+  rc = vo_matmul(tmp, &ls, go, &lv, dv, err, errlen);
+  if (rc != VO_OK) goto out;
+  free(probs);
+  probs = NULL;
+  /* Softmax arm on the saved input, then the Add arm (identity for scores). */
+  gs = tmp;
+  tmp = NULL;
+  rc = vo_softmax_backward_composite(scores, g, &ls, 3, gs, err, errlen);
+  if (rc != VO_OK) goto out;
+  /* Mul arm: d raw = d scores .mul(scale) */
+  rc = vo_binary(2, gs, &ls, &scale, &lsc, g, &ls, err, errlen);
+  if (rc != VO_OK) goto out;
+  /* q.matmul(k_t): dq = g.matmul(k_t^T = k), d k_t = q^T.matmul(g) */
+  rc = vo_matmul(g, &ls, k, &lv, dq, err, errlen);
+  if (rc != VO_OK) goto out;
+  tmp = falloc(N * Dk * S);
+  transpose_last2(q, N, S, Dk, tmp);
+  rc = vo_matmul(tmp, &lkT, g, &ls, gs, err, errlen); /* [B, H, Dk, S] into gs's storage */
+  if (rc != VO_OK) goto out;
+  transpose_last2(gs, N, Dk, S, dk); /* Transpose arm: back to [B, H, S, Dk] */
+out:
+  free(scores);
+  free(probs);
+  free(tmp);
+  free(g);
+  free(gs);
+  return rc;
+}
+
 /* ---------------------------------------------------------------- AdamW -- */
 
 /* f32::powi(t) lowers to compiler-rt's __powisf2: binary exponentiation. */
@@ -564,6 +682,11 @@ static void heads_split(const float* src, int64_t B, int64_t S, int64_t H, int64
 
 int vo_gpt_step(const vo_gpt_config* cfg, const float* const* P, const float* ids, const float* targets,
                 float* loss, float* const* G, char* err, size_t errlen) {
+  return vo_gpt_step_ex(cfg, P, ids, targets, 0, loss, G, err, errlen);
+}
+
+int vo_gpt_step_ex(const vo_gpt_config* cfg, const float* const* P, const float* ids, const float* targets,
+                   int unfused, float* loss, float* const* G, char* err, size_t errlen) {
   const int64_t B = cfg->B, S = cfg->S, D = cfg->D, H = cfg->H, F = cfg->F, V = cfg->V;
   const int64_t R = B * S, Dk = D / H;
   const float eps = 1e-5f;
@@ -603,7 +726,10 @@ int vo_gpt_step(const vo_gpt_config* cfg, const float* const* P, const float* id
   heads_split(q, B, S, H, Dk, qh, 0);
   heads_split(k, B, S, H, Dk, kh, 0);
   heads_split(v, B, S, H, Dk, vh, 0);
-  vo_fused_attention(qh, kh, vh, B, H, S, Dk, mask, &lmask, atth);
+  if (unfused)
+    TRY(rc = vo_attention_unfused(qh, kh, vh, B, H, S, Dk, mask, &lmask, atth, err, errlen));
+  else
+    vo_fused_attention(qh, kh, vh, B, H, S, Dk, mask, &lmask, atth);
   heads_split(atth, B, S, H, Dk, att, 1);
   linear_fwd(att, R, D, P[VO_P_O_W], D, P[VO_P_O_B], o);
   add_into(h1, h0, o, R * D);
@@ -655,7 +781,11 @@ int vo_gpt_step(const vo_gpt_config* cfg, const float* const* P, const float* id
   dqh = falloc(R * D);
   dkh = falloc(R * D);
   dvh = falloc(R * D);
-  vo_fused_attention_backward(qh, kh, vh, B, H, S, Dk, mask, &lmask, datth, dqh, dkh, dvh);
+  if (unfused)
+    TRY(rc = vo_attention_unfused_backward(qh, kh, vh, B, H, S, Dk, mask, &lmask, datth, dqh, dkh, dvh, err,
+                                           errlen));
+  else
+    vo_fused_attention_backward(qh, kh, vh, B, H, S, Dk, mask, &lmask, datth, dqh, dkh, dvh);
   dq = falloc(R * D);
   dk = falloc(R * D);
   dv = falloc(R * D);

@@ -130,6 +130,17 @@ int vo_fused_attention_backward(const float* q, const float* k, const float* v, 
                                 const vo_layout* ml, const float* go, float* dq, float* dk,
                                 float* dv);
 
+/* The unfused attention of MultiHeadAttention::forward with
+ * VEARO_USE_FUSED_ATTENTION=0 (nn:603-613): scores = q.matmul(k^T).mul(scale)
+ * (+ mask), probs = scores.softmax(3), out = probs.matmul(v), each op the CPU
+ * backend's own; the backward walks that tape's arms (Matmul, Softmax, Add,
+ * Mul, Matmul, Transpose; autograd:474-599). Same layouts as the fused form. */
+int vo_attention_unfused(const float* q, const float* k, const float* v, int64_t B, int64_t H, int64_t S,
+                         int64_t Dk, const float* mask, const vo_layout* ml, float* out, char* err, size_t errlen);
+int vo_attention_unfused_backward(const float* q, const float* k, const float* v, int64_t B, int64_t H,
+                                  int64_t S, int64_t Dk, const float* mask, const vo_layout* ml, const float* go,
+                                  float* dq, float* dk, float* dv, char* err, size_t errlen);
+
 /* Tensor::adamw_step on one parameter (tensor.rs:931-986), t >= 1. */
 void vo_adamw_step(float* p, const float* g, float* m, float* v, int64_t n, int t, float lr,
                    float beta1, float beta2, float eps, float wd);
@@ -154,6 +165,11 @@ void vo_gpt_param_numel(const vo_gpt_config* c, int64_t* numel);
  * model's own [S, S] tensor with -1e9 above the diagonal (nn:763-771). */
 int vo_gpt_step(const vo_gpt_config* c, const float* const* params, const float* ids,
                 const float* targets, float* loss, float* const* grads, char* err, size_t errlen);
+/* The same step with the attention on the unfused path when `unfused` is
+ * nonzero (VEARO_USE_FUSED_ATTENTION=0, nn:603-613). */
+int vo_gpt_step_ex(const vo_gpt_config* c, const float* const* params, const float* ids,
+                   const float* targets, int unfused, float* loss, float* const* grads, char* err,
+                   size_t errlen);
 
 /* `.ve` weight checkpoint (crates/vearo/src/checkpoint.rs:9-91), host tensors. */
 int vo_checkpoint_save(const char* path, int n, const float* const* data, const vo_layout* layouts, char* err,

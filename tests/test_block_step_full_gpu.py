@@ -22,8 +22,7 @@ CFG = (16, 1024, 768, 12, 3072, 50257, 1024)
 ADAM = (0.02, 0.9, 0.95, 1e-8, 0.01)  # verification_harness.rs:203-210
 
 
-def test_block_step_full_size_matches_oracle(vh):
-    from vearo_amd import _block
+def full_model():
     B, S, D, H, F, V, P = CFG
     r = np.random.default_rng(0x5EED0000 + 4)
     params = []
@@ -36,6 +35,12 @@ def test_block_step_full_size_matches_oracle(vh):
             params.append(r.standard_normal(sh, dtype=np.float32) * np.float32(0.02))
     ids = r.integers(0, V, size=(B, S)).astype(np.float32)
     tg = r.integers(0, V, size=(B, S)).astype(np.float32)
+    return params, ids, tg
+
+
+def test_block_step_full_size_matches_oracle(vh):
+    from vearo_amd import _block
+    params, ids, tg = full_model()
 
     g = _block.Gpt(_block.GptConfig(*CFG))
     g.set_params(params)
@@ -86,4 +91,37 @@ def test_block_step_full_size_matches_oracle(vh):
     oloss1, _ = O.gpt_step(O.GptConfig(*CFG), params, ids, tg, grads=False)
     print(f"oracle forward after AdamW {time.perf_counter() - t0:.1f} s: loss1 {oloss1:.7f}", flush=True)
     assert abs(loss1 - oloss1) <= 1e-4 * abs(oloss1), (loss1, oloss1)
+    assert abs(dloss1 - oloss1) <= 1e-4 * abs(oloss1), (dloss1, oloss1)
+
+
+def test_block_step_full_size_unfused_attention(vh):
+    """The drop-in step with MultiHeadAttention's unfused path
+    (VEARO_USE_FUSED_ATTENTION=0, nn:603-613) at the real size: the [16, 12,
+    1024, 1024] scores go through the matmul, mul, add and softmax slots, and
+    back through the Softmax arm's five slot calls. Step-0 loss, every
+    gradient elementwise and the loss after AdamW against the oracle's unfused
+    step on the same inputs."""
+    from vearo_amd import _block
+    params, ids, tg = full_model()
+    d = _block.DropIn(_block.GptConfig(*CFG), fused_attention=False)
+    d.set_params(params)
+    d.set_inputs(ids, tg)
+    dloss0 = d.step(backward=True, adamw=True, lr=ADAM[0], beta1=ADAM[1], beta2=ADAM[2], eps=ADAM[3], wd=ADAM[4])
+    dgrads = d.grads()
+    dloss1 = d.step(backward=False)
+    d.close()
+    print(f"drop-in unfused: loss0 {dloss0:.7f} loss1 {dloss1:.7f}", flush=True)
+    t0 = time.perf_counter()
+    oloss0, ograds = O.gpt_step(O.GptConfig(*CFG), params, ids, tg, fused_attention=False)
+    print(f"oracle unfused forward+backward {time.perf_counter() - t0:.1f} s: loss0 {oloss0:.7f}", flush=True)
+    assert abs(dloss0 - oloss0) <= 1e-4 * abs(oloss0), (dloss0, oloss0)
+    for i, dg in enumerate(dgrads):
+        if O.GPT_PARAM_NAMES[i] == "k_b":
+            assert np.abs(dg).max() < 1e-6
+            continue
+        assert_parity(dg, ograds[i], name=f"full-size unfused drop-in grad {O.GPT_PARAM_NAMES[i]}")
+    for p, gr in zip(params, ograds):
+        O.adamw_step(p, gr, np.zeros_like(p), np.zeros_like(p), 1, *ADAM)
+    oloss1, _ = O.gpt_step(O.GptConfig(*CFG), params, ids, tg, grads=False, fused_attention=False)
+    print(f"oracle unfused loss1 {oloss1:.7f}", flush=True)
     assert abs(dloss1 - oloss1) <= 1e-4 * abs(oloss1), (dloss1, oloss1)

@@ -1,6 +1,7 @@
 """The config[4] step issued op by op through the BackendOps mirror
 (vb_dropin_*, include/vearo_block.h): the tape SimpleGPT::forward records
-(crates/vearo-nn/src/lib.rs:584-621, 666-675, 745-791), walked in reverse
+(crates/vearo-nn/src/lib.rs:584-621, 666-675, 745-791; the attention on its
+fused path or, as with VEARO_USE_FUSED_ATTENTION=0, its unfused one), walked in reverse
 through backward_impl's arms (crates/vearo-autograd/src/lib.rs:429-792), then
 AdamW::step (crates/vearo-optim/src/lib.rs:105-123). Against the oracle's
 SimpleGPT step and the golden float64 torch model: the loss, every parameter
@@ -70,7 +71,8 @@ def test_dropin_medium_model_matches_oracle_and_fused_driver(vh):
     d.set_inputs(ids, tg)
     loss = d.step(backward=True, timing=True)
     ph = d.phase_ms()
-    assert len(ph) == 19 and all(v >= 0 for v in ph.values()) and ph["fwd.matmul"] > 0
+    assert len(ph) == 23 and all(v >= 0 for v in ph.values()) and ph["fwd.matmul"] > 0
+    assert ph["fwd.softmax"] == 0 and ph["bwd.softmax"] == 0  # the fused path
     assert ph["bwd.reduce_to"] > 0 and ph["bwd.grad_accumulate"] > 0, ph
     grads = d.grads()
     oloss, ograds = O.gpt_step(O.GptConfig(*cfg), params, ids, tg)
@@ -99,6 +101,72 @@ def test_dropin_medium_model_matches_oracle_and_fused_driver(vh):
     oloss2, _ = O.gpt_step(O.GptConfig(*cfg), ps, ids, tg, grads=False)
     assert abs(loss2 - oloss2) <= 1e-5 + 1e-4 * abs(oloss2), (loss2, oloss2)
     d.close()
+
+
+def test_dropin_unfused_attention(vh):
+    """MultiHeadAttention's unfused path (VEARO_USE_FUSED_ATTENTION=0,
+    crates/vearo-nn/src/lib.rs:603-613): scores through the matmul, mul, add
+    and softmax slots, the backward through the Matmul, Softmax (five slot
+    calls, autograd:547-553), Add, Mul and Transpose arms. Golden and medium
+    models against the oracle's unfused step (and the golden float64 model),
+    the losses after AdamW, and the environment switch itself."""
+    from vearo_amd import _block
+    cfg = tuple(int(x) for x in GOLD["gpt_cfg"])
+    params = [GOLD[f"gpt_p{i}"] for i in range(21)]
+    ids, tg = GOLD["gpt_ids"], GOLD["gpt_targets"]
+    d = _block.DropIn(_block.GptConfig(*cfg), fused_attention=False)
+    assert not d.fused_attention
+    d.set_params(params)
+    d.set_inputs(ids, tg)
+    loss = d.step(backward=True)
+    oloss, ograds = O.gpt_step(O.GptConfig(*cfg), params, ids, tg, fused_attention=False)
+    assert abs(loss - oloss) <= 1e-5 + 1e-4 * abs(oloss), (loss, oloss)
+    assert abs(loss - GOLD["gpt_loss"]) <= 1e-4 * GOLD["gpt_loss"]
+    check_grads(d.grads(), ograds, [GOLD[f"gpt_g{i}"] for i in range(21)], "dropin unfused golden")
+    d.set_params(params)
+    d.step(backward=True, adamw=True)
+    loss1 = d.step(backward=False)
+    oloss1, _ = O.gpt_step(O.GptConfig(*cfg), adam_ref(params, ograds), ids, tg, grads=False, fused_attention=False)
+    assert abs(loss1 - oloss1) <= 1e-5 + 1e-4 * abs(oloss1), (loss1, oloss1)
+    d.close()
+
+    cfg = (2, 128, 128, 4, 512, 1000, 128)
+    print("dropin unfused medium", flush=True)
+    params, ids, tg = random_model(cfg, 13)
+    d = _block.DropIn(_block.GptConfig(*cfg), fused_attention=False)
+    d.set_params(params)
+    d.set_inputs(ids, tg)
+    loss = d.step(backward=True, timing=True)
+    ph = d.phase_ms()
+    assert ph["fwd.fused_attention"] == 0 and ph["bwd.fused_attention"] == 0, ph
+    for k in ("fwd.mul", "fwd.softmax", "bwd.mul", "bwd.softmax"):
+        assert ph[k] > 0, (k, ph)
+    oloss, ograds = O.gpt_step(O.GptConfig(*cfg), params, ids, tg, fused_attention=False)
+    assert abs(loss - oloss) <= 1e-5 + 1e-4 * abs(oloss), (loss, oloss)
+    check_grads(d.grads(), ograds, tag="dropin unfused medium")
+    d.step(backward=True, adamw=True, want_loss=False)
+    loss1 = d.step(backward=False)
+    oloss1, _ = O.gpt_step(O.GptConfig(*cfg), adam_ref(params, ograds), ids, tg, grads=False, fused_attention=False)
+    assert abs(loss1 - oloss1) <= 1e-5 + 1e-4 * abs(oloss1), (loss1, oloss1)
+    d.close()
+
+    # The reference's switch: the fused path unless the variable is "0" or "false".
+    old = os.environ.get("VEARO_USE_FUSED_ATTENTION")
+    try:
+        for val, fused in (("0", False), ("false", False), ("1", True), ("no", True)):
+            os.environ["VEARO_USE_FUSED_ATTENTION"] = val
+            d = _block.DropIn(_block.GptConfig(*cfg))
+            assert d.fused_attention == fused, val
+            d.close()
+        del os.environ["VEARO_USE_FUSED_ATTENTION"]
+        d = _block.DropIn(_block.GptConfig(*cfg))
+        assert d.fused_attention
+        d.close()
+    finally:
+        if old is None:
+            os.environ.pop("VEARO_USE_FUSED_ATTENTION", None)
+        else:
+            os.environ["VEARO_USE_FUSED_ATTENTION"] = old
 
 
 def test_dropin_errors(vh):

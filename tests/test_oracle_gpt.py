@@ -12,7 +12,8 @@ step) before it is trusted as the GPU checker.
   gradient, and the loss after one AdamW step.
 * Exact identities: integer matmuls are exact; the AVX2 fused-multiply-add
   block and the scalar fmaf chain give bit-identical elements; AdamW's first
-  step has a closed form.
+  step has a closed form; the unfused attention equals its chain of single
+  oracle ops bit for bit.
 """
 import math
 import os
@@ -115,6 +116,40 @@ def test_attention_fused_matches_unfused_composite():
     assert np.abs(dv - dv_ref).max() < 1e-4
 
 
+def _unfused_chain(q, k, v, mask, go):
+    """MultiHeadAttention's unfused path (nn:603-613) and its tape's arms,
+    spelled out with the oracle's single ops (as the fused parity test does)."""
+    scale = np.float32([1.0 / math.sqrt(q.shape[-1])])
+    s_scaled = O.binary(2, O.matmul(q, np.ascontiguousarray(np.swapaxes(k, 2, 3))), scale)
+    scores = O.binary(0, s_scaled, mask) if mask is not None else s_scaled
+    p = O.softmax(scores, 3)
+    out = O.matmul(p, v)
+    dp = O.matmul(go, np.ascontiguousarray(np.swapaxes(v, 2, 3)))
+    dv = O.matmul(np.ascontiguousarray(np.swapaxes(p, 2, 3)), go)
+    dqk = O.binary(2, O.softmax_backward_composite(scores, dp, 3), scale)
+    dq = O.matmul(dqk, k)
+    dk = np.swapaxes(O.matmul(np.ascontiguousarray(np.swapaxes(q, 2, 3)), dqk), 2, 3)
+    return out, dq, dk, dv
+
+
+@pytest.mark.parametrize("tag", ["attkat", "attc", "attm", "attn"])
+def test_attention_unfused_is_the_op_chain(tag):
+    """vo_attention_unfused(_backward) run exactly the single ops of the chain
+    (same bits), and land on the float64 torch attention within the bar."""
+    q, k, v, go = (GOLD[f"{tag}_{n}"] for n in ("q", "k", "v", "go"))
+    mask = GOLD[f"{tag}_mask"] if f"{tag}_mask" in GOLD.files else None
+    out = O.attention_unfused(q, k, v, mask)
+    dq, dk, dv = O.attention_unfused_backward(q, k, v, mask, go)
+    ref = _unfused_chain(q, k, v, mask, go)
+    for name, got, want in zip(("out", "dq", "dk", "dv"), (out, dq, dk, dv), ref):
+        np.testing.assert_array_equal(got, want, err_msg=f"{tag} {name}")
+    if tag != "attkat":
+        for name, got in (("out", out), ("dq", dq), ("dk", dk), ("dv", dv)):
+            g = GOLD[f"{tag}_{name}"]
+            np.testing.assert_allclose(got, g, rtol=1e-4, atol=1e-5 * max(1.0, np.abs(g).max()),
+                                       err_msg=f"{tag} {name} vs float64")
+
+
 def test_attention_rows_are_convex_combinations():
     # With v = identity-like one-hot rows, out rows are the probability rows:
     # non-negative, summing to 1, zero above the diagonal under the causal mask.
@@ -184,6 +219,24 @@ def test_gpt_step_matches_float64_model():
     loss1, _ = O.gpt_step(cfg, params, ids, tg, grads=False)
     assert abs(loss1 - GOLD["gpt_loss1"]) <= 1e-4 * abs(GOLD["gpt_loss1"]), (loss1, GOLD["gpt_loss1"])
     assert loss1 < loss
+
+
+def test_gpt_step_unfused_attention_matches_float64_model():
+    """The step with VEARO_USE_FUSED_ATTENTION=0's path: the same float64
+    model (the two attention forms are the same mathematics), loss and every
+    gradient to the same bar as the fused step, and close to the fused step."""
+    cfg, params, ids, tg = _gpt_from_gold("gpt")
+    loss, grads = O.gpt_step(cfg, params, ids, tg, fused_attention=False)
+    floss, fgrads = O.gpt_step(cfg, params, ids, tg)
+    assert abs(loss - GOLD["gpt_loss"]) <= 1e-5 * abs(GOLD["gpt_loss"])
+    assert abs(loss - floss) <= 1e-5 * abs(floss)
+    for i, name in enumerate(O.GPT_PARAM_NAMES):
+        ref = GOLD[f"gpt_g{i}"]
+        if name == "k_b":
+            assert np.abs(grads[i]).max() < 1e-6
+            continue
+        assert np.abs(grads[i] - ref).max() / np.abs(ref).max() < 1e-4, name
+        assert np.abs(grads[i] - fgrads[i]).max() / np.abs(ref).max() < 1e-4, name
 
 
 def test_gpt_overfits_like_the_reference_test():

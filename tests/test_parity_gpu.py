@@ -336,6 +336,30 @@ def test_binary_row_broadcast(vh):
 
 
 
+def test_binary_block_scalar_and_column_broadcast(vh):
+    """The other broadcast streams the unfused attention and the Softmax arm
+    drive: a vector over the output's trailing dims (the [S, S] mask on [B, H,
+    S, S] scores), a single value (the scale), and a vector over the leading
+    dims with size-1 trailing dims (dy - sum(dy * y, keep_dim)); both operand
+    orders, every op, 16-byte and 4-byte units, the same bits as the oracle's
+    broadcast rule (cpu:160-238)."""
+    r = rng(17)
+    cases = [((2, 3, 64, 64), (64, 64)), ((2, 3, 64, 64), (1, 1, 64, 64)), ((2, 3, 64, 64), (1,)),
+             ((5, 7, 33), ()), ((2, 3, 64, 64), (2, 3, 64, 1)), ((4, 9, 30), (4, 9, 1)), ((6, 10), (6, 1)),
+             ((3, 5, 8), (5, 8)), ((3, 5, 7), (3, 1, 1))]
+    for fs, vs in cases:
+        f = r.normal(size=fs).astype(np.float32)
+        v = (r.normal(size=vs) + 3).astype(np.float32)
+        F, Vd = dev(vh, f), dev(vh, v)
+        for op in range(4):
+            for left in (False, True):
+                OUT = out(vh, fs)
+                a, al, b, bl = (Vd, v.shape, F, f.shape) if left else (F, f.shape, Vd, v.shape)
+                vh.check(vh.lib.vh_binary(op, a.ptr, vh.layout(al), b.ptr, vh.layout(bl), OUT.ptr, None))
+                want = O.binary(op, v, f) if left else O.binary(op, f, v)
+                np.testing.assert_array_equal(fetch(vh, OUT, fs), want, err_msg=f"{fs} {vs} op={op} left={left}")
+
+
 def test_binary_broadcast_and_strided(vh):
     r = rng(6)
     cases = [((64, 3072), (3072,)), ((3, 1, 5), (4, 1)), ((16, 12, 128, 128), (16, 12, 128, 1)),

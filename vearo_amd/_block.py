@@ -48,6 +48,8 @@ def _load():
         "vb_gpt_set_gemm_engine": (c_int, [H, c_int]),
         "vb_dropin_create": (c_int, [POINTER(GptConfig), POINTER(c_void_p)]),
         "vb_dropin_destroy": (None, [H]),
+        "vb_dropin_set_fused_attention": (c_int, [H, c_int]),
+        "vb_dropin_fused_attention": (c_int, [H]),
         "vb_dropin_set_param": (c_int, [H, c_int, c_void_p, c_int64]),
         "vb_dropin_get_param": (c_int, [H, c_int, c_void_p, c_int64]),
         "vb_dropin_get_grad": (c_int, [H, c_int, c_void_p, c_int64]),
@@ -156,7 +158,7 @@ class Gpt:
             pass
 
 
-DROPIN_NPHASES = 19
+DROPIN_NPHASES = 23
 
 
 class DropIn:
@@ -164,12 +166,20 @@ class DropIn:
     table in the reference's own order (SimpleGPT::forward's tape, then
     backward_impl's arms, then AdamW::step): include/vearo_block.h vb_dropin_*."""
 
-    def __init__(self, cfg: GptConfig):
+    def __init__(self, cfg: GptConfig, fused_attention=None):
+        """fused_attention: None keeps the reference's switch (the environment
+        variable VEARO_USE_FUSED_ATTENTION), True / False force the path."""
         self.cfg = cfg
         h = c_void_p()
         check(lib.vb_dropin_create(ctypes.byref(cfg), ctypes.byref(h)))
         self.h = h
         self.shapes = param_shapes(cfg)
+        if fused_attention is not None:
+            check(lib.vb_dropin_set_fused_attention(self.h, int(bool(fused_attention))))
+
+    @property
+    def fused_attention(self) -> bool:
+        return bool(lib.vb_dropin_fused_attention(self.h))
 
     def set_params(self, params) -> None:
         for i, a in enumerate(params):

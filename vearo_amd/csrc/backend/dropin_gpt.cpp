@@ -3,8 +3,11 @@
 //
 //   forward   SimpleGPT::forward (crates/vearo-nn/src/lib.rs:745-791) with one
 //             TransformerBlock::forward (nn:666-675), MultiHeadAttention::forward
-//             on its default fused path (nn:584-621) and Linear::forward
-//             (nn:119-127). Every Tensor op with an input that needs a gradient
+//             (nn:584-621) on its default fused path or, as the reference does
+//             with VEARO_USE_FUSED_ATTENTION=0 (read at create, or set with
+//             vb_dropin_set_fused_attention), its unfused path: q.matmul(k^T)
+//             .mul(scale).add(mask).softmax(3).matmul(v) (nn:603-613), and
+//             Linear::forward (nn:119-127). Every Tensor op with an input that needs a gradient
 //             records a tape node holding its inputs; a parameter becomes a leaf
 //             node on first use (Tape::push, autograd lib.rs:150-188).
 //   backward  loss.backward(): the tape walked in reverse with the arms of
@@ -19,8 +22,9 @@
 // reduce_to as `sum` slot calls, the Gelu arm's mask-and-multiply as one
 // vh_gelu_grad_mul, adamw_step as vh_adamw_step -- what a HIP-aware autograd and
 // optimizer would issue. The position ids, the causal mask (-1e9 above the
-// diagonal, nn:763-771) and the backward's seed gradient 1.0 (autograd:795-798)
-// are device tensors built once instead of host tensors built every call.
+// diagonal, nn:763-771), the unfused path's scale 1/sqrt(d_k) (nn:606) and the
+// backward's seed gradient 1.0 (autograd:795-798) are device tensors built
+// once instead of host tensors built every call.
 // Gradients of interior nodes and the tape's saved inputs are released as the
 // walk passes them (the reference holds them to the end of backward_impl).
 //
@@ -29,6 +33,8 @@
 // included), so the phases add up to the step.
 #include <hip/hip_runtime_api.h>
 
+#include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <exception>
 #include <string>
@@ -47,7 +53,7 @@ namespace {
 enum Phase : int {
   F_EMBED, F_LN, F_MATMUL, F_ADD, F_COPY, F_ATTN, F_GELU, F_XENT,
   B_XENT, B_MATMUL, B_REDUCE, B_ACC, B_COPY, B_LN, B_ATTN, B_GELU, B_EMBED,
-  O_CONTIG, O_ADAMW, NPHASE
+  O_CONTIG, O_ADAMW, F_MUL, F_SOFTMAX, B_MUL, B_SOFTMAX, NPHASE
 };
 static_assert(NPHASE == VB_DROPIN_NPHASES, "phase table");
 
@@ -56,17 +62,19 @@ const char* const kPhase[NPHASE] = {
     "fwd.reshape_copy",   "fwd.fused_attention", "fwd.gelu",             "fwd.cross_entropy",
     "bwd.cross_entropy",  "bwd.matmul",          "bwd.reduce_to",        "bwd.grad_accumulate",
     "bwd.reshape_copy",   "bwd.layernorm",       "bwd.fused_attention",  "bwd.gelu",
-    "bwd.embedding",      "adamw.grad_contiguous", "adamw.update"};
+    "bwd.embedding",      "adamw.grad_contiguous", "adamw.update",       "fwd.mul",
+    "fwd.softmax",        "bwd.mul",             "bwd.softmax"};
 
 constexpr float kEps = 1e-5f;  // LayerNorm::new(n_embd, 1e-5) (nn:652, 742)
 
-enum class Op { Leaf, Add, Matmul, Reshape, Transpose, Gelu, LayerNorm, Embedding, CrossEntropy, Attention };
+enum class Op { Leaf, Add, Mul, Matmul, Reshape, Transpose, Gelu, Softmax, LayerNorm, Embedding, CrossEntropy,
+                Attention };
 
 struct Node {
   Op op = Op::Leaf;
   std::vector<int> in;        // tape index per input; -1: no gradient flows there
   std::vector<Tensor> saved;  // the inputs (empty for a leaf)
-  int d0 = 0, d1 = 0;         // Transpose dims
+  int d0 = 0, d1 = 0;         // Transpose dims; Softmax: d0 = dim
 };
 
 // A tensor and its tape node; `rg` mirrors requires_grad.
@@ -85,7 +93,8 @@ void hip_check(hipError_t e, const char* what) {
 struct vb_dropin {
   vb_gpt_config c{};
   std::vector<Tensor> P, G, M, V;  // parameters, last gradients, AdamW moments
-  Tensor ids, tg, pos, mask, seed;
+  Tensor ids, tg, pos, mask, seed, scale;
+  bool fused_attention = true;  // MultiHeadAttention's path (nn:603-613)
   int t = 0;
   std::vector<Var> pv;
   std::vector<Node> tape;
@@ -158,6 +167,16 @@ struct vb_dropin {
     mark(F_MATMUL);
     return rec(o, Op::Matmul, {&a, &b});
   }
+  Var mul(Var& a, Var& b) {
+    Tensor o = a.t.mul(b.t);
+    mark(F_MUL);
+    return rec(o, Op::Mul, {&a, &b});
+  }
+  Var softmax(Var& x, int dim) {
+    Tensor o = x.t.softmax((size_t)dim);
+    mark(F_SOFTMAX);
+    return rec(o, Op::Softmax, {&x}, dim);
+  }
   Var transpose(Var& a, int d0, int d1) { return rec(a.t.transpose(d0, d1), Op::Transpose, {&a}, d0, d1); }
   Var reshape(Var& a, const Shape& sh) {
     const bool copies = !a.t.is_contiguous();
@@ -201,7 +220,7 @@ struct vb_dropin {
     const int64_t B = c.B, S = c.S, D = c.D, H = c.H, Dk = c.D / c.H;
     pv.assign(P.size(), Var{});
     for (size_t i = 0; i < P.size(); ++i) pv[i] = Var{P[i], -1, true};
-    Var vids{ids}, vpos{pos}, vtg{tg}, vmask{mask};
+    Var vids{ids}, vpos{pos}, vtg{tg}, vmask{mask}, vscale{scale};
     // SimpleGPT::forward (nn:745-791)
     Var tok = embedding(vids, pv[0]);
     Var pe = embedding(vpos, pv[1]);
@@ -216,7 +235,17 @@ struct vb_dropin {
     Var qr = reshape(q, heads), q4 = transpose(qr, 1, 2);
     Var kr = reshape(k, heads), k4 = transpose(kr, 1, 2);
     Var vr = reshape(v, heads), v4 = transpose(vr, 1, 2);
-    Var a = attention(q4, k4, v4, vmask);
+    Var a;
+    if (fused_attention) {
+      a = attention(q4, k4, v4, vmask);
+    } else {  // nn:604-612
+      Var kt = transpose(k4, 2, 3);
+      Var raw = matmul(q4, kt);
+      Var scaled = mul(raw, vscale);
+      Var scores = add(scaled, vmask);
+      Var probs = softmax(scores, 3);
+      a = matmul(probs, v4);
+    }
     Var at = transpose(a, 1, 2);
     Var a3 = reshape(at, Shape{B, S, D});
     Var o = linear(a3, pv[10], &pv[11]);
@@ -274,6 +303,29 @@ struct vb_dropin {
           gin[0] = reduce_to(g, nd.saved[0].shape());
           gin[1] = reduce_to(g, nd.saved[1].shape());
           break;
+        case Op::Mul: {  // autograd:480-489
+          const Tensor gl = g.mul(nd.saved[1]);
+          mark(B_MUL);
+          const Tensor gr = g.mul(nd.saved[0]);
+          mark(B_MUL);
+          gin[0] = reduce_to(gl, nd.saved[0].shape());
+          gin[1] = reduce_to(gr, nd.saved[1].shape());
+          break;
+        }
+        case Op::Softmax: {  // autograd:547-553, y recomputed from the saved input
+          const size_t dim = (size_t)nd.d0;
+          const Tensor y = nd.saved[0].softmax(dim);
+          mark(B_SOFTMAX);
+          const Tensor gy = g.mul(y);
+          mark(B_SOFTMAX);
+          const Tensor sgy = gy.sum(dim, true);
+          mark(B_SOFTMAX);
+          const Tensor d = g.sub(sgy);
+          mark(B_SOFTMAX);
+          gin[0] = y.mul(d);
+          mark(B_SOFTMAX);
+          break;
+        }
         case Op::Matmul: {
           const Tensor& l = nd.saved[0];
           const Tensor& r = nd.saved[1];
@@ -428,6 +480,10 @@ int vb_dropin_create(const vb_gpt_config* cfg, vb_dropin** out) {
       for (int64_t j = r + 1; j < c.S; ++j) mask[(size_t)(r * c.S + j)] = -1e9f;
     d->mask = Tensor::from_f32(mask, Shape{c.S, c.S});
     d->seed = Tensor::from_f32({1.0f}, Shape{1});
+    d->scale = Tensor::from_f32({1.0f / std::sqrt((float)(c.D / c.H))}, Shape{1});
+    // nn:603: the fused path unless VEARO_USE_FUSED_ATTENTION is "0" or "false".
+    const char* env = std::getenv("VEARO_USE_FUSED_ATTENTION");
+    d->fused_attention = !(env && (std::strcmp(env, "0") == 0 || std::strcmp(env, "false") == 0));
   });
   if (rc != VH_OK) {
     delete d;
@@ -438,6 +494,14 @@ int vb_dropin_create(const vb_gpt_config* cfg, vb_dropin** out) {
 }
 
 void vb_dropin_destroy(vb_dropin* d) { delete d; }
+
+int vb_dropin_set_fused_attention(vb_dropin* d, int fused) {
+  if (!d) return vb_fail(VH_ERR_INVALID, "vb_dropin_set_fused_attention: null handle");
+  d->fused_attention = fused != 0;
+  return VH_OK;
+}
+
+int vb_dropin_fused_attention(const vb_dropin* d) { return d && d->fused_attention ? 1 : 0; }
 
 int vb_dropin_set_param(vb_dropin* d, int i, const float* host, int64_t numel) {
   if (!d || !host || i < 0 || i >= VB_GPT_NPARAMS) return vb_fail(VH_ERR_INVALID, "vb_dropin_set_param: bad argument");

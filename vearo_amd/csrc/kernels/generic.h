@@ -44,10 +44,11 @@ VH_DEV void binary_contig_impl(const BinaryArgs& a) {
 }
 
 // op(full, vec) or op(vec, full) with a contiguous vector of length bn
-// repeating along the rows of a contiguous full operand (a bias add): one unit
-// per thread over the whole output, streaming loads and stores of the full
-// operand, the vector read through the caches. VW divides bn, so a unit stays
-// within one row.
+// repeating along the rows of a contiguous full operand -- a bias add, the
+// attention mask [S, S] added to [B, H, S, S] scores, or a single value (bn =
+// 1: the unfused attention's scale): one unit per thread over the whole
+// output, streaming loads and stores of the full operand, the vector read
+// through the caches. VW divides bn (or bn = 1), so a unit stays within one row.
 template <int VW>
 VH_DEV void binary_rowbcast_impl(const BinaryArgs& a) {
   const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -55,10 +56,35 @@ VH_DEV void binary_rowbcast_impl(const BinaryArgs& a) {
   const float* full = a.vec_lhs ? a.r : a.l;
   const float* vec = a.vec_lhs ? a.l : a.r;
   const Unit<VW> f = load_stream<VW>(full + u * VW);
-  const Unit<VW> v = *reinterpret_cast<const Unit<VW>*>(vec + (u * VW) % a.bn);
+  Unit<VW> v;
+  if (a.bn == 1) {
+    const float s = vec[0];
+#pragma unroll
+    for (int j = 0; j < VW; ++j) v.v[j] = s;
+  } else {
+    v = *reinterpret_cast<const Unit<VW>*>(vec + (u * VW) % a.bn);
+  }
   Unit<VW> o;
 #pragma unroll
   for (int j = 0; j < VW; ++j) o.v[j] = a.vec_lhs ? apply_op(a.op, v.v[j], f.v[j]) : apply_op(a.op, f.v[j], v.v[j]);
+  store_stream<VW>(a.out + u * VW, o);
+}
+
+// op(full, vec) or op(vec, full) with each vector element repeating over bn
+// consecutive output elements (the vector spans the output's leading dims,
+// with size-1 trailing dims: the Softmax arm's dy - sum(dy * y, keep_dim)).
+// One unit per thread; VW divides bn, so a unit uses one vector element.
+template <int VW>
+VH_DEV void binary_colbcast_impl(const BinaryArgs& a) {
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (u >= a.n / VW) return;
+  const float* full = a.vec_lhs ? a.r : a.l;
+  const float* vec = a.vec_lhs ? a.l : a.r;
+  const Unit<VW> f = load_stream<VW>(full + u * VW);
+  const float s = vec[(u * VW) / a.bn];
+  Unit<VW> o;
+#pragma unroll
+  for (int j = 0; j < VW; ++j) o.v[j] = a.vec_lhs ? apply_op(a.op, s, f.v[j]) : apply_op(a.op, f.v[j], s);
   store_stream<VW>(a.out + u * VW, o);
 }
 

@@ -168,6 +168,8 @@ extern "C" __global__ void __launch_bounds__(256) vh_binary_contig_v1(BinaryArgs
 extern "C" __global__ void __launch_bounds__(256) vh_binary_contig_v4(BinaryArgs a) { binary_contig_impl<4>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_binary_rowbcast_v1(BinaryArgs a) { binary_rowbcast_impl<1>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_binary_rowbcast_v4(BinaryArgs a) { binary_rowbcast_impl<4>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_binary_colbcast_v1(BinaryArgs a) { binary_colbcast_impl<1>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_binary_colbcast_v4(BinaryArgs a) { binary_colbcast_impl<4>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_binary_strided_i32(BinaryArgs a) { binary_strided_impl<uint32_t>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_binary_strided_i64(BinaryArgs a) { binary_strided_impl<uint64_t>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_reduce_thread(ReduceArgs a) { reduce_thread_impl(a); }

@@ -1084,20 +1084,62 @@ int vh_binary(int op, const float* l, const vh_layout* ll, const float* r, const
     return launch(vec ? "vh_binary_contig_v4" : "vh_binary_contig_v1", (unsigned)blocks, 1, 256, 0, s, a);
   }
   // A contiguous operand covering the whole output and a contiguous vector
-  // over its last dim (a bias): the row-broadcast stream.
-  const int64_t N = ol.dims[R - 1];
+  // that repeats along it: over the output's trailing dims (a bias, the
+  // attention mask, or one value) -- the row-broadcast stream -- or over its
+  // leading dims with size-1 trailing dims (a kept-dim row sum) -- the
+  // column-broadcast stream. The vector's own leading (or trailing) size-1
+  // dims do not matter.
   auto covers = [&](const vh_layout* t) { return is_contig(t) && numel(t) == n; };
-  auto last_vec = [&](const vh_layout* t) {
-    return t->rank >= 1 && is_contig(t) && numel(t) == N && t->dims[t->rank - 1] == N;
+  // Elements per repeat of t over the output's trailing dims (0: not such a vector).
+  auto suffix_len = [&](const vh_layout* t) -> int64_t {
+    if (!is_contig(t)) return 0;
+    int lo = 0;
+    while (lo < t->rank && t->dims[lo] == 1) ++lo;
+    const int k = t->rank - lo;
+    if (k > R) return 0;
+    int64_t len = 1;
+    for (int i = 0; i < k; ++i) {
+      if (t->dims[lo + i] != ol.dims[R - k + i]) return 0;
+      len *= t->dims[lo + i];
+    }
+    return len;
   };
-  const bool rvec = covers(ll) && last_vec(rl), lvec = !rvec && covers(rl) && last_vec(ll);
-  if ((rvec || lvec) && N > 0 && n / N > 1 && cdiv(n, 256) < (int64_t(1) << 31)) {
-    a.bn = N;
-    a.vec_lhs = lvec ? 1 : 0;
-    const bool vec = N % 4 == 0 && aligned16(l) && aligned16(r) && aligned16(out);
-    const int vw = vec ? 4 : 1;
-    return launch(vec ? "vh_binary_rowbcast_v4" : "vh_binary_rowbcast_v1", (unsigned)cdiv(n / vw, 256), 1, 256, 0, s,
-                  a);
+  // Output elements per element of t when t spans the output's leading dims.
+  auto prefix_run = [&](const vh_layout* t) -> int64_t {
+    if (!is_contig(t)) return 0;
+    int hi = t->rank;
+    while (hi > 0 && t->dims[hi - 1] == 1) --hi;
+    const int off = R - t->rank;  // t right-aligned; its leading dims must be the output's
+    for (int i = 0; i < off; ++i)
+      if (ol.dims[i] != 1) return 0;
+    for (int i = 0; i < hi; ++i)
+      if (t->dims[i] != ol.dims[off + i]) return 0;
+    int64_t run = 1;
+    for (int i = off + hi; i < R; ++i) run *= ol.dims[i];
+    return run;
+  };
+  const bool small_grid = cdiv(n, 256) < (int64_t(1) << 31);
+  for (int side = 0; side < 2 && small_grid; ++side) {  // side 0: vector on the right
+    const vh_layout* full = side == 0 ? ll : rl;
+    const vh_layout* vt = side == 0 ? rl : ll;
+    if (!covers(full) || numel(vt) >= n) continue;
+    a.vec_lhs = side;
+    const int64_t bn = suffix_len(vt);
+    if (bn > 0 && n / bn > 1) {
+      a.bn = bn;
+      const bool vec = (bn % 4 == 0 || bn == 1) && n % 4 == 0 && aligned16(l) && aligned16(r) && aligned16(out);
+      const int vw = vec ? 4 : 1;
+      return launch(vec ? "vh_binary_rowbcast_v4" : "vh_binary_rowbcast_v1", (unsigned)cdiv(n / vw, 256), 1, 256, 0,
+                    s, a);
+    }
+    const int64_t run = prefix_run(vt);
+    if (run > 1) {
+      a.bn = run;
+      const bool vec = run % 4 == 0 && aligned16(full == ll ? l : r) && aligned16(out);
+      const int vw = vec ? 4 : 1;
+      return launch(vec ? "vh_binary_colbcast_v4" : "vh_binary_colbcast_v1", (unsigned)cdiv(n / vw, 256), 1, 256, 0,
+                    s, a);
+    }
   }
   const int64_t blocks = std::min<int64_t>(cdiv(n, 256), 16384);
   return launch(n < INT32_MAX ? "vh_binary_strided_i32" : "vh_binary_strided_i64", (unsigned)blocks, 1,

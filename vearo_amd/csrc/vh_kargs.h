@@ -308,8 +308,9 @@ struct BinaryArgs {
   int64_t n;
   int32_t op;        // 0 add, 1 sub, 2 mul, 3 div
   int32_t contiguous;
-  int64_t bn;        // row-broadcast form: the vector's length (the output's last dim)
-  int32_t vec_lhs;   // row-broadcast form: 1 when the vector is the left operand
+  int64_t bn;        // row-broadcast form: the vector's length (a product of the output's trailing
+                     // dims, or 1); column-broadcast form: output elements per vector element
+  int32_t vec_lhs;   // broadcast forms: 1 when the vector is the left operand
 };
 
 struct ReduceArgs {
