@@ -323,14 +323,20 @@ int vh_matmul(const float* lhs, const vh_layout* ll, const float* rhs,
 /* Scaled dot-product attention over [B, H, S, Dk] layouts (any strides, unit
  * stride on Dk): out = softmax(q k^T / sqrt(Dk) + mask) v, with the CPU fused
  * kernel's normalisation p = e * (1/(sum + 1e-9)). mask: NULL or any layout that
- * broadcasts right-aligned to [B, H, S, S] (additive). causal = 1 declares that
- * keys past the query are masked (as the model's -1e9 upper triangle does),
- * which skips their work; it may be combined with a mask. Replaces
+ * broadcasts right-aligned to [B, H, S, S] (additive). causal = 0 computes
+ * every block; causal = 1 declares that keys past the query are masked (as the
+ * model's -1e9 upper triangle does), which skips their work; it may be
+ * combined with a mask. causal = VH_ATTN_CAUSAL_AUTO (2) decides on the
+ * device, with no host wait: one pass over the mask and operands (the test of
+ * vh_attention_mask_is_causal) sets a flag that the launches read, so the
+ * masked blocks are skipped exactly when that gives the dense form's bits
+ * (without a mask AUTO is causal = 0). Replaces
  * BackendOps.fused_attention / fused_attention_backward (tensor.rs:1172-1174,
  * 1709-1739; cpu:2366-2630; the CUDA backend runs these on the CPU,
  * cuda:1595-1636). The backward recomputes the probabilities from q and k as
  * the reference does. scratch: NULL or
  * vh_fused_attention_scratch_bytes(B, H, S, backward) bytes (the score block). */
+#define VH_ATTN_CAUSAL_AUTO 2
 int vh_fused_attention_fwd(const float* q, const vh_layout* ql, const float* k,
                            const vh_layout* kl, const float* v, const vh_layout* vl,
                            const float* mask, const vh_layout* ml, int causal, float* out,
@@ -351,10 +357,11 @@ size_t vh_fused_attention_scratch_bytes(int64_t B, int64_t H, int64_t S, int bac
  * exceeds twice the largest score the product can form (scale * Dk *
  * max|q| * max|k|) by enough that every masked exp() underflows to exactly 0
  * -- so the skipped blocks would have contributed exact zeros. One pass over
- * the operands and the mask on `stream`, then a wait for the answer (the
- * call returns after the stream drains). No counterpart in the reference: the
- * BackendOps fused_attention slots call it so that a model's -1e9 triangle
- * (nn:763-771) takes the causal kernels. */
+ * the operands and the mask on `stream`, then a host wait for the answer: the
+ * call synchronizes `stream` and returns after it drains. On a stream under
+ * graph capture (where that wait is not allowed) it launches nothing and
+ * answers 0. No counterpart in the reference; the attention entries' causal =
+ * VH_ATTN_CAUSAL_AUTO makes the same decision on the device instead. */
 int vh_attention_mask_is_causal(const float* q, const vh_layout* ql, const float* k,
                                 const vh_layout* kl, const float* v, const vh_layout* vl,
                                 const float* dout, const vh_layout* dol, const float* mask,

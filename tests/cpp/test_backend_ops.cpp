@@ -398,9 +398,10 @@ int main() {
     CHECK(maxdiff(dv.to_vec_f32(), rv) < 1e-4, "dv");
   });
 
-  // The slot drops SimpleGPT's -1e9 triangle (nn:763-771) for the causal
-  // kernels only when vh_attention_mask_is_causal proves every masked exp()
-  // is exactly 0: then out, dq, dk and dv are the dense masked form's bits.
+  // The slot skips the blocks SimpleGPT's -1e9 triangle (nn:763-771) masks
+  // only when the device-side probe (VH_ATTN_CAUSAL_AUTO) proves every masked
+  // exp() is exactly 0: out, dq, dk and dv are the dense masked form's bits
+  // whichever form runs.
   run("fused_attention_causal_mask_same_bits", [] {
     const int B = 2, H = 3, S = 200, DK = 32, n = B * H * S * DK;
     const auto qv = randn(n, 71), kv = randn(n, 72), vv = randn(n, 73), gv = randn(n, 74);

@@ -446,11 +446,48 @@ def test_attention_mask_probe(vh, case, want):
         mask = np.zeros((1, S), np.float32)
     print("mask probe", case, flush=True)
     assert mask_is_causal(vh, q, k, v, mask, g) == want
+    gg = g if g is not None else go
+    dense = attention_gpu(vh, q, k, v, mask, 0, gg)
     if want:
-        dense = attention_gpu(vh, q, k, v, mask, 0, go)
-        causal = attention_gpu(vh, q, k, v, None, 1, go)
+        causal = attention_gpu(vh, q, k, v, None, 1, gg)
         for name, a, b in zip(("out", "dq", "dk", "dv"), dense, causal):
             np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32), err_msg=f"{case} {name}")
+    # VH_ATTN_CAUSAL_AUTO makes the same decision on the device (the launches
+    # read its flag): the dense masked form's bits whatever it decides.
+    auto = attention_gpu(vh, q, k, v, mask, 2, gg)
+    for name, a, b in zip(("out", "dq", "dk", "dv"), dense, auto):
+        np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32), err_msg=f"{case} auto {name}")
+
+
+def test_attention_mask_probe_under_graph_capture(vh):
+    """The host-answer probe needs a host wait, which a capturing stream does
+    not allow: there it answers 0 and launches nothing (the captured graph is
+    empty)."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so.7")
+    B, H, S, Dk = 1, 2, 64, 16
+    r = np.random.default_rng(5)
+    q, k, v = (r.standard_normal((B, H, S, Dk), dtype=np.float32) for _ in range(3))
+    tri = np.zeros((S, S), np.float32)
+    tri[np.triu_indices(S, 1)] = -1e9
+    assert mask_is_causal(vh, q, k, v, tri, None) == 1
+    Q, K, V, M = dev(vh, q), dev(vh, k), dev(vh, v), dev(vh, tri)
+    ql, ml = vh.layout(q.shape), vh.layout(tri.shape)
+    st = C.c_void_p()
+    assert hip.hipStreamCreate(C.byref(st)) == 0
+    vh.sync()
+    assert hip.hipStreamBeginCapture(st, 2) == 0  # relaxed mode
+    res = C.c_int(7)
+    rc = vh.lib.vh_attention_mask_is_causal(Q.ptr, C.byref(ql), K.ptr, C.byref(ql), V.ptr, C.byref(ql), None, None,
+                                            M.ptr, C.byref(ml), C.byref(res), st)
+    graph = C.c_void_p()
+    assert hip.hipStreamEndCapture(st, C.byref(graph)) == 0
+    nodes = C.c_size_t(99)
+    assert hip.hipGraphGetNodes(graph, None, C.byref(nodes)) == 0
+    hip.hipGraphDestroy(graph)
+    hip.hipStreamDestroy(st)
+    vh.check(rc)
+    assert res.value == 0 and nodes.value == 0
 
 
 @pytest.mark.parametrize("n", [4096, 1000003])

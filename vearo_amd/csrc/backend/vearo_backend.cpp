@@ -471,17 +471,11 @@ static void attention_checks(const Tensor& q, const Tensor& k, const Tensor& v) 
 // diagonal, at most -1 above) with scores small enough that every masked
 // exponent underflows to exactly 0 -- SimpleGPT's -1e9 mask (nn:763-771) with
 // any ordinary activations -- gives the same bits as the causal kernels,
-// which skip the masked blocks; vh_attention_mask_is_causal proves that per
-// call (one pass over the operands and the mask, and a wait for its answer).
-static int causal_mask(const Tensor& q, const vh_layout& ql, const Tensor& k, const vh_layout& kl, const Tensor& v,
-                       const vh_layout& vl, const Tensor* g, const vh_layout* gl, const float* mask,
-                       const vh_layout& ml) {
-  if (!mask) return 0;
-  int c = 0;
-  check(vh_attention_mask_is_causal(q.data(), &ql, k.data(), &kl, v.data(), &vl, g ? g->data() : nullptr, gl,
-                                    mask, &ml, &c, nullptr));
-  return c;
-}
+// which skip the masked blocks. With a mask the slots ask for
+// VH_ATTN_CAUSAL_AUTO: one pass over the operands and the mask proves that
+// per call on the device, and the launches choose their form from its flag
+// (no host wait).
+static int causal_mode(const float* mask) { return mask ? VH_ATTN_CAUSAL_AUTO : 0; }
 
 // cpu:2366-2464: softmax(q k^T / sqrt(Dk) + mask) v, mask broadcast from the right.
 Tensor fused_attention(const Tensor& q0, const Tensor& k0, const Tensor& v0, const Tensor* mask) {
@@ -493,10 +487,8 @@ Tensor fused_attention(const Tensor& q0, const Tensor& k0, const Tensor& v0, con
   vh_layout ml{};
   if (mask) ml = layout_of(*mask);
   const float* mp = mask ? mask->data() : nullptr;
-  const int causal = causal_mask(q, ql, k, kl, v, vl, nullptr, nullptr, mp, ml);
-  if (causal) mp = nullptr;
-  check(vh_fused_attention_fwd(q.data(), &ql, k.data(), &kl, v.data(), &vl, mp, mp ? &ml : nullptr, causal,
-                               out.data(), &ol, nullptr, 0, nullptr));
+  check(vh_fused_attention_fwd(q.data(), &ql, k.data(), &kl, v.data(), &vl, mp, mp ? &ml : nullptr,
+                               causal_mode(mp), out.data(), &ol, nullptr, 0, nullptr));
   return out;
 }
 
@@ -518,11 +510,9 @@ std::tuple<Tensor, Tensor, Tensor> fused_attention_backward(const Tensor& q0, co
   vh_layout ml{};
   if (mask) ml = layout_of(*mask);
   const float* mp = mask ? mask->data() : nullptr;
-  const int causal = causal_mask(q, ql, k, kl, v, vl, &g, &gl, mp, ml);
-  if (causal) mp = nullptr;
-  check(vh_fused_attention_bwd(q.data(), &ql, k.data(), &kl, v.data(), &vl, mp, mp ? &ml : nullptr, causal,
-                               g.data(), &gl, dq.data(), &dl, dk.data(), &dl, dv.data(), &dl, nullptr, 0,
-                               nullptr));
+  check(vh_fused_attention_bwd(q.data(), &ql, k.data(), &kl, v.data(), &vl, mp, mp ? &ml : nullptr,
+                               causal_mode(mp), g.data(), &gl, dq.data(), &dl, dk.data(), &dl, dv.data(), &dl,
+                               nullptr, 0, nullptr));
   return {dq, dk, dv};
 }
 

@@ -144,6 +144,15 @@ VH_DEV void gm_tile_of(int bid, int nblk, int tiles_m, int tiles_n, int& tm, int
   tn = in / gsize;
 }
 
+// The launch's causal mode: a.causal, unless a device flag says the product is dense.
+VH_DEV int gm_causal(const GemmArgs& a) { return (a.causal_flag && *a.causal_flag == 0) ? 0 : a.causal; }
+// The addend: under a device flag that says causal, E is the attention's mask,
+// whose allowed entries are +-0 and whose masked ones the causal form skips, so
+// it is not added (as a caller passing causal = 1 drops it).
+VH_DEV const float* gm_addend(const GemmArgs& a) {
+  return (a.causal_flag && *a.causal_flag != 0) ? nullptr : a.E;
+}
+
 // The epilogue of one output element from its product sum v: the raw partial
 // under split-K (raw), else alpha v (+ E[m, n]) (+ old = out[m, n]).
 VH_DEV float gm_finish(const GemmArgs& a, const float* E, bool raw, float v, int64_t m, int64_t n, float old) {
@@ -212,7 +221,8 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   int tm, tn;
   int64_t bat = blockIdx.y;  // batch index (both batch dims)
-  if (a.causal >= 2 && a.ksplit <= 1) {
+  const int causal = gm_causal(a);
+  if (causal >= 2 && a.ksplit <= 1) {
     // The k range grows with the tile row (k <= m) or shrinks (k >= m): deal
     // the workgroups longest first across all batches, so the last ones to
     // start are short (the launch order is x fastest, then y).
@@ -220,13 +230,13 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
     const int64_t rank = lin / gridDim.y;
     bat = lin % gridDim.y;
     const int row = (int)(rank / a.tiles_n);
-    tm = a.causal == 2 ? a.tiles_m - 1 - row : row;
+    tm = causal == 2 ? a.tiles_m - 1 - row : row;
     tn = (int)(rank % a.tiles_n);
   } else {
     gm_tile_of(blockIdx.x, gridDim.x, a.tiles_m, a.tiles_n, tm, tn);
   }
   const int64_t m0 = (int64_t)tm * GM_TM, n0 = (int64_t)tn * TN;
-  if (a.causal == 1 && n0 > m0 + GM_TM - 1) return;  // the whole tile is masked
+  if (causal == 1 && n0 > m0 + GM_TM - 1) return;  // the whole tile is masked
 
   const bool split = a.ksplit > 1;
   const int64_t b1 = split ? 0 : bat / a.nb2, b2 = split ? 0 : bat % a.nb2;
@@ -235,8 +245,8 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
   float* C = a.C + b1 * a.sc1 + b2 * a.sc2;
 
   int64_t kb = 0, ke = a.K;
-  if (a.causal == 2) ke = m0 + GM_TM < a.K ? m0 + GM_TM : a.K;
-  if (a.causal == 3) kb = (m0 / GM_TK) * GM_TK;
+  if (causal == 2) ke = m0 + GM_TM < a.K ? m0 + GM_TM : a.K;
+  if (causal == 3) kb = (m0 / GM_TK) * GM_TK;
   if (split) {
     kb = (int64_t)blockIdx.y * a.kchunk;
     ke = kb + a.kchunk < a.K ? kb + a.kchunk : a.K;
@@ -366,7 +376,8 @@ VH_DEV void gemm_f32_impl(const GemmArgs& a) {
   // store writes 16 bytes and a half-wave a whole 512-byte row.
   float* out = split ? a.ws + (int64_t)blockIdx.y * a.M * a.N : C;
   const int64_t ldo = split ? a.N : a.ldc;
-  const float* E = !split && a.E ? a.E + b1 * a.se1 + b2 * a.se2 : nullptr;
+  const float* E0 = gm_addend(a);
+  const float* E = !split && E0 ? E0 + b1 * a.se1 + b2 * a.se2 : nullptr;
   const bool whole = m0 + GM_TM <= a.M && n0 + TN <= a.N && (ldo & 3) == 0 &&
                      (reinterpret_cast<uintptr_t>(out) & 15) == 0;
   if (whole) {
@@ -421,7 +432,9 @@ VH_DEV void gemm_f32_persist(const GemmArgs& a) {
   __shared__ __attribute__((aligned(16))) float L[4][GM_STAGE];  // A stages 0-1, B stages 2-3
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w >> 1, wn = w & 1, li = lane & 31, h = lane >> 5;
-  const int64_t live = a.causal == 1 ? (int64_t)a.tiles_m * (a.tiles_m + 1) / 2 : (int64_t)a.tiles_m * a.tiles_n;
+  const int causal = gm_causal(a);
+  const float* E0 = gm_addend(a);
+  const int64_t live = causal == 1 ? (int64_t)a.tiles_m * (a.tiles_m + 1) / 2 : (int64_t)a.tiles_m * a.tiles_n;
   const int64_t total = live * a.nbat;
   const int nloc = (int)(gridDim.x / 8), x = (int)(blockIdx.x % 8);
   const int64_t per = (total + 7) / 8;
@@ -441,7 +454,7 @@ VH_DEV void gemm_f32_persist(const GemmArgs& a) {
     const int64_t bat = it / live;
     const int64_t u = it % live;
     int64_t tm, tn;
-    if (a.causal == 1) {  // u = tm (tm + 1) / 2 + tn, tn <= tm
+    if (causal == 1) {  // u = tm (tm + 1) / 2 + tn, tn <= tm
       tm = (int64_t)((sqrtf(8.0f * (float)u + 1.0f) - 1.0f) * 0.5f);
       while (tm * (tm + 1) / 2 > u) --tm;
       while ((tm + 1) * (tm + 2) / 2 <= u) ++tm;
@@ -454,7 +467,7 @@ VH_DEV void gemm_f32_persist(const GemmArgs& a) {
     t.A = a.A + b1 * a.sa1 + b2 * a.sa2;
     t.B = a.B + b1 * a.sb1 + b2 * a.sb2;
     t.C = a.C + b1 * a.sc1 + b2 * a.sc2;
-    t.E = a.E ? a.E + b1 * a.se1 + b2 * a.se2 : nullptr;
+    t.E = E0 ? E0 + b1 * a.se1 + b2 * a.se2 : nullptr;
     t.m0 = tm * GM_TM;
     t.n0 = tn * TN;
     t.inside = t.m0 + GM_TM <= a.M && t.n0 + TN <= a.N && a.K % GM_TK == 0;

@@ -281,3 +281,44 @@ VH_DEV void attn_probe_impl(const AttnProbeArgs& a) {
     }
   }
 }
+
+// The probe's verdict, one wave: fold the 64 slots (or of the flags, max of
+// the rest), then the conditions under which skipping the masked blocks gives
+// the dense masked form's bits, in double precision: no flagged mask entry
+// and finite operands; a masked entry's x - rowmax below -256 with margin
+// (|m|min (1 - 2^-22) - 2 smax (1 + 2^-22) > 256, smax the largest |score|
+// scale * Dk * max|q| * max|k| widened by the f32 bound for a sum of Dk
+// products, gamma = Dk u / (1 - Dk u), and the scaling's rounding), where f32
+// exp is exactly 0; and, backward, Dk max|v| max|dO| < 1e37 so the products
+// that meet those zeros stay finite. *flag = 1 then, else 0.
+VH_DEV void attn_decide_impl(const AttnDecideArgs& a) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t* w = a.words + 8 * lane;
+  uint32_t h[6];
+  h[0] = w[0];
+#pragma unroll
+  for (int j = 1; j < 6; ++j) h[j] = w[j];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    h[0] |= (uint32_t)__shfl_xor((int)h[0], off, 64);
+#pragma unroll
+    for (int j = 1; j < 6; ++j) {
+      const uint32_t o = (uint32_t)__shfl_xor((int)h[j], off, 64);
+      h[j] = o > h[j] ? o : h[j];
+    }
+  }
+  if (lane != 0) return;
+  auto fl = [](uint32_t b) { return (double)__uint_as_float(b); };
+  const uint32_t kInf = 0x7f800000u;
+  int ok = h[0] == 0u;  // an allowed entry not +-0, or a masked one above -1 or NaN
+  ok = ok && h[2] < kInf && h[3] < kInf && h[4] < kInf && (!a.has_g || h[5] < kInf);  // NaN or inf
+  const double u = 0x1p-24, nu = (double)a.Dk * u;
+  ok = ok && nu < 0.25;
+  if (ok) {
+    const double smax = a.scale * (double)a.Dk * fl(h[2]) * fl(h[3]) * (1.0 + 2.0 * nu / (1.0 - nu)) * (1.0 + 2.0 * u);
+    const double mmin = fl(kInf - h[1]);  // the smallest |masked value| (inf when there is none)
+    ok = mmin * (1.0 - 0x1p-22) - 2.0 * smax * (1.0 + 0x1p-22) > 256.0;
+    if (ok && a.has_g) ok = (double)a.Dk * fl(h[4]) * fl(h[5]) < 1e37;
+  }
+  *a.flag = ok ? 1 : 0;
+}

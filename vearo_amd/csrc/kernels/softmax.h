@@ -25,10 +25,13 @@
 #pragma once
 #include "common.h"
 
+// The launch's causal mode: a.causal, unless a device flag says the rows are dense.
+VH_DEV int sm_causal(const SoftmaxArgs& a) { return (a.causal_flag && *a.causal_flag == 0) ? 0 : a.causal; }
+
 // End of the columns a row writes, given its live length L (causal: L - 1 is
 // the row's index in its T x T block).
-VH_DEV int zero_end(const SoftmaxArgs& a, int L) {
-  if (!a.causal || a.ztile <= 0) return a.T;
+VH_DEV int zero_end(const SoftmaxArgs& a, int causal, int L) {
+  if (!causal || a.ztile <= 0) return a.T;
   const int e = ((L - 1) / a.ztile + 1) * a.ztile;
   return e < a.T ? e : a.T;
 }
@@ -42,6 +45,7 @@ VH_DEV void softmax_fwd_impl(const SoftmaxArgs& a) {
   const int64_t row0 = ((int64_t)blockIdx.x * TPB + threadIdx.x / TEAM) * RPW;
   const int T = a.T;
   const int U = T / VW;
+  const int causal = sm_causal(a);
 
   Unit<VW> v[RPW][NV];
   int L[RPW];
@@ -49,7 +53,7 @@ VH_DEV void softmax_fwd_impl(const SoftmaxArgs& a) {
   for (int r = 0; r < RPW; ++r) {
     const int64_t row = row0 + r;
     const bool active = row < a.rows;
-    L[r] = a.causal ? (int)(row % T) + 1 : T;  // live length
+    L[r] = causal ? (int)(row % T) + 1 : T;  // live length
     const float* xr = a.x + (active ? row : 0) * (int64_t)T;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -91,7 +95,7 @@ VH_DEV void softmax_fwd_impl(const SoftmaxArgs& a) {
     const float inv = 1.0f / (s + 1e-9f);
     if (active) {
       float* yr = a.y + row * (int64_t)T;
-      const int Z = zero_end(a, L[r]);
+      const int Z = zero_end(a, causal, L[r]);
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
         const int u = lane + k * TEAM;
@@ -116,6 +120,7 @@ VH_DEV void softmax_bwd_impl(const SoftmaxArgs& a) {
   const int64_t row0 = ((int64_t)blockIdx.x * TPB + threadIdx.x / TEAM) * RPW;
   const int T = a.T;
   const int U = T / VW;
+  const int causal = sm_causal(a);
 
   Unit<VW> y[RPW][NV], g[RPW][NV];
   int L[RPW];
@@ -123,7 +128,7 @@ VH_DEV void softmax_bwd_impl(const SoftmaxArgs& a) {
   for (int r = 0; r < RPW; ++r) {
     const int64_t row = row0 + r;
     const bool active = row < a.rows;
-    L[r] = a.causal ? (int)(row % T) + 1 : T;
+    L[r] = causal ? (int)(row % T) + 1 : T;
     const int64_t off = (active ? row : 0) * (int64_t)T;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -181,7 +186,7 @@ VH_DEV void softmax_bwd_impl(const SoftmaxArgs& a) {
     dot = team_sum<TEAM>(dot, red);
     if (active) {
       float* dxr = a.y + row * (int64_t)T;
-      const int Z = zero_end(a, L[r]);
+      const int Z = zero_end(a, causal, L[r]);
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
         const int u = lane + k * TEAM;

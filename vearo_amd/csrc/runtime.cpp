@@ -742,6 +742,16 @@ int vh_gelu_bias_bwd(const float* x, const float* bias, const float* dy, float* 
 
 // --------------------------------------------------------------- softmax --
 
+// A device flag (vh_attn_decide's verdict) that the attention's products and
+// softmax passes read to choose their causal or dense form on the device; set
+// for the launches of one attention call on this thread (no host wait for the
+// probe's answer).
+static thread_local const int32_t* g_causal_flag = nullptr;
+struct CausalFlagScope {
+  explicit CausalFlagScope(const int32_t* f) { g_causal_flag = f; }
+  ~CausalFlagScope() { g_causal_flag = nullptr; }
+};
+
 static int softmax_common(const char* base, int cap, int rpw, const float* in, const float* dy,
                           float* out, int64_t rows, int64_t T, int causal, int input_is_x, hipStream_t s,
                           int attn = 0, int ztile = 0) {
@@ -756,7 +766,7 @@ static int softmax_common(const char* base, int cap, int rpw, const float* in, c
   set_rpw(&c, rpw);
   const int bs = block_of(c);
   const int64_t rpb = (int64_t)(bs / c.team) * c.rpw;
-  SoftmaxArgs a{in, dy, out, rows, (int32_t)T, causal ? 1 : 0, input_is_x ? 1 : 0, attn, ztile};
+  SoftmaxArgs a{in, dy, out, rows, (int32_t)T, causal ? 1 : 0, input_is_x ? 1 : 0, attn, ztile, g_causal_flag};
   return launch(fwd_kernel(base, c), (unsigned)cdiv(rows, rpb), 1, bs, 0, s, a);
 }
 
@@ -1307,6 +1317,7 @@ namespace {
 GemmArgs gemm_args(const vh_gemm_desc* d, int64_t lda, int64_t ldb, int64_t tiles_m, int64_t tiles_n,
                    int64_t b0 = 0) {
   GemmArgs g{};
+  g.causal_flag = g_causal_flag;
   g.A = d->a ? d->a + b0 * d->a_sb[0] : nullptr;
   g.B = d->b ? d->b + b0 * d->b_sb[0] : nullptr;
   g.C = d->c + b0 * d->c_sb[0];
@@ -1436,7 +1447,11 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
   // LIBRARY: large unbatched dense products, with no addend or a bias over
   // the output columns, go to hipBLASLt when it has an algorithm (the A/B
   // reference); everything else as DEFAULT.
-  if (d->engine == VH_GEMM_ENGINE_LIBRARY && d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE &&
+  // Under a device causal flag (an attention call) the product keeps one
+  // launch whose grid serves both forms: no library, large-product kernel or
+  // split of K.
+  const bool dflag = g_causal_flag != nullptr;
+  if (!dflag && d->engine == VH_GEMM_ENGINE_LIBRARY && d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE &&
       (!d->e || (d->e_sm == 0 && d->e_sn == 1)) && K > 0 && (double)M * (double)N * (double)K >= 67108864.0) {
     bool taken = false;
     VH_TRY(vh_rt::blaslt_gemm(d, akc, bkc, stream, &taken));
@@ -1445,14 +1460,14 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
       return VH_OK;
     }
   }
-  if (d->engine != VH_GEMM_ENGINE_TILED) {
+  if (!dflag && d->engine != VH_GEMM_ENGINE_TILED) {
     bool taken = false;
     VH_TRY(gemm_big(d, akc, bkc, lda, ldb, S(stream), &taken));
     if (taken) return VH_OK;
   }
   const bool avec = K > 0 && gemm_vec_ok(d->a, lda, akc ? K : M, d->a_sb);
   const bool bvec = K > 0 && gemm_vec_ok(d->b, ldb, bkc ? K : N, d->b_sb);
-  const GemmPlan plan = gemm_plan(M, N, K, d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE);
+  const GemmPlan plan = gemm_plan(M, N, K, !dflag && d->batch[0] * d->batch[1] == 1 && d->causal == VH_GEMM_DENSE);
   const int64_t tiles_m = cdiv(M, VH_GEMM_TILE_M), tiles_n = cdiv(N, plan.narrow ? 64 : VH_GEMM_TILE_N);
   if (tiles_m * tiles_n > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_gemm: too many tiles");
   const std::string name = std::string("vh_gemm_") + (akc ? "k" : "m") + (avec ? "4" : "1") + "_" +
@@ -1493,7 +1508,8 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
       (d->causal == VH_GEMM_DENSE || (d->causal == VH_GEMM_SKIP_UPPER && tiles_n >= tiles_m))) {
     GemmArgs g = gemm_args(d, lda, ldb, tiles_m, tiles_n);
     g.nbat = nbat;
-    const int64_t live = d->causal == VH_GEMM_SKIP_UPPER ? tiles_m * (tiles_m + 1) / 2 : tiles;
+    // Under a device flag the product may run dense: size the grid for that.
+    const int64_t live = (d->causal == VH_GEMM_SKIP_UPPER && !dflag) ? tiles_m * (tiles_m + 1) / 2 : tiles;
     const int64_t slots = 8 * std::max<int64_t>(1, 2 * std::max(g_rt.cu_count, 1) / 8);
     const int64_t grid = std::min<int64_t>(slots, 8 * cdiv(live * nbat, 8));
     const std::string pname = std::string("vh_gemmp_") + (akc ? "k4" : "m4") + "_" + (bkc ? "k4" : "n4");
@@ -1817,21 +1833,22 @@ size_t vh_fused_attention_scratch_bytes(int64_t B, int64_t H, int64_t S, int bac
   return backward ? 2 * one : one;
 }
 
-int vh_attention_mask_is_causal(const float* q, const vh_layout* ql, const float* k, const vh_layout* kl,
-                                const float* v, const vh_layout* vl, const float* g, const vh_layout* gl,
-                                const float* mask, const vh_layout* ml, int* is_causal, void* stream) {
-  VH_TRY(require_init());
-  if (!is_causal) return fail(VH_ERR_INVALID, "vh_attention_mask_is_causal: null result pointer");
-  *is_causal = 0;
-  AttnShape sh;
-  VH_TRY(attn_layout(ql, "attention mask probe q", &sh, true));
-  VH_TRY(attn_layout(kl, "attention mask probe k", &sh, false));
-  VH_TRY(attn_layout(vl, "attention mask probe v", &sh, false));
-  if (g) VH_TRY(attn_layout(gl, "attention mask probe grad", &sh, false));
-  if (!mask || !ml) return fail(VH_ERR_INVALID, "vh_attention_mask_is_causal: no mask");
-  int64_t mst[4];
-  VH_TRY(attn_mask(ml, sh, mst));
-  if (sh.B * sh.H * sh.S * sh.Dk == 0 || !q || !k || !v) return VH_OK;
+namespace {
+constexpr size_t kProbeWords = 64 * 8;  // the probe's 64 slots of 8 words
+constexpr size_t kProbeBytes = kProbeWords * sizeof(uint32_t) + 256;  // + the verdict
+
+// Launches the probe of an attention call's mask and operands (vh_attn_probe)
+// and its verdict (vh_attn_decide) into flag, a device int32: 1 when skipping
+// the masked blocks gives the dense masked form's bits (the conditions are
+// in attn_decide_impl). words: kProbeWords of device scratch. *usable is false,
+// and nothing is launched, when the call is outside what the probe handles
+// (no [S, S] block in the mask, or a grid beyond its limits): the dense form
+// must run then.
+int attn_probe_decide(const float* q, const vh_layout* ql, const float* k, const vh_layout* kl, const float* v,
+                      const vh_layout* vl, const float* g, const vh_layout* gl, const float* mask,
+                      const vh_layout* ml, const AttnShape& sh, uint32_t* words, int32_t* flag, hipStream_t s,
+                      bool* usable) {
+  *usable = false;
   // The mask must carry the [S, S] block itself (a broadcast row or column
   // cannot hold the triangle), each leading dim either its own or broadcast.
   if (ml->rank < 2 || ml->dims[ml->rank - 1] != sh.S || ml->dims[ml->rank - 2] != sh.S) return VH_OK;
@@ -1852,45 +1869,50 @@ int vh_attention_mask_is_causal(const float* q, const vh_layout* ql, const float
     a.d0[i] = (int32_t)dm[0]; a.d1[i] = (int32_t)dm[1]; a.d2[i] = (int32_t)dm[2]; a.d3[i] = (int32_t)dm[3];
     a.s0[i] = st[0]; a.s1[i] = st[1]; a.s2[i] = st[2]; a.s3[i] = st[3];
   }
-  hipStream_t s = S(stream);
   a.Y = (int32_t)std::max<int64_t>(sh.B * sh.H, (int64_t)a.d0[0] * a.d1[0]);
   if ((int64_t)a.Y * 5 > 65535) return VH_OK;  // grid y limit: leave such calls on the dense path
-  Scratch sc;
-  VH_TRY(sc.get(s, nullptr, 0, 64 * 8 * sizeof(uint32_t)));
-  uint32_t* w = static_cast<uint32_t*>(sc.p);
-  VH_TRY(fill(w, 0.0f, 64 * 8, s));
-  a.words = w;
+  VH_TRY(fill(reinterpret_cast<float*>(words), 0.0f, (int64_t)kProbeWords, s));
+  a.words = words;
   VH_TRY(launch("vh_attn_probe", (unsigned)cdiv(sh.S, 16), (unsigned)(5 * a.Y), 256, 0, s, a));
-  uint32_t slots[64 * 8];
-  VH_HIP(hipMemcpyAsync(slots, w, sizeof(slots), hipMemcpyDeviceToHost, s));
+  AttnDecideArgs dcs{words, flag, (double)(1.0f / std::sqrt((float)sh.Dk)), (int32_t)sh.Dk, g ? 1 : 0};
+  VH_TRY(launch("vh_attn_decide", 1, 1, 64, 0, s, dcs));
+  *usable = true;
+  return VH_OK;
+}
+}  // namespace
+
+int vh_attention_mask_is_causal(const float* q, const vh_layout* ql, const float* k, const vh_layout* kl,
+                                const float* v, const vh_layout* vl, const float* g, const vh_layout* gl,
+                                const float* mask, const vh_layout* ml, int* is_causal, void* stream) {
+  VH_TRY(require_init());
+  if (!is_causal) return fail(VH_ERR_INVALID, "vh_attention_mask_is_causal: null result pointer");
+  *is_causal = 0;
+  AttnShape sh;
+  VH_TRY(attn_layout(ql, "attention mask probe q", &sh, true));
+  VH_TRY(attn_layout(kl, "attention mask probe k", &sh, false));
+  VH_TRY(attn_layout(vl, "attention mask probe v", &sh, false));
+  if (g) VH_TRY(attn_layout(gl, "attention mask probe grad", &sh, false));
+  if (!mask || !ml) return fail(VH_ERR_INVALID, "vh_attention_mask_is_causal: no mask");
+  int64_t mst[4];
+  VH_TRY(attn_mask(ml, sh, mst));
+  if (sh.B * sh.H * sh.S * sh.Dk == 0 || !q || !k || !v) return VH_OK;
+  hipStream_t s = S(stream);
+  // The answer needs a host wait, which a stream under graph capture cannot
+  // make: answer "no" (the dense form is always right) without launching.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  VH_HIP(hipStreamIsCapturing(s, &cap));
+  if (cap != hipStreamCaptureStatusNone) return VH_OK;
+  Scratch sc;
+  VH_TRY(sc.get(s, nullptr, 0, kProbeBytes));
+  uint32_t* words = static_cast<uint32_t*>(sc.p);
+  int32_t* flag = reinterpret_cast<int32_t*>(words + kProbeWords);
+  bool usable = false;
+  VH_TRY(attn_probe_decide(q, ql, k, kl, v, vl, g, gl, mask, ml, sh, words, flag, s, &usable));
+  if (!usable) return VH_OK;
+  int32_t f = 0;
+  VH_HIP(hipMemcpyAsync(&f, flag, sizeof(f), hipMemcpyDeviceToHost, s));
   VH_HIP(hipStreamSynchronize(s));
-  uint32_t h[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int i = 0; i < 64; ++i) {
-    h[0] |= slots[8 * i];
-    for (int j = 1; j < 6; ++j) h[j] = std::max(h[j], slots[8 * i + j]);
-  }
-  h[1] = 0x7f800000u - h[1];  // the smallest |masked value| (inf when there is none)
-  auto fl = [](uint32_t b) { float f; std::memcpy(&f, &b, 4); return (double)f; };
-  if (h[0] != 0) return VH_OK;  // an allowed entry not +-0, or a masked one above -1 or NaN
-  const uint32_t kInf = 0x7f800000u;
-  if (h[2] >= kInf || h[3] >= kInf || h[4] >= kInf || (g && h[5] >= kInf)) return VH_OK;  // NaN or inf
-  // Largest |score| the product can form: |s| <= scale * Dk * max|q| * max|k|,
-  // widened by twice the f32 bound for a sum of Dk products in any order
-  // (gamma = Dk u / (1 - Dk u), u = 2^-24) and the scaling's rounding.
-  const double u = 0x1p-24, nu = (double)sh.Dk * u;
-  if (nu >= 0.25) return VH_OK;
-  const double scale = (double)(1.0f / std::sqrt((float)sh.Dk));
-  const double smax = scale * (double)sh.Dk * fl(h[2]) * fl(h[3]) * (1.0 + 2.0 * nu / (1.0 - nu)) * (1.0 + 2.0 * u);
-  // A masked x = fl(s + m) less the row max (>= the diagonal's score, >= -smax)
-  // is at most 2 smax - |m| plus two roundings of ~|m| 2^-24 each; expf of
-  // anything below -104 is exactly 0 in f32, so ask for -256 with margin.
-  const double mmin = fl(h[1]);
-  if (!(mmin * (1.0 - 0x1p-22) - 2.0 * smax * (1.0 + 0x1p-22) > 256.0)) return VH_OK;
-  // The zero probabilities multiply v (and, backward, dP = dO v^T): those
-  // products stay finite, so 0 * x is exactly 0 as in the dense form.
-  const double vmax = fl(h[4]), gmax = g ? fl(h[5]) : 0.0;
-  if (g && !((double)sh.Dk * vmax * gmax < 1e37)) return VH_OK;
-  *is_causal = 1;
+  *is_causal = f == 1 ? 1 : 0;
   return VH_OK;
 }
 
@@ -1909,10 +1931,29 @@ int vh_fused_attention_fwd(const float* q, const vh_layout* ql, const float* k, 
   if (sh.B * sh.H * sh.S * sh.Dk == 0) return VH_OK;
   if (!q || !k || !v || !out) return fail(VH_ERR_INVALID, "vh_fused_attention_fwd: null pointer");
   if (sh.S > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_fused_attention_fwd: S too large");
+  if (causal < 0 || causal > VH_ATTN_CAUSAL_AUTO) return fail(VH_ERR_INVALID, "vh_fused_attention_fwd: bad causal mode");
   hipStream_t s = S(stream);
   Scratch sc;
   VH_TRY(sc.get(S(stream), scratch, scratch_bytes, vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 0)));
   float* P = static_cast<float*>(sc.p);
+  // AUTO: the probe's verdict stays on the device; the launches below read it.
+  Scratch pb;
+  const int32_t* dflag = nullptr;
+  if (causal == VH_ATTN_CAUSAL_AUTO) {
+    causal = 0;
+    if (mask) {
+      VH_TRY(pb.get(s, nullptr, 0, kProbeBytes));
+      uint32_t* words = static_cast<uint32_t*>(pb.p);
+      int32_t* flag = reinterpret_cast<int32_t*>(words + kProbeWords);
+      bool usable = false;
+      VH_TRY(attn_probe_decide(q, ql, k, kl, v, vl, nullptr, nullptr, mask, ml, sh, words, flag, s, &usable));
+      if (usable) {
+        causal = 1;
+        dflag = flag;
+      }
+    }
+  }
+  CausalFlagScope fs(dflag);
   VH_TRY(attn_probs(q, ql, k, kl, mask, mst, causal, sh, P, s));
   vh_gemm_desc d{};  // out = P v
   d.M = sh.S;
@@ -1959,11 +2000,29 @@ int vh_fused_attention_bwd(const float* q, const vh_layout* ql, const float* k, 
   if (!q || !k || !v || !dout || !dq || !dk || !dv)
     return fail(VH_ERR_INVALID, "vh_fused_attention_bwd: null pointer");
   if (sh.S > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_fused_attention_bwd: S too large");
+  if (causal < 0 || causal > VH_ATTN_CAUSAL_AUTO) return fail(VH_ERR_INVALID, "vh_fused_attention_bwd: bad causal mode");
   hipStream_t s = S(stream);
   Scratch sc;
   VH_TRY(sc.get(S(stream), scratch, scratch_bytes, vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 1)));
   float* P = static_cast<float*>(sc.p);
   float* G = P + vh_fused_attention_scratch_bytes(sh.B, sh.H, sh.S, 0) / sizeof(float);
+  Scratch pb;
+  const int32_t* dflag = nullptr;
+  if (causal == VH_ATTN_CAUSAL_AUTO) {
+    causal = 0;
+    if (mask) {
+      VH_TRY(pb.get(s, nullptr, 0, kProbeBytes));
+      uint32_t* words = static_cast<uint32_t*>(pb.p);
+      int32_t* flag = reinterpret_cast<int32_t*>(words + kProbeWords);
+      bool usable = false;
+      VH_TRY(attn_probe_decide(q, ql, k, kl, v, vl, dout, dol, mask, ml, sh, words, flag, s, &usable));
+      if (usable) {
+        causal = 1;
+        dflag = flag;
+      }
+    }
+  }
+  CausalFlagScope fs(dflag);
   // P, recomputed from q and k as the reference does (cpu:2520-2569).
   VH_TRY(attn_probs(q, ql, k, kl, mask, mst, causal, sh, P, s));
   return attn_bwd_from_probs(P, G, q, ql, k, kl, v, vl, causal, dout, dol, dq, dql, dk, dkl, dv, dvl, sh, s);

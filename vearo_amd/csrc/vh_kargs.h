@@ -74,6 +74,8 @@ struct SoftmaxArgs {
   int32_t attn;     // 1: fused-attention numerics (p = e * (1/(sum + 1e-9)), fma sum of dy*y)
   int32_t ztile;    // causal, > 0: a row's masked zeros are written only up to the end of
                     // its ztile-row tile (what the causal products read); 0: the whole row
+  const int32_t* causal_flag;  // non-null: the causal form applies only when *causal_flag is 1,
+                               // else the rows are dense (decided on the device: vh_attn_decide)
 };
 
 // C tile of one GEMM workgroup (host and device agree on the grid).
@@ -107,6 +109,7 @@ struct GemmArgs {
   int64_t kchunk;
   float* ws;
   int64_t nbat;  // persistent form (vh_gemmp_*): batches in the launch (grid y is 1)
+  const int32_t* causal_flag;  // non-null: `causal` applies only when *causal_flag is 1, else dense
 };
 
 // Fixed-order sum of the split-K partials plus the GEMM epilogue.
@@ -363,4 +366,14 @@ struct AttnProbeArgs {
   int64_t s0[5], s1[5], s2[5], s3[5];     // strides (elements)
   uint32_t* words;  // 64 slots of 8: [0] mask pattern failures, [1] 0x7f800000 - min |masked| bits, [2..5] max |x| bits of q, k, v, g
   int32_t Y;        // grid y per segment: the largest leading (b, h) count
+};
+
+// The probe's verdict from its 64 slots (vh_attn_decide, one wave): *flag = 1
+// when the causal kernels give the dense masked form's bits, else 0.
+struct AttnDecideArgs {
+  const uint32_t* words;
+  int32_t* flag;
+  double scale;  // the attention's 1/sqrt(Dk) as f32, widened
+  int32_t Dk;
+  int32_t has_g;  // the backward's output gradient was probed (segment 4)
 };
