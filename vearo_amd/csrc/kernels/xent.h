@@ -5,6 +5,11 @@
 // loss = -(sum over rows of log_softmax) / B, returned as one float.
 // cross_entropy_backward (lib.rs:1053-1127): dl = go * (p - 1[c == t]) / B with
 // p = exp(l - max) / sum. Targets are f32 class ids, rounded like Rust's round().
+// The kernels evaluate it as (p - 1[c == t]) * (go / B) with go / B rounded once
+// per row: one correctly rounded division per element (p) instead of two. The
+// same bits as the reference's order when B is a power of two (the scaling is
+// then exact), within one rounding of it otherwise. Measured at [16384, 50257]
+// the second division cost about 8% of the backward's time.
 //
 // Layout: logits / dlogits [B, V] with row stride ld (>= V), targets [B], one
 // 512-thread workgroup (8 waves) per row. When V <= 512*128 the row is held in
@@ -91,8 +96,7 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
   }
   if constexpr (MODE != 0) {
     __builtin_amdgcn_sched_barrier(0);
-    const float go = *a.grad_out;
-    const float Bf = (float)a.B;
+    const float c = *a.grad_out / (float)a.B;
     const __amdgpu_buffer_rsrc_t rout =
         __builtin_amdgcn_make_buffer_rsrc(a.out + row * a.ld, 0, V * 4, VH_BUF_WORD3);
 #pragma unroll
@@ -100,7 +104,7 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
       const float p = v[k] / s;
       const float ind = (int)threadIdx.x == t - k * XE_TEAM ? 1.0f : 0.0f;
       // Units past the row end fall outside the resource and are dropped.
-      const float g = go * (p - ind) / Bf;
+      const float g = (p - ind) * c;
       __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, g), rout, voff + (k & 1) * XE_TEAM * 4,
                                             (k >> 1) * XE_TEAM * 8, 0);
       // At most 2 elements' correctly rounded divisions in flight: their
@@ -137,13 +141,12 @@ VH_DEV void xent_stream_impl(const XentArgs& a) {
   if constexpr (!BWD) {
     if (threadIdx.x == 0) a.out[row] = t >= 0 ? lr[t] - M - logf(s) : 0.0f;
   } else {
-    const float go = *a.grad_out;
-    const float Bf = (float)a.B;
+    const float gs = *a.grad_out / (float)a.B;
     float* o = a.out + row * a.ld;
     for (int c = threadIdx.x; c < V; c += 1024) {
       const float p = expf(lr[c] - M) / s;
       const float ind = c == t ? 1.0f : 0.0f;
-      o[c] = go * (p - ind) / Bf;
+      o[c] = (p - ind) * gs;
     }
   }
 }
