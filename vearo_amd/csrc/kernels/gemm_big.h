@@ -26,9 +26,11 @@
 //
 // Tile: 256 x BN (BN = 192 or 256). NW = 8 waves, two per SIMD, own 64 x BN/2
 // blocks (a 4 x 2 grid) as 2 x BN/64 matrix-core tiles of 32 x 32
-// (v_mfma_f32_32x32x2_f32), their accumulators in the accumulation registers:
-// while one wave of a SIMD waits on LDS or the barrier, the other's products
-// keep the matrix core busy. (NW = 4, one wave per SIMD owning 128 x BN/2,
+// (v_mfma_f32_32x32x2_f32). At two waves per SIMD each wave has 256 registers
+// of the unified register file; the compiler keeps the accumulators in
+// ordinary VGPRs beside the fragments and addresses (the code object reports
+// 256 VGPRs and no accumulation registers). While one wave of a SIMD waits on
+// LDS or the barrier, the other's products keep the matrix core busy. (NW = 4, one wave per SIMD owning 128 x BN/2,
 // measured on MI355X at [16384 x 768] x [768 x 50260] and the lm_head
 // gradients: 0.87-0.88 of the f32 matrix peak against 0.90-0.93 for NW = 8,
 // which also fits its registers without spilling and needs no software
