@@ -13,7 +13,11 @@ line under "configs" (gpt2_block -- config[4]'s training step, whose ms per
 step is also the top-level "gpt2_block_ms" -- gelu_bias, embedding_uniform,
 embedding_zipf, cross_entropy, softmax_dense -- the dense form the BackendOps
 slot runs -- and layernorm_cfg0); --no-extra skips them, --workload NAME
-prints one config's own line.
+prints one config's own line. gpt2_block also carries "ab_library" (its dense
+products on hipBLASLt), "dropin" (the same step op by op through the
+BackendOps mirror, shared-weight gradients folded into one product),
+"dropin_reference_arms" (the reference's own Matmul arm: per-batch products,
+then reduce_to) and "dropin_unfused" (MultiHeadAttention's unfused path).
 
 Inputs are resident in HBM before timing. Buffers that would otherwise stay in
 the 256 MB MALL between uses alternate between two sets (or are flushed by the
@@ -416,15 +420,18 @@ def wl_gpt2_block(vh):
             g.set_gemm_engine(vh.GEMM_ENGINE_DEFAULT)
         return out
 
-    def dropin(hip, stream, steps, fused=True):
+    def dropin(hip, stream, steps, fused=True, fold=True):
         # The same step issued op by op through the BackendOps mirror, in the
         # reference's own order (forward tape, backward_impl arms, AdamW::step):
-        # what an unchanged vearo program gets. Timed like the headline, then
-        # one step with an event after every op for the per-phase breakdown.
+        # what a vearo program gets. Timed like the headline, then one step
+        # with an event after every op for the per-phase breakdown.
         # fused=False: MultiHeadAttention's unfused path (the reference with
         # VEARO_USE_FUSED_ATTENTION=0), scores through the matmul, mul, add and
         # softmax slots and back through the Softmax arm's slot calls.
-        d = _block.DropIn(_block.GptConfig(*cfg), fused_attention=fused)
+        # fold=False: the reference's own Matmul arm for the shared weights
+        # (per-batch product, then reduce_to over the batch) instead of one
+        # product over all rows.
+        d = _block.DropIn(_block.GptConfig(*cfg), fused_attention=fused, fold_weight_grads=fold)
         try:
             d.set_params(params)
             d.set_inputs(ids, tg)
@@ -467,7 +474,8 @@ def wl_gpt2_block(vh):
     info = {"workload": "cfg[4] GPT-2-small block training step: B=16, T=1024, C=768, H=12, MLP 3072, "
                         "V=50257, one block; fwd + backward + AdamW",
             "flops_per_step": flops, "_mode": "step_ms", "_probe": probe, "_ab": ab, "_dropin": dropin,
-            "_dropin_unfused": lambda hip, stream, steps: dropin(hip, stream, steps, fused=False)}
+            "_dropin_unfused": lambda hip, stream, steps: dropin(hip, stream, steps, fused=False),
+            "_dropin_reference_arms": lambda hip, stream, steps: dropin(hip, stream, steps, fold=False)}
     return ops, info, cpu, (g, A, W, C, d, dl)
 
 
@@ -781,6 +789,7 @@ def run_one(name, vh, hip, stream, args, cpu_budget):
         ab = info.pop("_ab", None)
         dropin = info.pop("_dropin", None)
         dropin_unfused = info.pop("_dropin_unfused", None)
+        dropin_ref = info.pop("_dropin_reference_arms", None)
         step_s = m["wall"] / K
         flops = info["flops_per_step"]
         # HBM traffic of the lm_head product (counters over the product alone,
@@ -801,6 +810,8 @@ def run_one(name, vh, hip, stream, args, cpu_budget):
             res["ab_library"] = ab(hip, stream, max(3, min(K, 10)))
         if dropin is not None:
             res["dropin"] = dropin(hip, stream, max(3, min(K, 10)))
+        if dropin_ref is not None:
+            res["dropin_reference_arms"] = dropin_ref(hip, stream, max(3, min(K, 10)))
         if dropin_unfused is not None:
             res["dropin_unfused"] = dropin_unfused(hip, stream, max(3, min(K, 10)))
         if cpu_budget is not None:
@@ -923,6 +934,7 @@ def main():
         res["gpt2_block_frac_of_f32_mfma_peak"] = g["frac_of_f32_mfma_peak"]
         res["gpt2_block_ms_hipblaslt_ab"] = g.get("ab_library", {}).get("gpt2_block_ms_library")
         res["gpt2_block_dropin_ms"] = g.get("dropin", {}).get("ms_per_step")
+        res["gpt2_block_dropin_reference_arms_ms"] = g.get("dropin_reference_arms", {}).get("ms_per_step")
         res["gpt2_block_dropin_unfused_ms"] = g.get("dropin_unfused", {}).get("ms_per_step")
         res["configs"] = configs
     print(json.dumps(res), flush=True)

@@ -115,6 +115,17 @@ void vb_dropin_destroy(vb_dropin* d);
  * variable VEARO_USE_FUSED_ATTENTION ("0" or "false": unfused). */
 int vb_dropin_set_fused_attention(vb_dropin* d, int fused);
 int vb_dropin_fused_attention(const vb_dropin* d);
+/* The Matmul arm's gradient of a 2-D right operand shared by every batch (the
+ * Linear weights and the lm_head, [..., S, K] x [K, N]): fold = 1 (the
+ * default) computes reduce_to(l^T g, [K, N]) as one product over all leading
+ * rows, g.reshape([rows, N]).transpose(0, 1).matmul(l.reshape([rows, K]))
+ * passed on as its [K, N] transpose (the weight's gradient then arrives
+ * contiguous), the same sum in another grouping; fold = 0 issues the reference's arm, the
+ * per-batch product then reduce_to over the batch (autograd lib.rs:502-519,
+ * 316-361). No counterpart in the reference: a one-arm change a HIP-aware
+ * autograd would make. */
+int vb_dropin_set_fold_weight_grads(vb_dropin* d, int fold);
+int vb_dropin_fold_weight_grads(const vb_dropin* d);
 /* Host copies of parameter i (numel must match) and of its last gradient
  * (after a step with backward != 0). */
 int vb_dropin_set_param(vb_dropin* d, int i, const float* host, int64_t numel);

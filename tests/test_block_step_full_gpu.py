@@ -85,6 +85,16 @@ def test_block_step_full_size_matches_oracle(vh):
     dloss1 = d.step(backward=False)
     d.close()
     print(f"drop-in: loss1 {dloss1:.7f}", flush=True)
+    # The reference's own Matmul arm (per-batch weight gradients, then reduce_to).
+    d = _block.DropIn(_block.GptConfig(*CFG), fold_weight_grads=False)
+    d.set_params(params)
+    d.set_inputs(ids, tg)
+    rloss0 = d.step(backward=True)
+    assert abs(rloss0 - oloss0) <= 1e-4 * abs(oloss0), (rloss0, oloss0)
+    for i, dg in enumerate(d.grads()):
+        if O.GPT_PARAM_NAMES[i] != "k_b":
+            assert_parity(dg, ograds[i], name=f"full-size drop-in (reference arm) grad {O.GPT_PARAM_NAMES[i]}")
+    d.close()
     for p, gr in zip(params, ograds):
         O.adamw_step(p, gr, np.zeros_like(p), np.zeros_like(p), 1, *ADAM)
     t0 = time.perf_counter()

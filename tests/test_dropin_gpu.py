@@ -103,6 +103,42 @@ def test_dropin_medium_model_matches_oracle_and_fused_driver(vh):
     d.close()
 
 
+def test_dropin_weight_gradient_fold_and_reference_arm(vh):
+    """The Matmul arm's shared-weight gradient both ways: folded (the default,
+    one product over all B*S rows) and the reference's own arm (per-batch
+    product, then reduce_to over the batch, autograd:502-519, 316-361). Both
+    against the oracle, on the medium model and on the golden one (B = 2), and
+    against each other (the same sums in another grouping)."""
+    from vearo_amd import _block
+    for cfg, seed in (((2, 128, 128, 4, 512, 1000, 128), 17), (tuple(int(x) for x in GOLD["gpt_cfg"]), None)):
+        if seed is None:
+            params = [GOLD[f"gpt_p{i}"] for i in range(21)]
+            ids, tg = GOLD["gpt_ids"], GOLD["gpt_targets"]
+        else:
+            params, ids, tg = random_model(cfg, seed)
+        print(f"dropin fold cfg={cfg}", flush=True)
+        oloss, ograds = O.gpt_step(O.GptConfig(*cfg), params, ids, tg)
+        got = {}
+        for fold in (True, False):
+            d = _block.DropIn(_block.GptConfig(*cfg), fold_weight_grads=fold)
+            assert d.fold_weight_grads == fold
+            d.set_params(params)
+            d.set_inputs(ids, tg)
+            loss = d.step(backward=True, timing=True)
+            ph = d.phase_ms()
+            assert abs(loss - oloss) <= 1e-5 + 1e-4 * abs(oloss), (fold, loss, oloss)
+            got[fold] = d.grads()
+            check_grads(got[fold], ograds, tag=f"dropin fold={fold}")
+            assert ph["bwd.matmul"] > 0 and ph["bwd.reduce_to"] > 0, ph
+            d.close()
+        for i, (a, b) in enumerate(zip(got[True], got[False])):
+            if O.GPT_PARAM_NAMES[i] != "k_b":
+                assert_parity(a, b, ograds[i].astype(np.float64), name=f"fold vs reference arm {O.GPT_PARAM_NAMES[i]}")
+    d = _block.DropIn(_block.GptConfig(*cfg))
+    assert d.fold_weight_grads  # the default
+    d.close()
+
+
 def test_dropin_unfused_attention(vh):
     """MultiHeadAttention's unfused path (VEARO_USE_FUSED_ATTENTION=0,
     crates/vearo-nn/src/lib.rs:603-613): scores through the matmul, mul, add

@@ -50,6 +50,8 @@ def _load():
         "vb_dropin_destroy": (None, [H]),
         "vb_dropin_set_fused_attention": (c_int, [H, c_int]),
         "vb_dropin_fused_attention": (c_int, [H]),
+        "vb_dropin_set_fold_weight_grads": (c_int, [H, c_int]),
+        "vb_dropin_fold_weight_grads": (c_int, [H]),
         "vb_dropin_set_param": (c_int, [H, c_int, c_void_p, c_int64]),
         "vb_dropin_get_param": (c_int, [H, c_int, c_void_p, c_int64]),
         "vb_dropin_get_grad": (c_int, [H, c_int, c_void_p, c_int64]),
@@ -166,9 +168,12 @@ class DropIn:
     table in the reference's own order (SimpleGPT::forward's tape, then
     backward_impl's arms, then AdamW::step): include/vearo_block.h vb_dropin_*."""
 
-    def __init__(self, cfg: GptConfig, fused_attention=None):
+    def __init__(self, cfg: GptConfig, fused_attention=None, fold_weight_grads=True):
         """fused_attention: None keeps the reference's switch (the environment
-        variable VEARO_USE_FUSED_ATTENTION), True / False force the path."""
+        variable VEARO_USE_FUSED_ATTENTION), True / False force the path.
+        fold_weight_grads: the Matmul arm's shared-weight gradient as one
+        product over all rows (True) or the reference's per-batch product and
+        reduce_to (False)."""
         self.cfg = cfg
         h = c_void_p()
         check(lib.vb_dropin_create(ctypes.byref(cfg), ctypes.byref(h)))
@@ -176,10 +181,15 @@ class DropIn:
         self.shapes = param_shapes(cfg)
         if fused_attention is not None:
             check(lib.vb_dropin_set_fused_attention(self.h, int(bool(fused_attention))))
+        check(lib.vb_dropin_set_fold_weight_grads(self.h, int(bool(fold_weight_grads))))
 
     @property
     def fused_attention(self) -> bool:
         return bool(lib.vb_dropin_fused_attention(self.h))
+
+    @property
+    def fold_weight_grads(self) -> bool:
+        return bool(lib.vb_dropin_fold_weight_grads(self.h))
 
     def set_params(self, params) -> None:
         for i, a in enumerate(params):

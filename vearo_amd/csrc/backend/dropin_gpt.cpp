@@ -28,6 +28,17 @@
 // Gradients of interior nodes and the tape's saved inputs are released as the
 // walk passes them (the reference holds them to the end of backward_impl).
 //
+// One arm is folded by default (vb_dropin_set_fold_weight_grads(d, 0) keeps
+// the reference's own): the Matmul arm's right-operand gradient when that
+// operand is a 2-D weight shared by every batch ([..., S, K] x [K, N], every
+// Linear layer and the lm_head). The reference computes lᵀ·g per batch and
+// then reduce_to's the [B, K, N] result over the batch (autograd:502-519,
+// 316-361); folded, it is one product over all B·S rows,
+// g.reshape([B·S, N]).transpose(0, 1).matmul(l.reshape([B·S, K])) ([N, K],
+// the weight's own layout) passed on transposed, with the same slots
+// (reshape and transpose are views of contiguous tensors). The same sum in
+// another grouping, and no per-batch [B, K, N] intermediate.
+//
 // With timing on, an event follows each op on the library's stream and the
 // time between consecutive events is charged to that op's phase (launch gaps
 // included), so the phases add up to the step.
@@ -95,6 +106,7 @@ struct vb_dropin {
   std::vector<Tensor> P, G, M, V;  // parameters, last gradients, AdamW moments
   Tensor ids, tg, pos, mask, seed, scale;
   bool fused_attention = true;  // MultiHeadAttention's path (nn:603-613)
+  bool fold_weight_grads = true;  // the Matmul arm's shared-weight gradient as one product
   int t = 0;
   std::vector<Var> pv;
   std::vector<Node> tape;
@@ -333,10 +345,23 @@ struct vb_dropin {
           const Tensor lt = l.transpose(lr - 2, lr - 1), rt = r.transpose(rr - 2, rr - 1);
           const Tensor gl = g.matmul(rt);
           mark(B_MATMUL);
-          const Tensor gr = lt.matmul(g);
-          mark(B_MATMUL);
+          if (fold_weight_grads && rr == 2 && lr > 2 && l.is_contiguous() && g.is_contiguous()) {
+            // reduce_to(lᵀ·g, [K, N]) as one product over the B·S rows,
+            // computed as its transpose gᵀ·l ([N, K], contiguous) and handed
+            // on as a [K, N] view: r is the transposed view of a Linear weight
+            // [N, K], so the Transpose arm's view of this is that weight's
+            // gradient, contiguous, and AdamW's contiguous() copies nothing.
+            const int64_t K = l.shape()[lr - 1], N = g.shape()[g.shape().rank - 1];
+            const int64_t rows = l.shape().numel() / K;
+            const Tensor gwt = g.reshape(Shape{rows, N}).transpose(0, 1).matmul(l.reshape(Shape{rows, K}));
+            gin[1] = gwt.transpose(0, 1);
+            mark(B_MATMUL);
+          } else {
+            const Tensor gr = lt.matmul(g);
+            mark(B_MATMUL);
+            gin[1] = reduce_to(gr, r.shape());
+          }
           gin[0] = reduce_to(gl, l.shape());
-          gin[1] = reduce_to(gr, r.shape());
           break;
         }
         case Op::Reshape: {
@@ -502,6 +527,14 @@ int vb_dropin_set_fused_attention(vb_dropin* d, int fused) {
 }
 
 int vb_dropin_fused_attention(const vb_dropin* d) { return d && d->fused_attention ? 1 : 0; }
+
+int vb_dropin_set_fold_weight_grads(vb_dropin* d, int fold) {
+  if (!d) return vb_fail(VH_ERR_INVALID, "vb_dropin_set_fold_weight_grads: null handle");
+  d->fold_weight_grads = fold != 0;
+  return VH_OK;
+}
+
+int vb_dropin_fold_weight_grads(const vb_dropin* d) { return d && d->fold_weight_grads ? 1 : 0; }
 
 int vb_dropin_set_param(vb_dropin* d, int i, const float* host, int64_t numel) {
   if (!d || !host || i < 0 || i >= VB_GPT_NPARAMS) return vb_fail(VH_ERR_INVALID, "vb_dropin_set_param: bad argument");
