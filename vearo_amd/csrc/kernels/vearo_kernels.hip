@@ -217,15 +217,21 @@ K_GEMMP(false, false, vh_gemmp_m4_n4)
 
 extern "C" __global__ void __launch_bounds__(256) vh_gemm_reduce(GemmReduceArgs a) { gemm_reduce_impl(a); }
 
-// Large dense products: vh_gemmb_<A><B>_192, persistent 256 x 192 tiles (one
-// 512-thread workgroup per CU), and the fix-up of its stream-K round.
-#define K_GEMMB(AK, BK, NAME) \
-  extern "C" __global__ void __launch_bounds__(512, 1) NAME(GemmArgs a) { gemm_big_impl<AK, BK, 192, 8>(a); }
-K_GEMMB(true, true, vh_gemmb_kk_192)
-K_GEMMB(true, false, vh_gemmb_kn_192)
-K_GEMMB(false, true, vh_gemmb_mk_192)
-K_GEMMB(false, false, vh_gemmb_mn_192)
+// Large dense products: vh_gemmb_<A><B>_<BN>, persistent 256 x BN tiles (one
+// 512-thread workgroup per CU), and the fix-up of its stream-K round. BN = 256
+// for long k loops (K >= 8192: the lm_head dx and dW products), 192 otherwise.
+#define K_GEMMB(AK, BK, BN, NAME) \
+  extern "C" __global__ void __launch_bounds__(512, 1) NAME(GemmArgs a) { gemm_big_impl<AK, BK, BN, 8>(a); }
+K_GEMMB(true, true, 192, vh_gemmb_kk_192)
+K_GEMMB(true, false, 192, vh_gemmb_kn_192)
+K_GEMMB(false, true, 192, vh_gemmb_mk_192)
+K_GEMMB(false, false, 192, vh_gemmb_mn_192)
+K_GEMMB(true, true, 256, vh_gemmb_kk_256)
+K_GEMMB(true, false, 256, vh_gemmb_kn_256)
+K_GEMMB(false, true, 256, vh_gemmb_mk_256)
+K_GEMMB(false, false, 256, vh_gemmb_mn_256)
 extern "C" __global__ void __launch_bounds__(256) vh_gemmb_fix_192(GemmArgs a) { gemm_big_fix_impl<192>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_gemmb_fix_256(GemmArgs a) { gemm_big_fix_impl<256>(a); }
 
 // AdamW
 extern "C" __global__ void __launch_bounds__(256) vh_adamw_v1(AdamArgs a) { adamw_impl<1>(a); }

@@ -1352,8 +1352,13 @@ GemmArgs gemm_args(const vh_gemm_desc* d, int64_t lda, int64_t ldb, int64_t tile
 namespace {
 thread_local int g_gemm_path = VH_GEMM_PATH_NONE;
 
-// The persistent 256 x 192-tile kernel (kernels/gemm_big.h) for a large dense
-// unbatched product, when its conditions hold; *taken reports whether it ran.
+// The persistent 256 x BN-tile kernel (kernels/gemm_big.h) for a large dense
+// product, when its conditions hold; *taken reports whether it ran. BN = 256
+// when the k loop is long (K >= VH_GEMMB_WIDE_K) and N fills such tiles: a
+// wider tile does a third more products per k-tile barrier and loads 14 %
+// fewer operand bytes per product (lm_head dx 9.00 -> 8.90 ms, dW 9.14 ->
+// 8.93 ms on MI355X), while its epilogue keeps fewer registers free (it
+// spills), which short k loops pay for (fc2 forward, K = 3072: 544 -> 593 us).
 // Conditions: 4-byte-aligned operand bases (its 128-bit loads need no more); a
 // tile's reads within 2^32 bytes of its origin (leading dimensions < 2^22); k
 // tile and tile counts below 2^31 (K < 2^26). A k-contiguous operand with
@@ -1378,7 +1383,8 @@ int gemm_big(const vh_gemm_desc* d, bool akc, bool bkc, int64_t lda, int64_t ldb
   const int64_t K32 = (akc || bkc) ? K / 32 * 32 : K;
   if (K32 == 0) return VH_OK;
   if (K32 % 32 != 0 && ((!akc && lda < M) || (!bkc && ldb < N))) return VH_OK;
-  const int64_t tiles_m = cdiv(M, VH_GEMMB_TM), tiles_n = cdiv(N, VH_GEMMB_TN);
+  const int64_t BN = K32 >= VH_GEMMB_WIDE_K && N >= VH_GEMMB_TN_WIDE ? VH_GEMMB_TN_WIDE : VH_GEMMB_TN;
+  const int64_t tiles_m = cdiv(M, VH_GEMMB_TM), tiles_n = cdiv(N, BN);
   if (tiles_m * tiles_n * nb >= INT32_MAX) return VH_OK;
   const int64_t tiles = tiles_m * tiles_n * nb, rem = tiles % G;
   GemmArgs g = gemm_args(d, lda, ldb, tiles_m, tiles_n);
@@ -1386,15 +1392,16 @@ int gemm_big(const vh_gemm_desc* d, bool akc, bool bkc, int64_t lda, int64_t ldb
   g.nbat = nb;
   void* ws = nullptr;
   if (rem > 0) {
-    VH_TRY(g_arena.alloc((size_t)G * VH_GEMMB_SLOTS * VH_GEMMB_TM * VH_GEMMB_TN * sizeof(float), s, &ws));
+    VH_TRY(g_arena.alloc((size_t)G * VH_GEMMB_SLOTS * VH_GEMMB_TM * BN * sizeof(float), s, &ws));
     g.ws = static_cast<float*>(ws);
   }
-  const std::string name = std::string("vh_gemmb_") + (akc ? "k" : "m") + (bkc ? "k" : "n") + "_192";
+  const std::string bn = std::to_string(BN);
+  const std::string name = std::string("vh_gemmb_") + (akc ? "k" : "m") + (bkc ? "k" : "n") + "_" + bn;
   int rc = launch(name, (unsigned)G, 1, 512, 0, s, g);
   if (rc == VH_OK && rem > 0) {
     GemmArgs f = g;
     f.ksplit = G;
-    rc = launch("vh_gemmb_fix_192", (unsigned)(rem * (VH_GEMMB_TM / 16)), 1, 256, 0, s, f);
+    rc = launch("vh_gemmb_fix_" + bn, (unsigned)(rem * (VH_GEMMB_TM / 16)), 1, 256, 0, s, f);
   }
   if (ws) g_arena.free(ws, s);
   VH_TRY(rc);
