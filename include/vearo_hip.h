@@ -388,6 +388,15 @@ int vh_fused_attention_bwd_probs(const float* P, const float* q, const vh_layout
 int vh_adamw_step(float* param, const float* grad, float* m, float* v, int64_t n, int32_t t,
                   float lr, float beta1, float beta2, float eps, float weight_decay,
                   void* stream);
+/* vh_adamw_step over `count` tensors (arrays of device pointers and sizes in
+ * host memory) in as few launches as possible (up to 32 tensors per launch),
+ * each element updated exactly as vh_adamw_step updates it. For an optimizer
+ * that steps every parameter at once (AdamW::step's loop over parameters,
+ * crates/vearo-optim/src/lib.rs:105-123); no counterpart entry in the
+ * reference. */
+int vh_adamw_step_multi(int count, float* const* params, const float* const* grads, float* const* ms,
+                        float* const* vs, const int64_t* ns, int32_t t, float lr, float beta1, float beta2,
+                        float eps, float weight_decay, void* stream);
 
 /* --------------------------------------------- .ve checkpoints of device tensors -- */
 

@@ -168,6 +168,11 @@ SIGNATURES = {
         c_int,
         [fp, fp, fp, fp, c_int64, c_int32, c_float, c_float, c_float, c_float, c_float, c_void_p],
     ),
+    "vh_adamw_step_multi": (
+        c_int,
+        [c_int, POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p), POINTER(c_int64),
+         c_int32, c_float, c_float, c_float, c_float, c_float, c_void_p],
+    ),
     "vh_checkpoint_save": (c_int, [ctypes.c_char_p, c_int32, POINTER(c_void_p), POINTER(VhLayout), c_void_p]),
     "vh_checkpoint_load": (c_int, [ctypes.c_char_p, c_int32, POINTER(c_void_p), POINTER(VhLayout), c_void_p]),
 }

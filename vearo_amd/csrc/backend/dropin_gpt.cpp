@@ -425,19 +425,31 @@ struct vb_dropin {
   }
 
   // AdamW::step (optim:105-123).
+  // AdamW::step (optim:105-123): every gradient made contiguous, then every
+  // parameter updated -- in one vh_adamw_step_multi launch, each element as
+  // the per-parameter vh_adamw_step updates it (one launch per parameter left
+  // the small ones launch-bound: 21 launches, 0.52-0.60 ms a step).
   void adamw(float lr, float b1, float b2, float eps, float wd) {
     ++t;
+    std::vector<float*> ps, ms, vs;
+    std::vector<const float*> gs;
+    std::vector<int64_t> ns;
     for (size_t i = 0; i < P.size(); ++i) {
       if (!G[i].storage_id()) continue;
       if (!G[i].is_contiguous()) {
         G[i] = G[i].contiguous();
         mark(O_CONTIG);
       }
-      const int rc = vh_adamw_step(P[i].data(), G[i].data(), M[i].data(), V[i].data(), P[i].shape().numel(), t,
-                                   lr, b1, b2, eps, wd, nullptr);
-      if (rc != VH_OK) throw std::runtime_error(std::string("vh_adamw_step: ") + vh_last_error());
-      mark(O_ADAMW);
+      ps.push_back(P[i].data());
+      gs.push_back(G[i].data());
+      ms.push_back(M[i].data());
+      vs.push_back(V[i].data());
+      ns.push_back(P[i].shape().numel());
     }
+    const int rc = vh_adamw_step_multi((int)ps.size(), ps.data(), gs.data(), ms.data(), vs.data(), ns.data(), t, lr,
+                                       b1, b2, eps, wd, nullptr);
+    if (rc != VH_OK) throw std::runtime_error(std::string("vh_adamw_step_multi: ") + vh_last_error());
+    mark(O_ADAMW);
   }
 };
 

@@ -236,6 +236,7 @@ extern "C" __global__ void __launch_bounds__(256) vh_gemmb_fix_256(GemmArgs a) {
 // AdamW
 extern "C" __global__ void __launch_bounds__(256) vh_adamw_v1(AdamArgs a) { adamw_impl<1>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_adamw_v4(AdamArgs a) { adamw_impl<4>(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_adamw_multi(AdamMultiArgs a) { adamw_multi_impl(a); }
 
 // Row sums (bias gradients): first stage; the second is vh_col_reduce.
 extern "C" __global__ void __launch_bounds__(256) vh_col_partial(ColPartialArgs a) { col_partial_impl(a); }

@@ -2075,19 +2075,11 @@ static float powi_f32(float a, int b) {
   return recip ? 1.0f / r : r;
 }
 
-int vh_adamw_step(float* param, const float* grad, float* m, float* v, int64_t n, int32_t t, float lr,
-                  float beta1, float beta2, float eps, float weight_decay, void* stream) {
-  VH_TRY(require_init());
-  if (n < 0) return fail(VH_ERR_INVALID, "vh_adamw_step: negative size");
-  if (t < 1) return fail(VH_ERR_INVALID, "vh_adamw_step: step count t must be >= 1");
-  if (n == 0) return VH_OK;
-  if (!param || !grad || !m || !v) return fail(VH_ERR_INVALID, "vh_adamw_step: null pointer");
+namespace {
+// AdamW's hyper-parameters as the kernels take them (f32 roundings of the
+// reference's: 1 - beta, 1 - beta^t, lr * weight_decay).
+AdamArgs adam_hyper(int32_t t, float lr, float beta1, float beta2, float eps, float weight_decay) {
   AdamArgs a{};
-  a.p = param;
-  a.g = grad;
-  a.m = m;
-  a.v = v;
-  a.n = n;
   a.beta1 = beta1;
   a.beta2 = beta2;
   a.omb1 = 1.0f - beta1;
@@ -2097,6 +2089,63 @@ int vh_adamw_step(float* param, const float* grad, float* m, float* v, int64_t n
   a.lr = lr;
   a.lrwd = lr * weight_decay;
   a.eps = eps;
+  return a;
+}
+}  // namespace
+
+int vh_adamw_step_multi(int count, float* const* params, const float* const* grads, float* const* ms,
+                        float* const* vs, const int64_t* ns, int32_t t, float lr, float beta1, float beta2, float eps,
+                        float weight_decay, void* stream) {
+  VH_TRY(require_init());
+  if (count < 0) return fail(VH_ERR_INVALID, "vh_adamw_step_multi: negative count");
+  if (t < 1) return fail(VH_ERR_INVALID, "vh_adamw_step: step count t must be >= 1");
+  if (count > 0 && (!params || !grads || !ms || !vs || !ns))
+    return fail(VH_ERR_INVALID, "vh_adamw_step_multi: null array");
+  for (int i = 0; i < count; ++i) {
+    if (ns[i] < 0) return fail(VH_ERR_INVALID, "vh_adamw_step: negative size");
+    if (ns[i] > 0 && (!params[i] || !grads[i] || !ms[i] || !vs[i]))
+      return fail(VH_ERR_INVALID, "vh_adamw_step: null pointer");
+  }
+  AdamMultiArgs a{};
+  a.h = adam_hyper(t, lr, beta1, beta2, eps, weight_decay);
+  hipStream_t s = S(stream);
+  // Tensors in groups of up to VH_ADAMW_MULTI_MAX per launch, one unit per
+  // thread as vh_adamw_step; empty tensors take no blocks.
+  int64_t blocks = 0;
+  auto flush = [&]() -> int {
+    if (a.count == 0) return VH_OK;
+    const int rc = launch("vh_adamw_multi", (unsigned)blocks, 1, 256, 0, s, a);
+    a.count = 0;
+    blocks = 0;
+    return rc;
+  };
+  for (int i = 0; i < count; ++i) {
+    const int64_t n = ns[i];
+    if (n == 0) continue;
+    const bool vec = n % 4 == 0 && aligned16(params[i]) && aligned16(grads[i]) && aligned16(ms[i]) && aligned16(vs[i]);
+    const int64_t nb = cdiv(vec ? n / 4 : n, 256);
+    if (nb > INT32_MAX / 2) return fail(VH_ERR_UNSUPPORTED, "vh_adamw_step_multi: tensor too large");
+    if (a.count == VH_ADAMW_MULTI_MAX || blocks + nb > INT32_MAX / 2) VH_TRY(flush());
+    a.seg[a.count] = AdamSeg{params[i], grads[i], ms[i], vs[i], n, (int32_t)blocks, vec ? 1 : 0};
+    ++a.count;
+    blocks += nb;
+  }
+  return flush();
+}
+
+int vh_adamw_step(float* param, const float* grad, float* m, float* v, int64_t n, int32_t t, float lr,
+                  float beta1, float beta2, float eps, float weight_decay, void* stream) {
+  VH_TRY(require_init());
+  if (n < 0) return fail(VH_ERR_INVALID, "vh_adamw_step: negative size");
+  if (t < 1) return fail(VH_ERR_INVALID, "vh_adamw_step: step count t must be >= 1");
+  if (n == 0) return VH_OK;
+  if (!param || !grad || !m || !v) return fail(VH_ERR_INVALID, "vh_adamw_step: null pointer");
+  AdamArgs a = adam_hyper(t, lr, beta1, beta2, eps, weight_decay);
+  a.p = param;
+  a.g = grad;
+  a.m = m;
+  a.v = v;
+  a.n = n;
   const bool vec = n % 4 == 0 && aligned16(param) && aligned16(grad) && aligned16(m) && aligned16(v);
   // One unit per thread: over the 85 M parameters of the block step this runs
   // at 6.1 TB/s, against 5.3 TB/s for a grid of 8192 workgroups striding

@@ -136,6 +136,25 @@ struct AdamArgs {
   float lr, lrwd, eps;             // lrwd = lr * weight_decay (f32)
 };
 
+// Several parameter tensors in one launch: tensor s takes blocks
+// [blk0, blk0 + its units / 256 rounded up), units of 4 floats (vec) or 1.
+#define VH_ADAMW_MULTI_MAX 32
+struct AdamSeg {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  int64_t n;
+  int32_t blk0;
+  int32_t vec;
+};
+struct AdamMultiArgs {
+  AdamArgs h;  // the hyper-parameters (p, g, m, v, n unused)
+  int32_t count;
+  int32_t pad;
+  AdamSeg seg[VH_ADAMW_MULTI_MAX];
+};
+
 struct EltArgs {
   const float* x;
   const float* bias;  // [C] or null
