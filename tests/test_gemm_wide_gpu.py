@@ -1,11 +1,14 @@
 """The persistent GEMM's wide tile (256 x 256, kernels/gemm_big.h), which
-vh_gemm takes for products with at least VH_GEMMB_WIDE_K (8192) whole k tiles'
-worth of K and N >= 256 -- the block step's lm_head dx (K = 50260) and dW
-(K = 16384) products. Every operand layout, edges in M and N, a k tail left to
-the tiled kernel, bias / accumulate / alpha epilogues, operands only 4-byte
-aligned, and the stream-K round with its fix-up (fixed order: the same bits on
-a second call); against the oracle, float64 and the f32 error bound of a
-K-term sum (the checks of test_gemm_persistent_block_shapes)."""
+vh_gemm takes for products whose B is row-contiguous, with at least
+VH_GEMMB_WIDE_K (8192) of K in whole k tiles and N >= 256 -- the block step's
+lm_head dW ([50260, 768] = dlogits^T ln_f) and the drop-in's lm_head dx and
+weight gradients. Both such layouts (kn, mn), edges in M and N, a k tail left
+to the tiled kernel, bias / accumulate / alpha epilogues, operands only
+4-byte aligned, and the stream-K round with its fix-up (fixed order: the same
+bits on a second call); beside them the long-K products the narrow tile keeps
+(both operands k-contiguous, or A row-contiguous with B k-contiguous).
+Against the oracle, float64 and the f32 error bound of a K-term sum (the
+checks of test_gemm_persistent_block_shapes)."""
 import pytest
 
 from test_block_ops_gpu import test_gemm_persistent_block_shapes as check_persistent
@@ -20,12 +23,14 @@ pytestmark = pytest.mark.gpu
 # holds at any scale: the f32 error bound of a K-term sum.
 #   name, M, N, K, A k-contiguous, B k-contiguous, epilogue, a_scale[, offset]
 WIDE_CASES = [
-    ("kk, edges, bias + residual", 520, 600, 8224, True, True, "bias_acc", 1e-2),
     ("kn, lm_head dx shape, K tail", 512, 768, 50260, True, False, "", 1e-3),
     ("kn, alpha, bases one float off, K tail", 300, 1001, 9000, True, False, "alpha", 1e-2, 1),
-    ("mk, far-apart B rows", 1024, 768, 8192, False, True, "", 1.0),
-    ("mn, lm_head dW shape", 768, 1000, 16384, False, False, "", 1e-2),
+    ("kn, edges, bias + residual", 520, 600, 8224, True, False, "bias_acc", 1e-2),
+    ("mn, lm_head dW shape [V, D]", 1000, 768, 16384, False, False, "", 1e-2),
+    ("mn, lm_head dW^T shape [D, V]", 768, 1000, 16384, False, False, "", 1e-2),
     ("mn, odd M and N, 4-byte aligned", 1001, 777, 8192, False, False, "alpha_acc", 1e-2, 1),
+    ("narrow tile: kk, edges, bias + residual", 520, 600, 8224, True, True, "bias_acc", 1e-2),
+    ("narrow tile: mk, far-apart B rows", 1024, 768, 8192, False, True, "", 1.0),
 ]
 
 

@@ -219,7 +219,8 @@ extern "C" __global__ void __launch_bounds__(256) vh_gemm_reduce(GemmReduceArgs 
 
 // Large dense products: vh_gemmb_<A><B>_<BN>, persistent 256 x BN tiles (one
 // 512-thread workgroup per CU), and the fix-up of its stream-K round. BN = 256
-// for long k loops (K >= 8192: the lm_head dx and dW products), 192 otherwise.
+// for long k loops over a row-contiguous B (the lm_head dW products), 192
+// otherwise.
 #define K_GEMMB(AK, BK, BN, NAME) \
   extern "C" __global__ void __launch_bounds__(512, 1) NAME(GemmArgs a) { gemm_big_impl<AK, BK, BN, 8>(a); }
 K_GEMMB(true, true, 192, vh_gemmb_kk_192)

@@ -85,7 +85,7 @@ struct SoftmaxArgs {
 // rows x columns, and the workspace slots per workgroup of its stream-K round.
 #define VH_GEMMB_TM 256
 #define VH_GEMMB_TN 192       // the default tile width (and the smallest N it takes)
-#define VH_GEMMB_TN_WIDE 256  // the tile width for long k loops
+#define VH_GEMMB_TN_WIDE 256  // the tile width for long k loops over a row-contiguous B
 #define VH_GEMMB_WIDE_K 8192  // K (whole k tiles) from which the wide tile is used
 #define VH_GEMMB_SLOTS 2
 
