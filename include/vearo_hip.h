@@ -273,10 +273,14 @@ size_t vh_sum_rows_scratch_bytes(int64_t rows, int64_t C);
  * kernel, split along K where the output alone cannot fill the chip). TILED
  * forces the tiled kernel (tests of its split-K path); LIBRARY hands the
  * dense unbatched products hipBLASLt supports to it (an A/B reference for
- * benchmarks) and runs the rest as DEFAULT. No counterpart in the reference. */
+ * benchmarks) and runs the rest as DEFAULT; WIDE is DEFAULT with the
+ * persistent kernel's 256 x 256 tile wherever that kernel runs (tests of the
+ * tile DEFAULT picks only for long k loops over many tiles). No counterpart
+ * in the reference. */
 #define VH_GEMM_ENGINE_DEFAULT 0
 #define VH_GEMM_ENGINE_TILED 1
 #define VH_GEMM_ENGINE_LIBRARY 2
+#define VH_GEMM_ENGINE_WIDE 3
 
 /* C[m, n] = (C[m, n] +) alpha * sum_k A[m, k] B[k, n] (+ E[m, n]) over two batch
  * dims, on the f32 matrix cores. The epilogue order is v = acc*alpha;

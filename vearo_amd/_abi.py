@@ -59,7 +59,7 @@ class VhGemmDesc(ctypes.Structure):
 
 
 GEMM_DENSE, GEMM_SKIP_UPPER, GEMM_K_LE_M, GEMM_K_GE_M = 0, 1, 2, 3
-GEMM_ENGINE_DEFAULT, GEMM_ENGINE_TILED, GEMM_ENGINE_LIBRARY = 0, 1, 2
+GEMM_ENGINE_DEFAULT, GEMM_ENGINE_TILED, GEMM_ENGINE_LIBRARY, GEMM_ENGINE_WIDE = 0, 1, 2, 3
 GEMM_PATH_NONE, GEMM_PATH_TILED, GEMM_PATH_SPLIT_K, GEMM_PATH_PERSISTENT, GEMM_PATH_LIBRARY, GEMM_PATH_BATCHED = range(6)
 
 

@@ -1354,14 +1354,16 @@ thread_local int g_gemm_path = VH_GEMM_PATH_NONE;
 
 // The persistent 256 x BN-tile kernel (kernels/gemm_big.h) for a large dense
 // product, when its conditions hold; *taken reports whether it ran. BN = 256
-// when B is row-contiguous, the k loop is long (K >= VH_GEMMB_WIDE_K) and N
-// fills such tiles: a wider tile does a third more products per k-tile
-// barrier and loads 14 % fewer operand bytes per product (on MI355X, the
-// lm_head dW as [50260, 768] 9.16 -> 8.93 ms, as [768, 50260] 9.07 -> 8.92),
-// while its epilogue keeps fewer registers free (it spills), which short k
-// loops pay for (fc2 forward, K = 3072: 544 -> 593 us). With both operands
-// k-contiguous the narrow tile stays ahead even on long k loops (lm_head dx,
-// K = 50260: 8.65 against 9.00 ms).
+// when B is row-contiguous, the k loop is long (K >= VH_GEMMB_WIDE_K) and the
+// wide tiles fill at least one round of workgroups: a wider tile does a third
+// more products per k-tile barrier and loads 14 % fewer operand bytes per
+// product (on MI355X, the lm_head dW as [50260, 768] 9.16 -> 8.93 ms, as
+// [768, 50260] 9.07 -> 8.92), while its epilogue keeps fewer registers free
+// (it spills), which short k loops pay for (fc2 forward, K = 3072: 544 -> 593
+// us), and a product of fewer wide tiles than workgroups runs all of them in
+// the stream-K round (the [768, 768] weight gradient, K = 16384: 180 -> 196
+// us). With both operands k-contiguous the narrow tile stays ahead even on
+// long k loops (lm_head dx, K = 50260: 8.65 against 9.00 ms).
 // Conditions: 4-byte-aligned operand bases (its 128-bit loads need no more); a
 // tile's reads within 2^32 bytes of its origin (leading dimensions < 2^22); k
 // tile and tile counts below 2^31 (K < 2^26). A k-contiguous operand with
@@ -1386,7 +1388,10 @@ int gemm_big(const vh_gemm_desc* d, bool akc, bool bkc, int64_t lda, int64_t ldb
   const int64_t K32 = (akc || bkc) ? K / 32 * 32 : K;
   if (K32 == 0) return VH_OK;
   if (K32 % 32 != 0 && ((!akc && lda < M) || (!bkc && ldb < N))) return VH_OK;
-  const int64_t BN = !bkc && K32 >= VH_GEMMB_WIDE_K && N >= VH_GEMMB_TN_WIDE ? VH_GEMMB_TN_WIDE : VH_GEMMB_TN;
+  const bool wide = (d->engine == VH_GEMM_ENGINE_WIDE && N >= VH_GEMMB_TN_WIDE) ||
+                    (!bkc && K32 >= VH_GEMMB_WIDE_K && N >= VH_GEMMB_TN_WIDE &&
+                     cdiv(M, VH_GEMMB_TM) * cdiv(N, VH_GEMMB_TN_WIDE) * nb >= G);
+  const int64_t BN = wide ? VH_GEMMB_TN_WIDE : VH_GEMMB_TN;
   const int64_t tiles_m = cdiv(M, VH_GEMMB_TM), tiles_n = cdiv(N, BN);
   if (tiles_m * tiles_n * nb >= INT32_MAX) return VH_OK;
   const int64_t tiles = tiles_m * tiles_n * nb, rem = tiles % G;
@@ -1452,7 +1457,7 @@ int vh_gemm(const vh_gemm_desc* d, void* stream) {
     return fail(VH_ERR_UNSUPPORTED, "vh_gemm: B needs a unit stride along k or n");
   const int64_t lda = akc ? (M == 1 ? 0 : d->a_sm) : d->a_sk;
   const int64_t ldb = bkc ? (N == 1 ? 0 : d->b_sn) : d->b_sk;
-  if (d->engine < VH_GEMM_ENGINE_DEFAULT || d->engine > VH_GEMM_ENGINE_LIBRARY)
+  if (d->engine < VH_GEMM_ENGINE_DEFAULT || d->engine > VH_GEMM_ENGINE_WIDE)
     return fail(VH_ERR_INVALID, "vh_gemm: unknown engine");
   // LIBRARY: large unbatched dense products, with no addend or a bias over
   // the output columns, go to hipBLASLt when it has an algorithm (the A/B
