@@ -97,7 +97,12 @@ def launcher_kernel_names():
         for t, v in cfgs_all:
             names |= {f"vh_ln_fwd_t{t}_n{v}_v{vw}_r1", f"vh_sm_fwd_t{t}_n{v}_v{vw}_r1"}
         for t, v in cfgs_small:
-            names |= {f"vh_ln_bwd_t{t}_n{v}_v{vw}_b{max(t, 256)}", f"vh_sm_bwd_t{t}_n{v}_v{vw}_r1"}
+            names.add(f"vh_sm_bwd_t{t}_n{v}_v{vw}_r1")
+            if not (t == 1024 and v * vw > 16):  # longer rows take the streaming kernels
+                names.add(f"vh_ln_bwd_t{t}_n{v}_v{vw}_b{max(t, 256)}")
+        names |= {f"vh_sm_fwd_wide_v{vw}", f"vh_sm_bwd_wide_v{vw}", f"vh_ln_fwd_wide_v{vw}",
+                  f"vh_ln_stats_wide_v{vw}", f"vh_ln_tile_wide_v{vw}", f"vh_binary_rowbcast_v{vw}",
+                  f"vh_binary_colbcast_v{vw}", f"vh_emb_sum_v{vw}"}
         for t, v in multi:
             names |= {f"vh_ln_fwd_t{t}_n{v}_v{vw}_r2", f"vh_ln_fwd_t{t}_n{v}_v{vw}_r4",
                       f"vh_sm_fwd_t{t}_n{v}_v{vw}_r2", f"vh_sm_bwd_t{t}_n{v}_v{vw}_r2"}
@@ -117,7 +122,12 @@ def launcher_kernel_names():
               "vh_emb_tokens", "vh_emb_alloc", "vh_emb_place", "vh_fill", "vh_stream_copy",
               "vh_binary_strided_i32", "vh_binary_strided_i64", "vh_reduce_thread",
               "vh_reduce_wave", "vh_strided_copy_i32", "vh_strided_copy_i64", "vh_col_partial",
-              "vh_adamw_v1", "vh_adamw_v4", "vh_gemm_reduce"}
+              "vh_adamw_v1", "vh_adamw_v4", "vh_adamw_multi", "vh_gemm_reduce", "vh_emb_sort",
+              "vh_attn_probe", "vh_attn_decide"}
+    for bn in (192, 256):
+        names.add(f"vh_gemmb_fix_{bn}")
+        for lay in ("kk", "kn", "mk", "mn"):
+            names.add(f"vh_gemmb_{lay}_{bn}")
     for a in ("k4", "k1", "m4", "m1"):
         for b in ("k4", "k1", "n4", "n1"):
             names.add(f"vh_gemm_{a}_{b}")

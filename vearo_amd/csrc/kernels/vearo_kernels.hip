@@ -13,6 +13,7 @@
 #include "generic.h"
 #include "layernorm.h"
 #include "optim.h"
+#include "rowwide.h"
 #include "softmax.h"
 #include "xent.h"
 
@@ -62,7 +63,11 @@ K_LN_FWD_F(64, 1) K_LN_FWD_F(64, 2) K_LN_FWD_F(64, 3) K_LN_FWD_F(64, 4)
 #define K_LN_BWD(T, N, VW) K_LN_BWD_X(T, N, VW, BSLIT_##T)
 #define K_LN_BWD_512(T, N, VW) K_LN_BWD_B(T, N, VW, 512)
 ROW_CFG_SMALL(K_LN_BWD, 1)
-ROW_CFG_SMALL(K_LN_BWD, 4)
+// 128-bit units: rows held by 1024-thread teams up to 16 floats per lane (the
+// 24- and 32-float forms spilled; longer rows take kernels/rowwide.h).
+K_LN_BWD(16, 1, 4) K_LN_BWD(32, 1, 4) K_LN_BWD(64, 1, 4) K_LN_BWD(64, 2, 4) K_LN_BWD(64, 3, 4)
+K_LN_BWD(64, 4, 4) K_LN_BWD(64, 6, 4) K_LN_BWD(64, 8, 4) K_LN_BWD(1024, 1, 4) K_LN_BWD(1024, 2, 4)
+K_LN_BWD(1024, 3, 4) K_LN_BWD(1024, 4, 4)
 // Wave teams with rows up to 1024 units: 8 row-groups per workgroup.
 K_LN_BWD_512(64, 1, 1) K_LN_BWD_512(64, 2, 1) K_LN_BWD_512(64, 3, 1) K_LN_BWD_512(64, 4, 1)
 K_LN_BWD_512(64, 1, 4) K_LN_BWD_512(64, 2, 4) K_LN_BWD_512(64, 3, 4) K_LN_BWD_512(64, 4, 4)
@@ -141,6 +146,26 @@ extern "C" __global__ void __launch_bounds__(256) vh_emb_heavy_final_v4(EmbFinal
 extern "C" __global__ void __launch_bounds__(1024) vh_emb_sort(EmbSortArgs a) { emb_sort_impl(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_emb_sum_v1(EmbSumArgs a) { emb_sum_impl<1>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_emb_sum_v4(EmbSumArgs a) { emb_sum_impl<4>(a); }
+
+// Rows too long for the register-held row kernels (kernels/rowwide.h).
+#define K_WIDE(VW)                                                                                  \
+  extern "C" __global__ void __launch_bounds__(RW_TEAM) vh_sm_fwd_wide_v##VW(SoftmaxArgs a) {       \
+    sm_fwd_wide_impl<VW>(a);                                                                        \
+  }                                                                                                 \
+  extern "C" __global__ void __launch_bounds__(RW_TEAM) vh_sm_bwd_wide_v##VW(SoftmaxArgs a) {       \
+    sm_bwd_wide_impl<VW>(a);                                                                        \
+  }                                                                                                 \
+  extern "C" __global__ void __launch_bounds__(RW_TEAM) vh_ln_fwd_wide_v##VW(LnFwdArgs a) {         \
+    ln_fwd_wide_impl<VW>(a);                                                                        \
+  }                                                                                                 \
+  extern "C" __global__ void __launch_bounds__(RW_TEAM) vh_ln_stats_wide_v##VW(LnWideArgs a) {      \
+    ln_stats_wide_impl<VW>(a);                                                                      \
+  }                                                                                                 \
+  extern "C" __global__ void __launch_bounds__(256) vh_ln_tile_wide_v##VW(LnWideArgs a) {           \
+    ln_tile_wide_impl<VW>(a);                                                                       \
+  }
+K_WIDE(1)
+K_WIDE(4)
 
 // Cross-entropy
 // Up to NV = 104 (V <= 53,248) the kernels are held to 128 VGPRs: 4 waves per

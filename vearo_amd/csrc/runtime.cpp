@@ -210,6 +210,7 @@ int fill(void* p, float value, int64_t n, hipStream_t s) {
 }
 
 // --------------------------------------------------------- row engine cfg --
+constexpr unsigned RW_TEAM_HOST = 1024;  // threads of the streaming wide-row kernels (kernels/rowwide.h)
 struct RowCfg {
   int team, nv, vw;
   int rpw = 1;        // rows per team (forward kernels)
@@ -539,8 +540,13 @@ int vh_layernorm_fwd(const float* x, const float* w, const float* b, float* y, i
   if (C > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_fwd: C too large");
   RowCfg c;
   const bool vec = aligned16(x) && aligned16(w) && aligned16(b) && aligned16(y);
-  if (!pick_row_cfg(C, vec, 16, &c))
-    return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_fwd: C=" + std::to_string(C) + " exceeds 65536");
+  if (!pick_row_cfg(C, vec, 16, &c)) {
+    // Longer rows: one workgroup per row streams it (kernels/rowwide.h).
+    if (rows > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_fwd: too many rows");
+    LnFwdArgs a{x, w, b, y, rows, (int32_t)C, eps};
+    return launch(std::string("vh_ln_fwd_wide_v") + (vec && C % 4 == 0 ? "4" : "1"), (unsigned)rows, 1, RW_TEAM_HOST,
+                  0, S(stream), a);
+  }
   set_rpw(&c, kLnFwdRpw);
   set_ln_full(&c, C);
   if (c.full && c.rpw != 4) c.full = false;
@@ -548,21 +554,6 @@ int vh_layernorm_fwd(const float* x, const float* w, const float* b, float* y, i
   const int64_t rpb = (int64_t)(bs / c.team) * c.rpw;
   LnFwdArgs a{x, w, b, y, rows, (int32_t)C, eps};
   return launch(fwd_kernel("vh_ln_fwd", c), (unsigned)cdiv(rows, rpb), 1, bs, 0, S(stream), a);
-}
-
-size_t vh_layernorm_bwd_scratch_bytes(int64_t rows, int64_t C) {
-  // The largest need over the vector and scalar configurations (the one used
-  // depends on operand alignment).
-  if (rows <= 0 || C <= 0) return 0;
-  size_t need = 0;
-  for (bool vec : {true, false}) {
-    RowCfg c;
-    if (pick_row_cfg(C, vec, 8, &c)) {
-      set_ln_bwd_bs(&c);
-      need = std::max(need, align256((size_t)ln_bwd_blocks(rows, c) * 2 * (size_t)C * sizeof(float)));
-    }
-  }
-  return need;
 }
 
 }  // extern "C"
@@ -574,11 +565,30 @@ struct LnBwdPlan {
   RowCfg c;
   int64_t G;
   size_t need;
+  // Rows too long for the register kernel (or whose register form spills:
+  // 1024-thread teams holding more than 16 floats of x per lane): per-row
+  // statistics, then G row blocks of rpb rows under column tiles.
+  bool wide = false;
+  int vw = 1;
+  int64_t rpb = 0;
+  size_t stats_bytes = 0;
 };
 
 int ln_bwd_plan(int64_t rows, int64_t C, bool vec, LnBwdPlan* p) {
-  if (!pick_row_cfg(C, vec, 8, &p->c))
-    return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_bwd: C=" + std::to_string(C) + " exceeds 32768");
+  if (!pick_row_cfg(C, vec, 8, &p->c) || (p->c.team == 1024 && p->c.nv * p->c.vw > 16)) {
+    if (rows > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_layernorm_bwd: too many rows");
+    p->wide = true;
+    p->vw = vec && C % 4 == 0 ? 4 : 1;
+    const int64_t tiles = cdiv(C / p->vw, 256);
+    // About 1024 workgroups (column tiles x row blocks), at most 64 row blocks:
+    // the partials and the reduction order depend on (rows, C) only.
+    const int64_t want = std::max<int64_t>(1, std::min<int64_t>(64, cdiv(1024, tiles)));
+    p->rpb = cdiv(rows, std::min<int64_t>(rows, want));
+    p->G = cdiv(rows, p->rpb);
+    p->stats_bytes = align256((size_t)rows * 4 * sizeof(float));
+    p->need = p->stats_bytes + align256((size_t)p->G * 2 * (size_t)C * sizeof(float));
+    return VH_OK;
+  }
   set_ln_bwd_bs(&p->c);
   set_ln_full(&p->c, C);
   if (p->c.full && block_of(p->c) != 512) p->c.full = false;
@@ -590,6 +600,16 @@ int ln_bwd_plan(int64_t rows, int64_t C, bool vec, LnBwdPlan* p) {
 // Launches the backward with `part` as the partials buffer (at least p.need bytes).
 int ln_bwd_launch(const LnBwdPlan& p, const float* x, const float* w, const float* dy, float* dx, float* dw,
                   float* db, int64_t rows, int64_t C, float eps, float* part, hipStream_t s) {
+  if (p.wide) {
+    float* stats = part;
+    float* parts = reinterpret_cast<float*>(reinterpret_cast<char*>(part) + p.stats_bytes);
+    LnWideArgs a{x, w, dy, dx, stats, parts, rows, p.rpb, (int32_t)C, eps};
+    const std::string v = p.vw == 4 ? "4" : "1";
+    VH_TRY(launch("vh_ln_stats_wide_v" + v, (unsigned)rows, 1, RW_TEAM_HOST, 0, s, a));
+    VH_TRY(launch("vh_ln_tile_wide_v" + v, (unsigned)cdiv(C / p.vw, 256), (unsigned)p.G, 256, 0, s, a));
+    ColReduceArgs r{parts, dw, db, (int32_t)p.G, (int32_t)C, 2};
+    return launch("vh_col_reduce", (unsigned)cdiv(C, VH_COLR_COLS), 2, VH_COLR_COLS * 16, 0, s, r);
+  }
   const int bs = block_of(p.c);
   const int groups = bs / p.c.team;
   // Full-row forms fold in static LDS; the others in a dynamic pairwise tree.
@@ -620,6 +640,18 @@ int ln_bwd_check(const char* fn, const float* x, const float* w, const float* dy
 }  // namespace
 
 extern "C" {
+
+size_t vh_layernorm_bwd_scratch_bytes(int64_t rows, int64_t C) {
+  // The largest need over the vector and scalar configurations (the one used
+  // depends on operand alignment).
+  if (rows <= 0 || C <= 0) return 0;
+  size_t need = 0;
+  for (bool vec : {true, false}) {
+    LnBwdPlan p;
+    if (ln_bwd_plan(rows, C, vec, &p) == VH_OK) need = std::max(need, p.need);
+  }
+  return need;
+}
 
 int vh_layernorm_bwd(const float* x, const float* w, const float* dy, float* dx, float* dw,
                      float* db, int64_t rows, int64_t C, float eps, void* scratch,
@@ -757,8 +789,13 @@ static int softmax_common(const char* base, int cap, int rpw, const float* in, c
                           int attn = 0, int ztile = 0) {
   RowCfg c;
   const bool vec = aligned16(in) && aligned16(out) && (!dy || aligned16(dy));
-  if (!pick_row_cfg(T, vec, cap, &c))
-    return fail(VH_ERR_UNSUPPORTED, std::string(base) + ": T=" + std::to_string(T) + " too large");
+  if (!pick_row_cfg(T, vec, cap, &c)) {
+    // Longer rows: one workgroup per row streams it (kernels/rowwide.h).
+    if (rows > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, std::string(base) + ": too many rows");
+    SoftmaxArgs a{in, dy, out, rows, (int32_t)T, causal ? 1 : 0, input_is_x ? 1 : 0, attn, ztile, g_causal_flag};
+    return launch(std::string(base) + "_wide_v" + (vec && T % 4 == 0 ? "4" : "1"), (unsigned)rows, 1, RW_TEAM_HOST,
+                  0, s, a);
+  }
   // Rows of 129-256 units on two-wave teams holding 2 units per lane instead of
   // one wave holding 3-4: at T = 1024 (MI355X, warm clocks) the forward 204.7
   // against 216.9 us and the backward 271.2 against 278.9 us.

@@ -40,6 +40,21 @@ struct LnBwdArgs {
   float eps;
 };
 
+// LayerNorm backward over rows too long for the register kernels
+// (kernels/rowwide.h): per-row statistics, then column tiles over row blocks.
+struct LnWideArgs {
+  const float* x;
+  const float* w;
+  const float* dy;
+  float* dx;
+  float* stats;  // [rows][4]: mean, inv_std, sum(dy*w), sum(dy*w*xhat)
+  float* part;   // [row blocks][2][C] dgamma / dbeta partials
+  int64_t rows;
+  int64_t rpb;   // rows per row block
+  int32_t C;
+  float eps;
+};
+
 // Column reduction of [P][2][C] partials into dw[C], db[C] (fixed order).
 // Column reduce launch shape: VH_COLR_COLS columns per workgroup, 16 partial
 // ranges per column, so VH_COLR_COLS * 16 threads.
