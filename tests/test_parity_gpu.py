@@ -258,6 +258,41 @@ def test_embedding_heavy_token_clustered(vh):
     check_embedding_grad(fetch(vh, DW, (V, D)), ids, dy, V)
 
 
+@pytest.mark.parametrize("n,D,dist", [(40000, 96, "uniform"), (40000, 96, "zipf"), (82020, 64, "zipf")])
+def test_embedding_many_tokens(vh, n, D, dist):
+    """More positions than the sorted path takes (16384): the general path
+    (token histogram, per-row position slots sorted in registers) -- light rows
+    bit-exact, heavy rows within tolerance, two runs the same bits."""
+    print(f"embedding many tokens n={n} D={D} {dist}", flush=True)
+    r = rng(41)
+    V = 50257
+    ids = (r.integers(0, V, size=n).astype(np.float32) if dist == "uniform" else zipf_ids(r, n, V))
+    dy = r.normal(size=(n, D)).astype(np.float32)
+    I, DY = dev(vh, ids), dev(vh, dy)
+    A, B = out(vh, (V, D)), out(vh, (V, D))
+    vh.check(vh.lib.vh_embedding_bwd(I.ptr, DY.ptr, A.ptr, n, V, D, None, 0, None))
+    vh.check(vh.lib.vh_embedding_bwd(I.ptr, DY.ptr, B.ptr, n, V, D, None, 0, None))
+    a = fetch(vh, A, (V, D))
+    np.testing.assert_array_equal(a, fetch(vh, B, (V, D)))
+    check_embedding_grad(a, ids, dy, V)
+
+
+def test_embedding_many_tokens_report_first_bad_id(vh):
+    # Two bad ids far apart among 40000 positions: the panic names the first
+    # one in position order, as the CPU loop would.
+    n, V, D = 40000, 50257, 4
+    ids = np.arange(n, dtype=np.float32) % V
+    ids[35000], ids[20000] = -1.0, 60000.0
+    I, DY, DW = dev(vh, ids), dev(vh, np.ones((n, D))), out(vh, (V, D))
+    vh.check(vh.lib.vh_embedding_bwd(I.ptr, DY.ptr, DW.ptr, n, V, D, None, 0, None))
+    with pytest.raises(vh.DevicePanic) as ei:
+        vh.sync()
+    with pytest.raises(O.Panic) as eo:
+        O.embedding(ids, np.ones((V, D), np.float32))
+    assert ei.value.msg == str(eo.value) == "Token ID 60000 out of vocabulary bound 50257"
+    vh.sync()
+
+
 @pytest.mark.parametrize("bad,msg", [(-1.0, "Token ID cannot be negative: -1"),
                                      (7.0, "Token ID 7 out of vocabulary bound 5"),
                                      (4.5, "Token ID 5 out of vocabulary bound 5"),
