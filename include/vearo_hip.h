@@ -100,6 +100,15 @@ int vh_d2h(void* dst, const void* src, size_t bytes);
 int vh_d2d(void* dst, const void* src, size_t bytes, void* stream);
 /* out[i] = value for i < n (a fill kernel, never hipMemset). */
 int vh_fill_f32(float* out, float value, int64_t n, void* stream);
+/* Diagnostic, with no counterpart in the reference: y[i] = expf, logf or
+ * tanhf of x[i] (which = VH_MATH_EXP / LOG / TANH), evaluated by the same
+ * device functions the kernels call (softmax's and cross-entropy's exp,
+ * cross-entropy's log, GELU's tanh), for tests that bound their rounding
+ * against correctly rounded values and the C library's. */
+#define VH_MATH_EXP 0
+#define VH_MATH_LOG 1
+#define VH_MATH_TANH 2
+int vh_math_probe(int32_t which, const float* x, float* y, int64_t n, void* stream);
 int vh_mem_stats_get(vh_mem_stats* out);
 /* hipFree every cached (free) block. */
 int vh_empty_cache(void);

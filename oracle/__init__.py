@@ -64,6 +64,7 @@ def _load():
         "vo_cross_entropy": [f, L, f, L, f] + err,
         "vo_cross_entropy_backward": [f, L, f, L, f, c_int64, f] + err,
         "vo_gelu_grad_mask": [f, c_int64, f],
+        "vo_math": [c_int, f, f, c_int64],
         "vo_reduce_to": [f, L, POINTER(c_int64), c_int, f] + err,
         "vo_softmax_backward_composite": [f, f, L, c_int, f] + err,
         "vo_gelu_bias_forward": [f, f, c_int64, c_int64, f],
@@ -443,3 +444,12 @@ def checkpoint_save(path, arrays) -> None:
 def checkpoint_load(path, arrays) -> None:
     """load_checkpoint (checkpoint.rs:40-91) into float32 arrays, in place."""
     _ckpt_call(lib.vo_checkpoint_load, path, arrays)
+
+
+def math_fn(which, x):
+    """The C library's expf / logf / tanhf (which = 0 / 1 / 2) on every element."""
+    xb = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.empty_like(xb)
+    if xb.size:
+        lib.vo_math(int(which), _ptr(xb), _ptr(out), xb.size)
+    return out.reshape(np.shape(x))

@@ -634,3 +634,8 @@ void vo_gelu_bias_backward(const float* x, const float* bias, const float* dy,
       dbias[c] += g;
     }
 }
+
+/* ---------------------------------------------------------- libm probe */
+void vo_math(int which, const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = which == 0 ? expf(x[i]) : which == 1 ? logf(x[i]) : tanhf(x[i]);
+}

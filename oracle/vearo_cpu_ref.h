@@ -171,6 +171,12 @@ int vo_gpt_step_ex(const vo_gpt_config* c, const float* const* params, const flo
                    const float* targets, int unfused, float* loss, float* const* grads, char* err,
                    size_t errlen);
 
+/* y[i] = expf / logf / tanhf (x[i]) (which = 0 / 1 / 2): the C library's
+ * functions, as every oracle function above calls them (the reference's f32
+ * `exp`, `ln`, `tanh` call the same libm on Linux). For tests that bound their
+ * rounding against correctly rounded values. */
+void vo_math(int which, const float* x, float* y, int64_t n);
+
 /* `.ve` weight checkpoint (crates/vearo/src/checkpoint.rs:9-91), host tensors. */
 int vo_checkpoint_save(const char* path, int n, const float* const* data, const vo_layout* layouts, char* err,
                        size_t errlen);

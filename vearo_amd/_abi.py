@@ -60,6 +60,7 @@ class VhGemmDesc(ctypes.Structure):
 
 GEMM_DENSE, GEMM_SKIP_UPPER, GEMM_K_LE_M, GEMM_K_GE_M = 0, 1, 2, 3
 GEMM_ENGINE_DEFAULT, GEMM_ENGINE_TILED, GEMM_ENGINE_LIBRARY, GEMM_ENGINE_WIDE = 0, 1, 2, 3
+MATH_EXP, MATH_LOG, MATH_TANH = 0, 1, 2
 GEMM_PATH_NONE, GEMM_PATH_TILED, GEMM_PATH_SPLIT_K, GEMM_PATH_PERSISTENT, GEMM_PATH_LIBRARY, GEMM_PATH_BATCHED = range(6)
 
 
@@ -94,6 +95,7 @@ SIGNATURES = {
     "vh_d2h": (c_int, [c_void_p, c_void_p, c_size_t]),
     "vh_d2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "vh_fill_f32": (c_int, [fp, c_float, c_int64, c_void_p]),
+    "vh_math_probe": (c_int, [c_int32, fp, fp, c_int64, c_void_p]),
     "vh_mem_stats_get": (c_int, [POINTER(VhMemStats)]),
     "vh_empty_cache": (c_int, []),
     "vh_layernorm_fwd": (c_int, [fp, fp, fp, fp, c_int64, c_int64, c_float, c_void_p]),

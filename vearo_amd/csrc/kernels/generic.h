@@ -156,6 +156,17 @@ VH_DEV void transpose_impl(const TransposeArgs& a) {
   }
 }
 
+// The device's expf / logf / tanhf as the kernels call them (softmax's and
+// cross-entropy's exp, cross-entropy's log, GELU's tanh): same functions,
+// same build flags, one element per thread.
+VH_DEV void math_probe_impl(const MathProbeArgs& a) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride) {
+    const float v = a.x[i];
+    a.y[i] = a.fn == 0 ? expf(v) : a.fn == 1 ? logf(v) : tanhf(v);
+  }
+}
+
 VH_DEV void fill_impl(const FillArgs& a) {
   const int64_t n4 = (reinterpret_cast<uintptr_t>(a.p) & 15) ? 0 : a.n / 4;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;

@@ -205,6 +205,7 @@ extern "C" __global__ void __launch_bounds__(256) vh_transpose(TransposeArgs a) 
 extern "C" __global__ void __launch_bounds__(256) vh_attn_probe(AttnProbeArgs a) { attn_probe_impl(a); }
 extern "C" __global__ void __launch_bounds__(64) vh_attn_decide(AttnDecideArgs a) { attn_decide_impl(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_fill(FillArgs a) { fill_impl(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_math_probe(MathProbeArgs a) { math_probe_impl(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_stream_copy(StreamCopyArgs a) { stream_copy_impl(a); }
 
 // Matrix multiply: vh_gemm_<A><B>, each operand k-contiguous ("k") or

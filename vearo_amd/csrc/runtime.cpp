@@ -512,6 +512,15 @@ int vh_fill_f32(float* out, float value, int64_t n, void* stream) {
   return fill(out, value, n, S(stream));
 }
 
+int vh_math_probe(int32_t which, const float* x, float* y, int64_t n, void* stream) {
+  VH_TRY(require_init());
+  if (which < VH_MATH_EXP || which > VH_MATH_TANH) return fail(VH_ERR_INVALID, "vh_math_probe: unknown function");
+  if (n < 0 || (n > 0 && (!x || !y))) return fail(VH_ERR_INVALID, "vh_math_probe: bad arguments");
+  if (n == 0) return VH_OK;
+  MathProbeArgs a{x, y, n, which};
+  return launch("vh_math_probe", (unsigned)std::min<int64_t>(cdiv(n, 256), 8192), 1, 256, 0, S(stream), a);
+}
+
 int vh_mem_stats_get(vh_mem_stats* out) {
   if (!out) return fail(VH_ERR_INVALID, "vh_mem_stats_get: null out");
   std::lock_guard<std::mutex> lk(g_arena.mu);

@@ -385,6 +385,14 @@ struct FillArgs {
   float value;
 };
 
+// Diagnostic: y[i] = expf / logf / tanhf (x[i]) (fn = VH_MATH_EXP / LOG / TANH).
+struct MathProbeArgs {
+  const float* x;
+  float* y;
+  int64_t n;
+  int32_t fn;
+};
+
 // Device-to-device copy of n4 16-byte units (both pointers 16-byte aligned).
 struct StreamCopyArgs {
   const float* src;
