@@ -518,12 +518,21 @@ VH_DEV uint32_t lanes_below(unsigned long long m) {
 // atomics that set them.)
 VH_DEV void emb_sort_impl(const EmbSortArgs& a) {
   if ((int)blockIdx.x >= EMB_RANGES) {
+    // Four stores per iteration (one grid stride apart), then the rest.
     const int64_t stride = (int64_t)(gridDim.x - EMB_RANGES) * blockDim.x;
-    for (int64_t u = (int64_t)(blockIdx.x - EMB_RANGES) * blockDim.x + threadIdx.x; u < a.fill_n; u += stride) {
-      if (a.vec)
-        store_stream<4>(a.dW + u * 4, zero_unit<4>());
-      else
-        store_stream<1>(a.dW + u, zero_unit<1>());
+    int64_t u = (int64_t)(blockIdx.x - EMB_RANGES) * blockDim.x + threadIdx.x;
+    if (a.vec) {
+      for (; u + 3 * stride < a.fill_n; u += 4 * stride) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) store_stream<4>(a.dW + (u + j * stride) * 4, zero_unit<4>());
+      }
+      for (; u < a.fill_n; u += stride) store_stream<4>(a.dW + u * 4, zero_unit<4>());
+    } else {
+      for (; u + 3 * stride < a.fill_n; u += 4 * stride) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) store_stream<1>(a.dW + u + j * stride, zero_unit<1>());
+      }
+      for (; u < a.fill_n; u += stride) store_stream<1>(a.dW + u, zero_unit<1>());
     }
     return;
   }
