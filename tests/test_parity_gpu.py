@@ -87,6 +87,12 @@ def test_layernorm_explicit_scratch_and_errors(vh):
     _, dw_cpu, db_cpu = O.layernorm_backward(x, w, np.zeros(C, np.float32), dy, 1e-5)
     assert_parity(fetch(vh, DB, (C,)), db_cpu, dy.astype(np.float64).sum(0), name="dbeta")
     assert vh.lib.vh_layernorm_fwd(X.ptr, W.ptr, W.ptr, DX.ptr, -1, C, 1e-5, None) == vh.VH_ERR_INVALID
+    # Rows longer than int32 are refused before any launch, by both entries.
+    big = 1 << 31
+    assert vh.lib.vh_layernorm_fwd(X.ptr, W.ptr, W.ptr, DX.ptr, 1, big, 1e-5, None) == vh.VH_ERR_UNSUPPORTED
+    for rc in (vh.lib.vh_layernorm_bwd(X.ptr, W.ptr, DY.ptr, DX.ptr, DW.ptr, DB.ptr, 1, big, 1e-5, None, 0, None),
+               vh.lib.vh_layernorm_bwd_noalloc(X.ptr, W.ptr, DY.ptr, DX.ptr, DW.ptr, DB.ptr, 1, big, 1e-5, None)):
+        assert rc == vh.VH_ERR_UNSUPPORTED and "C too large" in vh.last_error()
 
 
 # ----------------------------------------------------------------------- gelu
