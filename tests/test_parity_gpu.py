@@ -139,7 +139,7 @@ def causal_scores(r, B, H, T):
 # (1, 1, 201): 201 one-float units on two-wave teams and an odd row count, so a
 # workgroup's second team has no row; (1, 3, 600): 150 four-float units.
 @pytest.mark.parametrize("B,H,T", [(2, 12, 1024), (1, 2, 37), (2, 3, 128), (1, 1, 1000),
-                                   (1, 1, 2048), (1, 1, 5000), (1, 1, 201), (1, 3, 600)])
+                                   (1, 1, 2048), (1, 1, 5000), (1, 1, 201), (1, 3, 600), (2, 3, 1), (1, 1, 3)])
 @pytest.mark.parametrize("causal", [0, 1])
 def test_softmax_fwd_bwd(vh, B, H, T, causal):
     print(f"softmax B={B} H={H} T={T} causal={causal}", flush=True)
@@ -168,9 +168,8 @@ def test_softmax_dense_rows(vh):
         dy = r.normal(size=(rows, T)).astype(np.float32)
         X, DY, Y, DX = dev(vh, x), dev(vh, dy), out(vh, x.shape), out(vh, x.shape)
         vh.check(vh.lib.vh_softmax_fwd(X.ptr, Y.ptr, rows, T, 0, None))
-        if T <= 32768:
-            vh.check(vh.lib.vh_softmax_bwd(X.ptr, DY.ptr, DX.ptr, rows, T, 1, 0, None))
-            assert_parity(fetch(vh, DX, x.shape), O.softmax_backward_composite(x, dy, 1), name="dx")
+        vh.check(vh.lib.vh_softmax_bwd(X.ptr, DY.ptr, DX.ptr, rows, T, 1, 0, None))
+        assert_parity(fetch(vh, DX, x.shape), O.softmax_backward_composite(x, dy, 1), name=f"dx T={T}")
         assert_parity(fetch(vh, Y, x.shape), O.softmax(x, 1), name=f"y T={T}")
 
 
