@@ -123,7 +123,7 @@ def launcher_kernel_names():
               "vh_binary_strided_i32", "vh_binary_strided_i64", "vh_reduce_thread",
               "vh_reduce_wave", "vh_strided_copy_i32", "vh_strided_copy_i64", "vh_col_partial",
               "vh_adamw_v1", "vh_adamw_v4", "vh_adamw_multi", "vh_gemm_reduce", "vh_emb_sort",
-              "vh_attn_probe", "vh_attn_decide", "vh_math_probe"}
+              "vh_attn_probe", "vh_attn_decide", "vh_math_probe", "vh_transpose", "vh_transpose_v4"}
     for bn in (192, 256):
         names.add(f"vh_gemmb_fix_{bn}")
         for lay in ("kk", "kn", "mk", "mn"):

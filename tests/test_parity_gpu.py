@@ -461,7 +461,9 @@ def test_strided_copy_transposed_views(vh):
     exact copies, edge tiles included."""
     r = rng(8)
     cases = [((777, 1000), None), ((3, 130, 67), (0, 2, 1)), ((3, 130, 67), (1, 0, 2)), ((2, 3, 65, 129), (0, 1, 3, 2)),
-             ((64, 64), None), ((17, 5000), None)]
+             ((64, 64), None), ((17, 5000), None),
+             # 128-bit form (sizes and strides multiples of 4), edge tiles included
+             ((768, 1024), None), ((68, 132), None), ((2, 3, 64, 132), (0, 1, 3, 2)), ((4, 36, 200), (0, 2, 1))]
     for shape, perm in cases:
         x = r.normal(size=shape).astype(np.float32)
         X = dev(vh, x)

@@ -156,6 +156,41 @@ VH_DEV void transpose_impl(const TransposeArgs& a) {
   }
 }
 
+// transpose_impl with 128-bit accesses on both sides: a thread loads 4
+// consecutive r of one c and stores 4 consecutive c of one r. The host takes
+// it when R, C and every stride are multiples of 4 and both bases are 16-byte
+// aligned, so each 4-run is wholly inside or outside the matrix. LDS t[c][r]
+// with a 65-float row: the writes (4 r of one c per thread) and the reads (one
+// r of 4 c per thread) each hit 64 distinct banks per wave.
+VH_DEV void transpose4_impl(const TransposeArgs& a) {
+  __shared__ float t[64][65];
+  const int q = threadIdx.x & 15, p = threadIdx.x >> 4;
+  const int64_t c0 = (int64_t)blockIdx.x * 64, r0 = (int64_t)blockIdx.y * 64;
+  const int64_t b = blockIdx.z;
+  const float* src = a.src + (b / a.nb1) * a.sb0 + (b % a.nb1) * a.sb1;
+  float* dst = a.dst + b * a.R * a.C;
+  const int64_t r = r0 + 4 * q;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t c = c0 + p + 16 * i;
+    if (r < a.R && c < a.C) {
+      const float4 v = *reinterpret_cast<const float4*>(src + r + c * a.sc);
+      float* row = &t[p + 16 * i][4 * q];
+      row[0] = v.x; row[1] = v.y; row[2] = v.z; row[3] = v.w;
+    }
+  }
+  __syncthreads();
+  const int64_t c = c0 + 4 * q;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int rl = p + 16 * i;
+    const int64_t rr = r0 + rl;
+    if (rr < a.R && c < a.C)
+      *reinterpret_cast<float4*>(dst + rr * a.C + c) =
+          make_float4(t[4 * q][rl], t[4 * q + 1][rl], t[4 * q + 2][rl], t[4 * q + 3][rl]);
+  }
+}
+
 // The device's expf / logf / tanhf as the kernels call them (softmax's and
 // cross-entropy's exp, cross-entropy's log, GELU's tanh): same functions,
 // same build flags, one element per thread.

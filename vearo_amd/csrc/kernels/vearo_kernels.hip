@@ -202,6 +202,7 @@ extern "C" __global__ void __launch_bounds__(256) vh_reduce_wave(ReduceArgs a) {
 extern "C" __global__ void __launch_bounds__(256) vh_strided_copy_i32(CopyArgs a) { strided_copy_impl<uint32_t>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_strided_copy_i64(CopyArgs a) { strided_copy_impl<uint64_t>(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_transpose(TransposeArgs a) { transpose_impl(a); }
+extern "C" __global__ void __launch_bounds__(256) vh_transpose_v4(TransposeArgs a) { transpose4_impl(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_attn_probe(AttnProbeArgs a) { attn_probe_impl(a); }
 extern "C" __global__ void __launch_bounds__(64) vh_attn_decide(AttnDecideArgs a) { attn_decide_impl(a); }
 extern "C" __global__ void __launch_bounds__(256) vh_fill(FillArgs a) { fill_impl(a); }

@@ -1270,8 +1270,10 @@ int vh_strided_copy(const float* src, const vh_layout* sl, float* dst, void* str
       t.sb0 = sl->strides[0];
       t.sb1 = sl->strides[1];
     }
+    const bool v4 = t.R % 4 == 0 && t.C % 4 == 0 && t.sc % 4 == 0 && t.sb0 % 4 == 0 && t.sb1 % 4 == 0 &&
+                    aligned16(src) && aligned16(dst);
     if (cdiv(t.C, 64) < (int64_t(1) << 31) && cdiv(t.R, 64) < 65536 && nb < 65536)
-      return launch("vh_transpose", cdiv(t.C, 64), cdiv(t.R, 64), 256, 0, s, t, nb);
+      return launch(v4 ? "vh_transpose_v4" : "vh_transpose", cdiv(t.C, 64), cdiv(t.R, 64), 256, 0, s, t, nb);
   }
   CopyArgs a{src, dst, to_kl(*sl), n};
   const int64_t blocks = std::min<int64_t>(cdiv(n, 256), 16384);
