@@ -19,9 +19,10 @@
 // The attention's q/k/v/out stay in the Linear layout [B, S, H, Dk] (q, k, v as
 // column blocks of one [B*S, 3D] buffer); the reshape/transpose views of
 // nn:585-601 are passed as strides, so no copy runs.
-// The logits and their gradient have rows padded to Vp = V rounded up to 4
+// The logits and their gradient have rows padded to Vp = V rounded up to 32
 // (zero columns), and lm_head's weight is followed by Vp - V zero rows, so the
-// three lm_head products run on 128-bit loads; the padding adds exact zeros.
+// three lm_head products run on 128-bit loads and the dx product (K = Vp) in
+// whole k tiles, with no tail product; the padding adds exact zeros.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -312,7 +313,7 @@ int vb_gpt_create(const vb_gpt_config* cfg, vb_gpt** out) {
   g->c = c;
   g->R = c.B * c.S;
   g->Dk = c.D / c.H;
-  g->Vp = (c.V + 3) / 4 * 4;
+  g->Vp = (c.V + 31) / 32 * 32;
   const int64_t D = c.D, F = c.F;
   const int64_t sizes[VB_GPT_NPARAMS] = {c.V * D, c.P * D, D, D, D * D, D, D * D, D, D * D, D, D * D, D,
                                          D,       D,       F * D, F, D * F, D, D, D, c.V * D};
