@@ -84,3 +84,24 @@ def max_errs(gpu, cpu):
 
 def ptr(buf):
     return ctypes.c_void_p(buf.ptr)
+
+
+# Float64 statements of the row ops, for the fallback of assert_parity where a
+# long f32 sum makes the oracle drift (non-finite inputs give NaN rows).
+def ln64(x, w, b, eps, dy):
+    x = x.astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        m = x.mean(1, keepdims=True)
+        rstd = 1.0 / np.sqrt(((x - m) ** 2).mean(1, keepdims=True) + eps)
+        xh = (x - m) * rstd
+        g = dy * w
+        dx = rstd * (g - g.mean(1, keepdims=True) - xh * (g * xh).mean(1, keepdims=True))
+    return xh * w + b, dx
+
+
+def softmax64(x, dy):
+    x = x.astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        e = np.exp(x - x.max(1, keepdims=True))
+        y = e / e.sum(1, keepdims=True)
+        return y, y * (dy - (dy * y).sum(1, keepdims=True))

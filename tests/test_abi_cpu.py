@@ -112,7 +112,7 @@ def launcher_kernel_names():
                 names |= {f"vh_ln_bwd_t64_n{v}_v4_b512_f", f"vh_ln_fwd_t64_n{v}_v4_r4_f"}
         for v in nv:
             names.add(f"vh_gelu_bias_fwd_n{v}_v{vw}")
-        names.add(f"vh_gelu_bias_bwd_tile_v{vw}")
+        names |= {f"vh_gelu_bias_bwd_tile_v{vw}", f"vh_gelu_bias_fwd_tile_v{vw}"}
         names |= {f"vh_sm_fwd_t128_n2_v{vw}_r1", f"vh_sm_bwd_t128_n2_v{vw}_r1"}
         names |= {f"vh_gelu_fwd_v{vw}", f"vh_gelu_gradmul_v{vw}", f"vh_emb_fwd_v{vw}",
                   f"vh_emb_rows_v{vw}", f"vh_emb_heavy_final_v{vw}", f"vh_binary_contig_v{vw}"}

@@ -98,8 +98,10 @@ def test_layernorm_explicit_scratch_and_errors(vh):
 # ----------------------------------------------------------------------- gelu
 # (2500, 768) and (20000, 192): row blocks of 3 and 20 rows (at most 1024
 # dbias partials), so a block's rows end partway through a batch of loads.
+# (5, 4097), (3, 20000), (2, 70001): rows wider than the forward's registers
+# hold (4096 single floats, 16384 as 128-bit units) take its column-tile form.
 @pytest.mark.parametrize("rows,C", [(16384, 3072), (3, 5), (33, 100), (7, 4096), (5, 5000), (2500, 768),
-                                    (20000, 192)])
+                                    (20000, 192), (5, 4097), (3, 20000), (2, 70001)])
 def test_gelu_bias_fwd_bwd(vh, rows, C):
     print(f"gelu_bias rows={rows} C={C}", flush=True)
     r = rng(1)
@@ -114,6 +116,26 @@ def test_gelu_bias_fwd_bwd(vh, rows, C):
     dx_cpu, db_cpu = O.gelu_bias_backward(x, bias, dy)
     assert_parity(fetch(vh, DX, (rows, C)), dx_cpu, name="dx")
     assert_parity(fetch(vh, DB, (C,)), db_cpu, dx_cpu.astype(np.float64).sum(0), name="dbias")
+
+
+def test_gelu_bias_fwd_tile_form_same_bits(vh):
+    """The column-tile forward (rows past the register form's width) gives the
+    register form's bits: C = 4100 runs in registers as 128-bit units from
+    aligned buffers and as column tiles of single floats one float past them."""
+    r = rng(9)
+    rows, C = 6, 4100
+    x = (2.0 * r.normal(size=(rows, C))).astype(np.float32)
+    bias = r.normal(size=C).astype(np.float32)
+    X, Bi, Y = dev(vh, x), dev(vh, bias), out(vh, (rows, C))
+    vh.check(vh.lib.vh_gelu_bias_fwd(X.ptr, Bi.ptr, Y.ptr, rows, C, None))
+    X1 = dev(vh, np.concatenate([[0.0], x.reshape(-1)]))
+    B1 = dev(vh, np.concatenate([[0.0], bias]))
+    Y1 = out(vh, (rows * C + 1,))
+    vh.check(vh.lib.vh_gelu_bias_fwd(X1.ptr + 4, B1.ptr + 4, Y1.ptr + 4, rows, C, None))
+    a = fetch(vh, Y, (rows, C))
+    b = fetch(vh, Y1, (rows * C + 1,))[1:].reshape(rows, C)
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert_parity(a, O.gelu_bias_forward(x, bias), name="gelu(x + b) C=4100")
 
 
 @pytest.mark.parametrize("n", [1, 7, 4096, 1000003])

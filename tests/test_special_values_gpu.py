@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from parity import assert_parity, dev, fetch, out
+from parity import assert_parity, dev, fetch, ln64, out, softmax64
 
 pytestmark = pytest.mark.gpu
 
@@ -28,25 +28,6 @@ def same(gpu, cpu, name, ref64=None):
     assert np.array_equal(gpu[inf], cpu[inf]) and not np.isinf(gpu[~inf]).any(), f"{name}: infinity mismatch"
     fin = np.isfinite(cpu)
     assert_parity(gpu[fin], cpu[fin], None if ref64 is None else np.asarray(ref64, np.float64)[fin], name=name)
-
-
-def ln64(x, w, b, eps, dy):
-    x = x.astype(np.float64)
-    with np.errstate(invalid="ignore", over="ignore"):
-        m = x.mean(1, keepdims=True)
-        rstd = 1.0 / np.sqrt(((x - m) ** 2).mean(1, keepdims=True) + eps)
-        xh = (x - m) * rstd
-        g = dy * w
-        dx = rstd * (g - g.mean(1, keepdims=True) - xh * (g * xh).mean(1, keepdims=True))
-    return xh * w + b, dx
-
-
-def softmax64(x, dy):
-    x = x.astype(np.float64)
-    with np.errstate(invalid="ignore", over="ignore"):
-        e = np.exp(x - x.max(1, keepdims=True))
-        y = e / e.sum(1, keepdims=True)
-        return y, y * (dy - (dy * y).sum(1, keepdims=True))
 
 
 def test_gelu_special_values(vh):

@@ -12,7 +12,8 @@
 // workgroup, one unit per lane, so every wave streams 64 consecutive units of
 // a row (the layout a plain copy streams best in) and the dbias partial of the
 // tile's columns is summed in the workgroup. Every tensor byte moves once (fwd
-// 8 B/elem, bwd 12 B/elem) and dbias needs no atomics.
+// 8 B/elem, bwd 12 B/elem) and dbias needs no atomics. Rows wider than the
+// forward's registers hold take a column-tile forward of the backward's shape.
 #pragma once
 #include "common.h"
 
@@ -83,6 +84,29 @@ VH_DEV void gelu_bias_fwd_impl(const GeluBiasBwdArgs& a) {
         store_stream<VW>(yr + u * VW, o);
       }
     }
+  }
+}
+
+// The same forward for rows wider than one workgroup holds in registers
+// (past 256 x 16 units): a tile of 64 column units by one row block per
+// 256-thread workgroup, one unit per lane, wave w taking rows r0 + w, r0 + w +
+// 4, ...; the same gelu(x + b) per element, so the same bits.
+template <int VW>
+VH_DEV void gelu_bias_fwd_tile_impl(const GeluBiasBwdArgs& a) {
+  const int64_t C = a.C;
+  const int64_t U = C / VW;
+  const int64_t u = (int64_t)blockIdx.x * 64 + (threadIdx.x & 63);
+  if (u >= U) return;
+  const Unit<VW> b = load_unit<VW>(a.bias + u * VW);
+  const int64_t r0 = (int64_t)blockIdx.y * a.rows_per_block;
+  int64_t r1 = r0 + a.rows_per_block;
+  if (r1 > a.rows) r1 = a.rows;
+  for (int64_t r = r0 + (threadIdx.x >> 6); r < r1; r += 4) {
+    const Unit<VW> x = load_stream<VW>(a.x + r * C + u * VW);
+    Unit<VW> o;
+#pragma unroll
+    for (int j = 0; j < VW; ++j) o.v[j] = gelu_f(x.v[j] + b.v[j]);
+    store_stream<VW>(a.dx + r * C + u * VW, o);
   }
 }
 

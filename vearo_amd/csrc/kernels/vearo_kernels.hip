@@ -128,8 +128,14 @@ extern "C" __global__ void __launch_bounds__(256) vh_gelu_gradmul_v4(EltArgs a) 
   extern "C" __global__ void __launch_bounds__(256) vh_gelu_bias_bwd_tile_v##VW(GeluBiasBwdArgs a) { \
     gelu_bias_bwd_tile_impl<VW, 2>(a);                                                    \
   }
+#define K_GB_FWD_TILE(VW)                                                                 \
+  extern "C" __global__ void __launch_bounds__(256) vh_gelu_bias_fwd_tile_v##VW(GeluBiasBwdArgs a) { \
+    gelu_bias_fwd_tile_impl<VW>(a);                                                     \
+  }
 GB_CFG(K_GB_FWD, 1)
 GB_CFG(K_GB_FWD, 4)
+K_GB_FWD_TILE(1)
+K_GB_FWD_TILE(4)
 K_GB_BWD(1)
 K_GB_BWD(4)
 

@@ -744,9 +744,17 @@ int vh_gelu_bias_fwd(const float* x, const float* bias, float* y, int64_t rows, 
   if (rows < 0 || C < 0) return fail(VH_ERR_INVALID, "vh_gelu_bias_fwd: negative size");
   if (rows == 0 || C == 0) return VH_OK;
   if (!x || !bias || !y) return fail(VH_ERR_INVALID, "vh_gelu_bias_fwd: null pointer");
+  if (C > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_gelu_bias_fwd: C too large");
   int nv, vw;
-  if (!gb_cfg(C, aligned16(x) && aligned16(bias) && aligned16(y), &nv, &vw))
-    return fail(VH_ERR_UNSUPPORTED, "vh_gelu_bias_fwd: C too large");
+  if (!gb_cfg(C, aligned16(x) && aligned16(bias) && aligned16(y), &nv, &vw)) {
+    // Rows wider than a workgroup's registers: 64-unit column tiles by row
+    // blocks (the backward's grid), the same bits.
+    const int64_t G0 = gb_blocks(rows);
+    const int64_t rpb = cdiv(rows, G0);
+    GeluBiasBwdArgs a{x, bias, nullptr, y, nullptr, rows, rpb, (int32_t)C};
+    return launch("vh_gelu_bias_fwd_tile_v" + std::to_string(vw), cdiv(C / vw, 64), cdiv(rows, rpb), 256, 0,
+                  S(stream), a);
+  }
   // One row per workgroup: 68.5 us at [16384, 3072] against 80 us for 4096
   // workgroups of 4 rows each (measured; the bias is re-read from L2 per row).
   const int64_t G = std::max<int64_t>(1, std::min<int64_t>(rows, INT32_MAX));
@@ -770,9 +778,9 @@ int vh_gelu_bias_bwd(const float* x, const float* bias, const float* dy, float* 
   if (!dbias) return fail(VH_ERR_INVALID, "vh_gelu_bias_bwd: null pointer");
   if (rows == 0) return fill(dbias, 0.0f, C, s);
   if (!x || !bias || !dy || !dx) return fail(VH_ERR_INVALID, "vh_gelu_bias_bwd: null pointer");
-  int nv, vw;
-  if (!gb_cfg(C, aligned16(x) && aligned16(bias) && aligned16(dy) && aligned16(dx), &nv, &vw))
-    return fail(VH_ERR_UNSUPPORTED, "vh_gelu_bias_bwd: C too large");
+  if (C > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_gelu_bias_bwd: C too large");
+  // The column-tile kernel takes any width.
+  const int vw = (aligned16(x) && aligned16(bias) && aligned16(dy) && aligned16(dx) && C % 4 == 0) ? 4 : 1;
   const int64_t G0 = gb_blocks(rows);
   const int64_t rpb = cdiv(rows, G0);
   const int64_t G = cdiv(rows, rpb);
