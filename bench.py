@@ -320,6 +320,30 @@ def wl_cross_entropy(vh):
         (L, T, GO, LOSS, DL, SC)
 
 
+def wl_cross_entropy_rowstats(vh):
+    """The same fwd+bwd with the forward keeping each row's (max, sum-exp) and
+    the backward streaming from them (vh_cross_entropy_fwd_rs_ld /
+    vh_cross_entropy_bwd_rs_ld): the same loss and dlogits bits as the slot
+    pair above, for a caller that keeps per-row state between its forward and
+    backward. Bytes: fwd R logits + W stats, bwd R logits + W dlogits + R stats
+    (targets read by both)."""
+    B, V = 16384, 50257
+    r = np.random.default_rng(SEED + 4)
+    L = vh.DeviceBuffer.from_array(r.standard_normal(size=(B, V), dtype=np.float32))
+    T = vh.DeviceBuffer.from_array(r.integers(0, V, size=B).astype(np.float32))
+    GO = vh.DeviceBuffer.from_array(np.float32([1.0]))
+    LOSS, DL, ST = vh.DeviceBuffer(4), vh.DeviceBuffer(4 * B * V), vh.DeviceBuffer(8 * B)
+    nsc = vh.lib.vh_cross_entropy_fwd_scratch_bytes(B)
+    SC = vh.DeviceBuffer(nsc)
+    fb, bb = 4 * B * V + 8 * B + 8 * B, 8 * B * V + 8 * B + 4 * B
+    ops = [("cross_entropy_fwd_rs", fb, lambda i: vh.lib.vh_cross_entropy_fwd_rs_ld(
+               L.ptr, V, T.ptr, LOSS.ptr, ST.ptr, B, V, SC.ptr, nsc, None)),
+           ("cross_entropy_bwd_rs", bb, lambda i: vh.lib.vh_cross_entropy_bwd_rs_ld(
+               L.ptr, V, T.ptr, ST.ptr, GO.ptr, DL.ptr, B, V, None))]
+    return ops, {"workload": "cross-entropy fwd+bwd over logits [16384,50257], the backward from the "
+                             "forward's row statistics"}, None, (L, T, GO, LOSS, DL, ST, SC)
+
+
 def wl_softmax_dense(vh):
     """The softmax the BackendOps slot runs: vearo's attention adds the causal
     mask to the scores (scores.add(mask).softmax(3)), so the slot sees a plain
@@ -581,6 +605,7 @@ def run_checkpoint(args, vh):
 WORKLOADS = {"ln_softmax": wl_ln_softmax, "gpt2_block": wl_gpt2_block, "layernorm_cfg0": wl_layernorm_cfg0,
              "gelu_bias": wl_gelu_bias, "embedding_uniform": wl_embedding_uniform,
              "embedding_zipf": wl_embedding_zipf, "cross_entropy": wl_cross_entropy,
+             "cross_entropy_rowstats": wl_cross_entropy_rowstats,
              "softmax_dense": wl_softmax_dense, "lm_head_gemm": wl_lm_head_gemm, "checkpoint": run_checkpoint}
 
 # The kernels each op launches (name patterns), per workload: the per-dispatch
@@ -595,6 +620,8 @@ PMC_KERNELS = {
     "embedding_uniform": {"embedding_fwd": r"^vh_emb_fwd", "embedding_bwd": r"^vh_emb_(sort|sum)"},
     "embedding_zipf": {"embedding_fwd": r"^vh_emb_fwd", "embedding_bwd": r"^vh_emb_(sort|sum)"},
     "cross_entropy": {"cross_entropy_fwd": r"^vh_xent_fwd|^vh_xent_reduce$", "cross_entropy_bwd": r"^vh_xent_bwd"},
+    "cross_entropy_rowstats": {"cross_entropy_fwd_rs": r"^vh_xent_fwd|^vh_xent_reduce$",
+                               "cross_entropy_bwd_rs": r"^vh_xent_bwd_rs"},
     "softmax_dense": {"softmax_dense_fwd": r"^vh_sm_fwd_", "softmax_dense_bwd": r"^vh_sm_bwd_"},
     "lm_head_gemm": {"lm_head_gemm": r"^vh_gemm"},
     "gpt2_block": {"cross_entropy_fused": r"^vh_xent_fb_|^vh_xent_reduce$"},
@@ -668,12 +695,19 @@ def pmc_summarize(root):
             res[op] = {"symbols": syms, "fetch_kib": round(f, 1), "write_kib": round(w, 1),
                        "traffic_bytes": int(round((f * fscale + w * wscale) * 1024))}
         out["workloads"][wl] = res
+    # Workloads not measured under root keep their earlier records (each was
+    # scaled by the copy calibration of its own run).
+    if os.path.exists(PMC_FILE):
+        with open(PMC_FILE) as f:
+            prev = json.load(f).get("workloads", {})
+        for wl, rec in prev.items():
+            out["workloads"].setdefault(wl, rec)
     with open(PMC_FILE, "w") as f:
         json.dump(out, f, indent=1)
     print(json.dumps({wl: {op: v["traffic_bytes"] for op, v in r.items()} for wl, r in out["workloads"].items()}))
 # Run by default after the headline, each reported under "configs" in the one line.
-EXTRA = ["gpt2_block", "gelu_bias", "embedding_uniform", "embedding_zipf", "cross_entropy", "softmax_dense",
-         "layernorm_cfg0"]
+EXTRA = ["gpt2_block", "gelu_bias", "embedding_uniform", "embedding_zipf", "cross_entropy",
+         "cross_entropy_rowstats", "softmax_dense", "layernorm_cfg0"]
 
 
 def host_info():

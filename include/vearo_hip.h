@@ -227,6 +227,26 @@ int vh_cross_entropy_fwd_ld(const float* logits, int64_t ld, const float* target
 int vh_cross_entropy_bwd_ld(const float* logits, int64_t ld, const float* targets,
                             const float* grad_out, float* dlogits, int64_t B, int64_t V,
                             void* stream);
+/* The forward above that also keeps, per row b, row_stats[2b] = max_c logits[b, c]
+ * and row_stats[2b + 1] = sum_c exp(logits[b, c] - that max) (row_stats: [B, 2]
+ * floats, 8-byte aligned) -- the two values the reference's backward recomputes
+ * from the logits (cpu:1102-1114). Loss as vh_cross_entropy_fwd_ld. Replaces
+ * BackendOps.cross_entropy (tensor.rs:1141; cpu:982-1051) for a caller that keeps
+ * per-row state between its forward and backward (autograd's saved tensors).
+ * scratch: NULL or vh_cross_entropy_fwd_scratch_bytes(B) bytes. */
+int vh_cross_entropy_fwd_rs_ld(const float* logits, int64_t ld, const float* targets,
+                               float* loss, float* row_stats, int64_t B, int64_t V,
+                               void* scratch, size_t scratch_bytes, void* stream);
+/* Backward from those statistics: one streaming pass, no reduction. dlogits has
+ * the same bits as vh_cross_entropy_bwd_ld's when row_stats came from
+ * vh_cross_entropy_fwd_rs_ld on the same logits, V and ld; dlogits may alias
+ * logits. Replaces BackendOps.cross_entropy_backward (tensor.rs:1143;
+ * cpu:1053-1127) for that caller. Grid: B * ceil((V / 4 + 1) / 512) workgroups
+ * when logits and dlogits are 16-byte aligned, else B * ceil(V / 4096); at most
+ * INT32_MAX. */
+int vh_cross_entropy_bwd_rs_ld(const float* logits, int64_t ld, const float* targets,
+                               const float* row_stats, const float* grad_out, float* dlogits,
+                               int64_t B, int64_t V, void* stream);
 /* Forward and backward in one read of the logits, for a caller that knows
  * grad_out before running the forward (the training step: the seed gradient of
  * loss.backward() is 1, autograd:795-798). Same loss and dlogits as

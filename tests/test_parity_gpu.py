@@ -359,6 +359,93 @@ def test_cross_entropy_fwd_bwd(vh, B, V):
     assert_parity(fetch(vh, DL, (B, V)), O.cross_entropy_backward(logits, tg, go), name="dlogits")
 
 
+# (4, 4096) and (3, 8193): whole and ragged 4096-column chunks of the row-statistics backward.
+@pytest.mark.parametrize("B,V", [(512, 50257), (3, 5), (64, 1000), (7, 70000), (1, 1), (1500, 3000),
+                                 (4, 4096), (3, 8193)])
+def test_cross_entropy_row_stats(vh, B, V):
+    """The forward that keeps each row's (max, sum-exp) and the streaming
+    backward from them: the loss bit-equal to vh_cross_entropy_fwd's, the max
+    equal to the row's maximum, dlogits bit-equal to the recomputing backward
+    (row-cached and streaming V alike), with a row stride, in place, with inf
+    and NaN logits, and against the oracle."""
+    print(f"cross_entropy row stats B={B} V={V}", flush=True)
+    r = rng(41)
+    logits = (2.0 * r.normal(size=(B, V))).astype(np.float32)
+    if B >= 3 and V >= 3:
+        logits[1, V // 2] = np.inf
+        logits[2, 1] = np.nan
+    tg = r.integers(0, V, size=B).astype(np.float32)
+    go = np.float32([1.3])
+    L, T, GO = dev(vh, logits), dev(vh, tg), dev(vh, go)
+    LOSS, LOSS2, ST = out(vh, (1,)), out(vh, (1,)), out(vh, (B, 2))
+    DL, DL2 = out(vh, (B, V)), out(vh, (B, V))
+    vh.check(vh.lib.vh_cross_entropy_fwd(L.ptr, T.ptr, LOSS.ptr, B, V, None, 0, None))
+    vh.check(vh.lib.vh_cross_entropy_bwd(L.ptr, T.ptr, GO.ptr, DL.ptr, B, V, None))
+    vh.check(vh.lib.vh_cross_entropy_fwd_rs_ld(L.ptr, V, T.ptr, LOSS2.ptr, ST.ptr, B, V, None, 0, None))
+    vh.check(vh.lib.vh_cross_entropy_bwd_rs_ld(L.ptr, V, T.ptr, ST.ptr, GO.ptr, DL2.ptr, B, V, None))
+    np.testing.assert_array_equal(fetch(vh, LOSS2, (1,)), fetch(vh, LOSS, (1,)))
+    st = fetch(vh, ST, (B, 2))
+    # The reference's max skips NaN (`if l > max`, cpu:1102-1108).
+    np.testing.assert_array_equal(st[:, 0], np.nanmax(logits, axis=1))
+    want = fetch(vh, DL, (B, V))
+    np.testing.assert_array_equal(fetch(vh, DL2, (B, V)), want)
+    fin = np.isfinite(logits).all(axis=1)
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = O.cross_entropy_backward(logits, tg, go)
+    assert_parity(want[fin], ref[fin], name="dlogits")
+    if fin.all():
+        assert_parity(fetch(vh, LOSS2, (1,)), O.cross_entropy(logits, tg), name="loss")
+    # Row stride ld > V (both buffers), then in place over the logits.
+    ld = V + 7
+    wide = np.full((B, ld), 5.0, np.float32)
+    wide[:, :V] = logits
+    LW, DW = dev(vh, wide), dev(vh, np.full((B, ld), -3.0, np.float32))
+    vh.check(vh.lib.vh_cross_entropy_fwd_rs_ld(LW.ptr, ld, T.ptr, LOSS2.ptr, ST.ptr, B, V, None, 0, None))
+    vh.check(vh.lib.vh_cross_entropy_bwd_rs_ld(LW.ptr, ld, T.ptr, ST.ptr, GO.ptr, DW.ptr, B, V, None))
+    dw = fetch(vh, DW, (B, ld))
+    np.testing.assert_array_equal(dw[:, :V], want)
+    assert np.all(dw[:, V:] == -3.0)
+    vh.check(vh.lib.vh_cross_entropy_bwd_rs_ld(LW.ptr, ld, T.ptr, ST.ptr, GO.ptr, LW.ptr, B, V, None))
+    lw = fetch(vh, LW, (B, ld))
+    np.testing.assert_array_equal(lw[:, :V], want)
+    assert np.all(lw[:, V:] == 5.0)
+    # Buffers 4 bytes past a 16-byte boundary: the 32-bit kernel.
+    LO = dev(vh, np.concatenate([np.float32([7.0]), logits.ravel()]))
+    DO = dev(vh, np.full(B * V + 1, -3.0, np.float32))
+    vh.check(vh.lib.vh_cross_entropy_fwd_rs_ld(LO.ptr + 4, V, T.ptr, LOSS2.ptr, ST.ptr, B, V, None, 0, None))
+    vh.check(vh.lib.vh_cross_entropy_bwd_rs_ld(LO.ptr + 4, V, T.ptr, ST.ptr, GO.ptr, DO.ptr + 4, B, V, None))
+    do = fetch(vh, DO, (B * V + 1,))
+    np.testing.assert_array_equal(do[1:].reshape(B, V), want)
+    assert do[0] == -3.0
+
+
+def test_cross_entropy_row_stats_errors(vh):
+    """Argument errors and the invalid-target panic through the row-statistics
+    entries, with the reference's messages."""
+    L = dev(vh, np.zeros((2, 3), np.float32))
+    LOSS, ST, GO, DL = out(vh, (1,)), out(vh, (2, 2)), dev(vh, np.float32([1.0])), out(vh, (2, 3))
+    for tv, msg in [(-1.0, "Target class cannot be negative: -1"),
+                    (3.0, "Target class 3 out of vocab bounds 3")]:
+        T = dev(vh, np.float32([0.0, tv]))
+        vh.check(vh.lib.vh_cross_entropy_fwd_rs_ld(L.ptr, 3, T.ptr, LOSS.ptr, ST.ptr, 2, 3, None, 0, None))
+        with pytest.raises(vh.DevicePanic) as ei:
+            vh.sync()
+        assert ei.value.msg == msg
+        vh.check(vh.lib.vh_cross_entropy_bwd_rs_ld(L.ptr, 3, T.ptr, ST.ptr, GO.ptr, DL.ptr, 2, 3, None))
+        with pytest.raises(vh.DevicePanic) as ei:
+            vh.sync()
+        assert ei.value.msg == msg
+    T = dev(vh, np.float32([0.0, 1.0]))
+    rc = vh.lib.vh_cross_entropy_bwd_rs_ld(L.ptr, 3, T.ptr, ST.ptr, GO.ptr, DL.ptr, 0, 3, None)
+    assert rc == vh.VH_ERR_INVALID and vh.last_error() == "Batch size must be greater than 0"
+    rc = vh.lib.vh_cross_entropy_bwd_rs_ld(L.ptr, 2, T.ptr, ST.ptr, GO.ptr, DL.ptr, 2, 3, None)
+    assert rc == vh.VH_ERR_INVALID and "row stride below V" in vh.last_error()
+    rc = vh.lib.vh_cross_entropy_bwd_rs_ld(L.ptr, 3, T.ptr, ST.ptr + 4, GO.ptr, DL.ptr, 2, 3, None)
+    assert rc == vh.VH_ERR_INVALID and "8-byte aligned" in vh.last_error()
+    rc = vh.lib.vh_cross_entropy_fwd_rs_ld(L.ptr, 3, T.ptr, LOSS.ptr, None, 2, 3, None, 0, None)
+    assert rc == vh.VH_ERR_INVALID and "null pointer" in vh.last_error()
+
+
 def test_cross_entropy_kats_and_panics(vh):
     L, T = dev(vh, np.float32([[1000.0, -1000.0]])), dev(vh, np.float32([0.0]))
     LOSS = out(vh, (1,))

@@ -67,6 +67,12 @@ def test_cross_entropy_cfg4_full(vh):
     assert abs(loss - exact) <= 1e-5 + 1e-4 * abs(exact), (loss, exact)
     assert_parity(np.float32([loss]), O.cross_entropy(logits, tg), name="loss")
     dl = fetch(vh, DL, (B, V))
+    # The row-statistics pair on the same logits: the same loss and dlogits bits.
+    ST, LOSS2 = out(vh, (B, 2)), out(vh, (1,))
+    vh.check(vh.lib.vh_cross_entropy_fwd_rs_ld(L.ptr, V, T.ptr, LOSS2.ptr, ST.ptr, B, V, None, 0, None))
+    vh.check(vh.lib.vh_cross_entropy_bwd_rs_ld(L.ptr, V, T.ptr, ST.ptr, GO.ptr, DL.ptr, B, V, None))
+    assert fetch(vh, LOSS2, (1,))[0] == loss
+    assert np.array_equal(fetch(vh, DL, (B, V)), dl)
     del DL, L
     np.testing.assert_allclose(dl.sum(axis=1, dtype=np.float64), 0.0, atol=1e-9)
     ti = tg.astype(np.int64)

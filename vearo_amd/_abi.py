@@ -132,6 +132,11 @@ SIGNATURES = {
         [fp, c_int64, fp, fp, c_int64, c_int64, c_void_p, c_size_t, c_void_p],
     ),
     "vh_cross_entropy_bwd_ld": (c_int, [fp, c_int64, fp, fp, fp, c_int64, c_int64, c_void_p]),
+    "vh_cross_entropy_fwd_rs_ld": (
+        c_int,
+        [fp, c_int64, fp, fp, fp, c_int64, c_int64, c_void_p, c_size_t, c_void_p],
+    ),
+    "vh_cross_entropy_bwd_rs_ld": (c_int, [fp, c_int64, fp, fp, fp, fp, c_int64, c_int64, c_void_p]),
     "vh_cross_entropy_fwd_bwd_ld": (
         c_int,
         [fp, c_int64, fp, fp, fp, fp, c_int64, c_int64, c_void_p, c_size_t, c_void_p],

@@ -193,6 +193,8 @@ XE_CFG(K_XE)
 extern "C" __global__ void __launch_bounds__(1024) vh_xent_fwd_stream(XentArgs a) { xent_stream_impl<false>(a); }
 extern "C" __global__ void __launch_bounds__(1024) vh_xent_bwd_stream(XentArgs a) { xent_stream_impl<true>(a); }
 extern "C" __global__ void __launch_bounds__(1024) vh_xent_reduce(XentReduceArgs a) { xent_reduce_impl(a); }
+extern "C" __global__ void __launch_bounds__(XR4_THREADS) vh_xent_bwd_rs4(XentArgs a) { xent_bwd_rs4_impl(a); }
+extern "C" __global__ void __launch_bounds__(XR_THREADS) vh_xent_bwd_rs(XentArgs a) { xent_bwd_rs_impl(a); }
 
 // Generic building blocks
 extern "C" __global__ void __launch_bounds__(256) vh_binary_contig_v1(BinaryArgs a) { binary_contig_impl<1>(a); }

@@ -19,7 +19,9 @@
 // order, so the loss is deterministic. MODE 2 does forward and backward in one
 // read of the row (for a caller that knows grad_out before the forward, as the
 // training step does: the seed gradient of backward() is 1): the same row
-// loss and the same dlogits as MODE 0 and MODE 1.
+// loss and the same dlogits as MODE 0 and MODE 1. The forwards can also write
+// each row's (max, sum-exp); xent_bwd_rs*_impl is then the backward as a flat
+// stream from them, with MODE 1's bits.
 #pragma once
 #include "common.h"
 
@@ -92,7 +94,10 @@ VH_DEV void xent_cached_impl(const XentArgs& a) {
   }
   s = team_sum<XE_TEAM>(s, red);
   if constexpr (MODE == 0) {
-    if (threadIdx.x == 0) a.out[row] = t >= 0 ? lr[t] - m - logf(s) : 0.0f;
+    if (threadIdx.x == 0) {
+      a.out[row] = t >= 0 ? lr[t] - m - logf(s) : 0.0f;
+      if (a.stats) *reinterpret_cast<float2*>(a.stats + 2 * row) = make_float2(m, s);
+    }
   }
   if constexpr (MODE != 0) {
     __builtin_amdgcn_sched_barrier(0);
@@ -139,7 +144,10 @@ VH_DEV void xent_stream_impl(const XentArgs& a) {
   s = team_sum<1024>(s, red);
   const int32_t t = xent_target(a, row);
   if constexpr (!BWD) {
-    if (threadIdx.x == 0) a.out[row] = t >= 0 ? lr[t] - M - logf(s) : 0.0f;
+    if (threadIdx.x == 0) {
+      a.out[row] = t >= 0 ? lr[t] - M - logf(s) : 0.0f;
+      if (a.stats) *reinterpret_cast<float2*>(a.stats + 2 * row) = make_float2(M, s);
+    }
   } else {
     const float gs = *a.grad_out / (float)a.B;
     float* o = a.out + row * a.ld;
@@ -148,6 +156,95 @@ VH_DEV void xent_stream_impl(const XentArgs& a) {
       const float ind = c == t ? 1.0f : 0.0f;
       o[c] = (p - ind) * gs;
     }
+  }
+}
+
+// Backward from the forward's row statistics (stats[2 r] = the row max m,
+// stats[2 r + 1] = the row's sum of exp(l - m), as the forward kernel of the
+// same V computed them): dl = (expf(l - m) / s - 1[c == t]) * (go / B), the
+// operations the backward kernels above apply after their reductions, so the
+// same bits. Nothing is left to reduce, so the row need not be held in
+// registers: a flat stream of short-lived workgroups, one per (row, chunk).
+VH_DEV float xent_rs_grad(float x, int i, int32_t t, float2 st, float c) {
+  const float p = expf(x - st.x) / st.y;
+  const float ind = i == t ? 1.0f : 0.0f;
+  return (p - ind) * c;
+}
+
+// 16-byte form (logits and dlogits 16-byte aligned): per row, the head
+// elements before the first 16-byte boundary and the 0-3 tail elements are
+// done by threads 0-7 of chunk 0; the rest as 16-byte units, XR4_PER per
+// thread, streaming (non-temporal) loads and stores. At [16384, 50257]
+// (MI355X): 256 threads x 2 units 1131 us; 4 units 1178, 8 units 1247, 1 unit
+// 1358; 512 threads x 2 units 1164; cached-hint loads and stores 1159 us.
+#define XR4_THREADS 256
+#define XR4_PER 2
+#define XR4_CHUNK (XR4_THREADS * XR4_PER)  // 16-byte units per workgroup
+VH_DEV void xent_bwd_rs4_impl(const XentArgs& a) {
+  const int V = a.V;
+  const uint32_t nch = (uint32_t)((V / 4 + 1 + XR4_CHUNK - 1) / XR4_CHUNK);
+  const uint32_t row32 = blockIdx.x / nch;
+  const int u0 = (int)(blockIdx.x - row32 * nch) * XR4_CHUNK;
+  const int64_t row = row32;
+  const float2 st = *reinterpret_cast<const float2*>(a.stats + 2 * row);
+  const int32_t t = xent_target(a, row);
+  const float c = *a.grad_out / (float)a.B;
+  const int64_t base = row * a.ld;
+  const int hv = min((int)((4 - (base & 3)) & 3), V);  // head elements
+  const int nvec = (V - hv) / 4;
+  const float* lr = a.logits + base;
+  float* o = a.out + base;
+  const int tid = threadIdx.x;
+  if (u0 == 0 && tid < 8) {
+    const int i = tid < 4 ? tid : hv + 4 * nvec + (tid - 4);
+    if (tid < 4 ? tid < hv : i < V) o[i] = xent_rs_grad(lr[i], i, t, st, c);
+  }
+  const float* l4 = lr + hv;
+  float* o4 = o + hv;
+  Unit<4> x[XR4_PER];
+#pragma unroll
+  for (int k = 0; k < XR4_PER; ++k) {
+    const int u = u0 + k * XR4_THREADS + tid;
+    x[k] = u < nvec ? load_stream<4>(l4 + 4 * u) : zero_unit<4>();
+  }
+#pragma unroll
+  for (int k = 0; k < XR4_PER; ++k) {
+    const int u = u0 + k * XR4_THREADS + tid;
+    if (u < nvec) {
+      Unit<4> r;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r.v[j] = xent_rs_grad(x[k].v[j], hv + 4 * u + j, t, st, c);
+      store_stream<4>(o4 + 4 * u, r);
+    }
+  }
+}
+
+// Any alignment: 32-bit elements, XR_PER per thread, lane-contiguous.
+#define XR_THREADS 256
+#define XR_PER 16
+#define XR_CHUNK (XR_THREADS * XR_PER)  // elements per workgroup
+VH_DEV void xent_bwd_rs_impl(const XentArgs& a) {
+  const int V = a.V;
+  const uint32_t nch = (uint32_t)((V + XR_CHUNK - 1) / XR_CHUNK);
+  const uint32_t row32 = blockIdx.x / nch;
+  const int c0 = (int)(blockIdx.x - row32 * nch) * XR_CHUNK;
+  const int64_t row = row32;
+  const float2 st = *reinterpret_cast<const float2*>(a.stats + 2 * row);
+  const int32_t t = xent_target(a, row);
+  const float c = *a.grad_out / (float)a.B;
+  const float* lr = a.logits + row * a.ld;
+  float* o = a.out + row * a.ld;
+  const int n = V - c0;
+  float x[XR_PER];
+#pragma unroll
+  for (int k = 0; k < XR_PER; ++k) {
+    const int i = k * XR_THREADS + (int)threadIdx.x;
+    x[k] = i < n ? lr[c0 + i] : 0.0f;
+  }
+#pragma unroll
+  for (int k = 0; k < XR_PER; ++k) {
+    const int i = k * XR_THREADS + (int)threadIdx.x;
+    if (i < n) o[c0 + i] = xent_rs_grad(x[k], c0 + i, t, st, c);
   }
 }
 

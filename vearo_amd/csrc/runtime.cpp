@@ -1061,7 +1061,7 @@ int vh_cross_entropy_fwd_ld(const float* logits, int64_t ld, const float* target
   hipStream_t s = S(stream);
   Scratch sc;
   VH_TRY(sc.get(S(stream), scratch, scratch_bytes, vh_cross_entropy_fwd_scratch_bytes(B)));
-  XentArgs a{logits, targets, nullptr, static_cast<float*>(sc.p), nullptr, g_rt.err, B, ld, (int32_t)V};
+  XentArgs a{logits, targets, nullptr, static_cast<float*>(sc.p), nullptr, g_rt.err, B, ld, (int32_t)V, nullptr};
   VH_TRY(launch(xent_kernel("fwd", V), B, 1, xent_threads(xent_kernel("fwd", V)), 0, s, a));
   XentReduceArgs r{static_cast<float*>(sc.p), loss, B};
   return launch("vh_xent_reduce", 1, 1, 1024, 0, s, r);
@@ -1070,6 +1070,27 @@ int vh_cross_entropy_fwd_ld(const float* logits, int64_t ld, const float* target
 int vh_cross_entropy_fwd(const float* logits, const float* targets, float* loss, int64_t B,
                          int64_t V, void* scratch, size_t scratch_bytes, void* stream) {
   return vh_cross_entropy_fwd_ld(logits, V, targets, loss, B, V, scratch, scratch_bytes, stream);
+}
+
+int vh_cross_entropy_fwd_rs_ld(const float* logits, int64_t ld, const float* targets, float* loss,
+                               float* row_stats, int64_t B, int64_t V, void* scratch, size_t scratch_bytes,
+                               void* stream) {
+  VH_TRY(require_init());
+  if (B <= 0) return fail(VH_ERR_INVALID, "Batch size must be greater than 0");
+  if (V <= 0) return fail(VH_ERR_INVALID, "vh_cross_entropy_fwd_rs: vocabulary must be > 0");
+  if (ld < V) return fail(VH_ERR_INVALID, "vh_cross_entropy_fwd_rs: row stride below V");
+  if (!logits || !targets || !loss || !row_stats)
+    return fail(VH_ERR_INVALID, "vh_cross_entropy_fwd_rs: null pointer");
+  if (reinterpret_cast<uintptr_t>(row_stats) % 8 != 0)
+    return fail(VH_ERR_INVALID, "vh_cross_entropy_fwd_rs: row_stats must be 8-byte aligned");
+  if (V > INT32_MAX || B > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_cross_entropy_fwd_rs: size exceeds int32");
+  hipStream_t s = S(stream);
+  Scratch sc;
+  VH_TRY(sc.get(S(stream), scratch, scratch_bytes, vh_cross_entropy_fwd_scratch_bytes(B)));
+  XentArgs a{logits, targets, nullptr, static_cast<float*>(sc.p), nullptr, g_rt.err, B, ld, (int32_t)V, row_stats};
+  VH_TRY(launch(xent_kernel("fwd", V), B, 1, xent_threads(xent_kernel("fwd", V)), 0, s, a));
+  XentReduceArgs r{static_cast<float*>(sc.p), loss, B};
+  return launch("vh_xent_reduce", 1, 1, 1024, 0, s, r);
 }
 
 int vh_cross_entropy_bwd_ld(const float* logits, int64_t ld, const float* targets, const float* grad_out,
@@ -1081,8 +1102,32 @@ int vh_cross_entropy_bwd_ld(const float* logits, int64_t ld, const float* target
   if (!logits || !targets || !grad_out || !dlogits)
     return fail(VH_ERR_INVALID, "vh_cross_entropy_bwd: null pointer");
   if (V > INT32_MAX || B > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_cross_entropy_bwd: size exceeds int32");
-  XentArgs a{logits, targets, grad_out, dlogits, nullptr, g_rt.err, B, ld, (int32_t)V};
+  XentArgs a{logits, targets, grad_out, dlogits, nullptr, g_rt.err, B, ld, (int32_t)V, nullptr};
   return launch(xent_kernel("bwd", V), B, 1, xent_threads(xent_kernel("bwd", V)), 0, S(stream), a);
+}
+
+// Chunks of the row-statistics backward: 256 threads x 2 16-byte units
+// (XR4_CHUNK) when logits and dlogits are 16-byte aligned, else 256 threads x
+// 16 elements (XR_CHUNK).
+constexpr int64_t kXr4Chunk = 512;
+constexpr int64_t kXrChunk = 4096;
+
+int vh_cross_entropy_bwd_rs_ld(const float* logits, int64_t ld, const float* targets, const float* row_stats,
+                               const float* grad_out, float* dlogits, int64_t B, int64_t V, void* stream) {
+  VH_TRY(require_init());
+  if (B <= 0) return fail(VH_ERR_INVALID, "Batch size must be greater than 0");
+  if (V <= 0) return fail(VH_ERR_INVALID, "vh_cross_entropy_bwd_rs: vocabulary must be > 0");
+  if (ld < V) return fail(VH_ERR_INVALID, "vh_cross_entropy_bwd_rs: row stride below V");
+  if (!logits || !targets || !row_stats || !grad_out || !dlogits)
+    return fail(VH_ERR_INVALID, "vh_cross_entropy_bwd_rs: null pointer");
+  if (reinterpret_cast<uintptr_t>(row_stats) % 8 != 0)
+    return fail(VH_ERR_INVALID, "vh_cross_entropy_bwd_rs: row_stats must be 8-byte aligned");
+  if (V > INT32_MAX || B > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_cross_entropy_bwd_rs: size exceeds int32");
+  XentArgs a{logits, targets, grad_out, dlogits, nullptr, g_rt.err, B, ld, (int32_t)V, const_cast<float*>(row_stats)};
+  const bool v4 = (reinterpret_cast<uintptr_t>(logits) | reinterpret_cast<uintptr_t>(dlogits)) % 16 == 0;
+  const int64_t grid = B * (v4 ? cdiv(V / 4 + 1, kXr4Chunk) : cdiv(V, kXrChunk));
+  if (grid > INT32_MAX) return fail(VH_ERR_UNSUPPORTED, "vh_cross_entropy_bwd_rs: grid exceeds int32");
+  return launch(v4 ? "vh_xent_bwd_rs4" : "vh_xent_bwd_rs", grid, 1, 256, 0, S(stream), a);
 }
 
 int vh_cross_entropy_fwd_bwd_ld(const float* logits, int64_t ld, const float* targets, const float* grad_out,
@@ -1105,7 +1150,7 @@ int vh_cross_entropy_fwd_bwd_ld(const float* logits, int64_t ld, const float* ta
   Scratch sc;
   VH_TRY(sc.get(S(stream), scratch, scratch_bytes, vh_cross_entropy_fwd_scratch_bytes(B)));
   float* rows = static_cast<float*>(sc.p);
-  XentArgs a{logits, targets, grad_out, dlogits, rows, g_rt.err, B, ld, (int32_t)V};
+  XentArgs a{logits, targets, grad_out, dlogits, rows, g_rt.err, B, ld, (int32_t)V, nullptr};
   VH_TRY(launch(xent_kernel("fb", V), B, 1, xent_threads(xent_kernel("fb", V)), 0, s, a));
   XentReduceArgs r{rows, loss, B};
   return launch("vh_xent_reduce", 1, 1, 1024, 0, s, r);

@@ -322,6 +322,7 @@ struct XentArgs {
   int64_t B;
   int64_t ld;             // row stride of logits and dlogits (>= V)
   int32_t V;
+  float* stats;           // fwd: NULL or per-row (max, sum-exp) out [B, 2]; bwd_rs: in
 };
 
 struct XentReduceArgs {
