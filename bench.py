@@ -11,8 +11,10 @@ issued in that order on the runtime stream, as a training step meets them
 other configs of BASELINE.json the same way and reports them in the same JSON
 line under "configs" (gpt2_block -- config[4]'s training step, whose ms per
 step is also the top-level "gpt2_block_ms" -- gelu_bias, embedding_uniform,
-embedding_zipf, cross_entropy, softmax_dense -- the dense form the BackendOps
-slot runs -- and layernorm_cfg0); --no-extra skips them, --workload NAME
+embedding_zipf, cross_entropy, cross_entropy_rowstats -- the same with the
+backward streaming from the forward's row statistics -- softmax_dense -- the
+dense form the BackendOps slot runs -- and layernorm_cfg0); --no-extra skips
+them, --workload NAME
 prints one config's own line. gpt2_block also carries "ab_library" (its dense
 products on hipBLASLt), "dropin" (the same step op by op through the
 BackendOps mirror, shared-weight gradients folded into one product),
